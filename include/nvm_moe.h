@@ -1,0 +1,141 @@
+/*
+ * nvm_moe.h — C ABI of the MI355X (gfx950) Qwen3 sparse-MoE block.
+ *
+ * This shared library replaces, for the MoE hot path of nano-vllm-metal, the
+ * reference's native op binding and the MLX built-ins that `layers/moe.py`
+ * calls.  Paths below are relative to the reference's `src/nano_vllm_metal`.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are HIP device pointers; sizes are element counts (int64_t).
+ *   - Activation tensors ("act") are fp16 or bf16, selected by `dtype`
+ *     (NVM_DTYPE_F16 / NVM_DTYPE_BF16); scales and biases share that dtype
+ *     (the reference checks the same, metal/src/quantized_matmul.cpp:26-37).
+ *   - Quantised weights use the MLX affine layout: `bits` = 4, uint32 words
+ *     packing 8 codes each, code j of a word in bits [4j, 4j+4); per-group
+ *     scale and bias with `group_size` in {64, 128}; w = q*scale + bias.
+ *     Expert tensors are [E, out, in/8] words and [E, out, in/group] scales.
+ *   - All tensors are dense row-major (the reference requires row-contiguous
+ *     inputs, quantized_matmul.cpp:96-101).
+ *   - Work is enqueued on `stream` (a hipStream_t); nothing synchronises the
+ *     host.  The library allocates no device memory: callers pass outputs and,
+ *     where stated, a workspace sized by the matching *_workspace_size call.
+ *   - Return value: NVM_OK (0) or a negative NVM_ERR_* code; the message is
+ *     available from nvm_last_error() on the calling thread.  No C++
+ *     exception crosses this boundary.
+ *   - Calls on one stream are ordered; calls sharing a workspace must not
+ *     overlap in time.
+ */
+#ifndef NVM_MOE_H
+#define NVM_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NVM_ABI_VERSION 1
+
+enum nvm_dtype { NVM_DTYPE_F16 = 0, NVM_DTYPE_BF16 = 1 };
+
+enum nvm_status {
+  NVM_OK = 0,
+  NVM_ERR_INVALID = -1,     /* bad argument: shape, dtype, null pointer  */
+  NVM_ERR_UNSUPPORTED = -2, /* valid request this build does not handle  */
+  NVM_ERR_WORKSPACE = -3,   /* workspace missing or too small            */
+  NVM_ERR_HIP = -4          /* a HIP runtime call failed                 */
+};
+
+/* Expert-product regime: the decode MFMA-GEMV or the prefill LDS/MFMA GEMM.
+ * NVM_REGIME_AUTO picks by routed pairs per expert. */
+enum nvm_regime { NVM_REGIME_AUTO = 0, NVM_REGIME_DECODE = 1, NVM_REGIME_PREFILL = 2 };
+
+typedef void *nvm_stream_t; /* hipStream_t */
+
+int nvm_abi_version(void);
+const char *nvm_last_error(void);
+
+/*
+ * Dense W4A16 matmul: out[M,K] = a[M,N] . dequant(b[K,N/8])^T.
+ * Replaces `_ext.quantized_matmul(scales, biases, group_size, bits, a, b,
+ * transpose_b)` (metal/bindings.cpp:16-32; op metal/src/quantized_matmul.cpp:17-82,
+ * CPU loop :84-148), which `quantized_linear` uses for the router logits
+ * (layers/linear.py:92-126, layers/moe.py:43).  Like the reference, only
+ * transpose_b = 1 and bits = 4 are accepted; group_size may be 64 or 128.
+ * The dot products accumulate in float64 and are rounded once to act.
+ * Needs no workspace.
+ */
+int nvm_quantized_matmul(const void *scales, const void *biases, int group_size, int bits,
+                         const void *a, const uint32_t *b, int transpose_b, void *out,
+                         int64_t M, int64_t N, int64_t K, int dtype, nvm_stream_t stream);
+
+/*
+ * Router: logits = x . dequant(Wr)^T rounded to act, probs = act-rounded
+ * softmax (float64 inside), ids = top-k with ties to the lower expert index
+ * in (prob desc, index asc) slot order, scores = probs[ids], renormalised to
+ * rnd(s / rnd(sum s)) when norm_topk_prob != 0.
+ * Replaces `route_topk` (layers/moe.py:37-49).
+ *   x [T,H] act; wr [E,H/8]; sr, br [E,H/group] act
+ *   probs [T,E] act (may be NULL); ids [T,k] int32; scores [T,k] act
+ * Workspace: nvm_route_workspace_size.
+ */
+int nvm_route_workspace_size(int64_t T, int64_t H, int64_t E, size_t *bytes);
+int nvm_moe_route(const void *x, int64_t T, int64_t H, const uint32_t *wr, const void *sr,
+                  const void *br, int64_t E, int group_size, int bits, int top_k,
+                  int norm_topk_prob, int dtype, void *probs, int32_t *ids, void *scores,
+                  void *workspace, size_t workspace_bytes, nvm_stream_t stream);
+
+/*
+ * Dispatch: counting sort of the flat expert ids (n = pairs, usually T*k)
+ * into expert order, stable in pair index.  Replaces the `argsort` pair of
+ * `grouped_expert_linear` (layers/moe.py:16-17).
+ *   ids [n] int32 in [0,E); expert_offsets [E+1] int32 (exclusive prefix of
+ *   the histogram); sorted_pairs [n] int32 (pair indices, expert-major).
+ * Out-of-range ids make the call fail only if detected on the host (E is
+ * validated); the kernel clamps nothing, so ids must be in range.
+ * Needs no workspace.
+ */
+int nvm_moe_dispatch(const int32_t *ids, int64_t n, int64_t E, int32_t *expert_offsets,
+                     int32_t *sorted_pairs, nvm_stream_t stream);
+
+/*
+ * Grouped expert linear: out[r] = x[r] . dequant(W[ids[r]])^T rounded to act,
+ * for every row r of x [n, D].  Replaces `grouped_expert_linear`
+ * (layers/moe.py:8-34, whose product runs in MLX `gather_qmm`).
+ *   w [E,O,D/8]; s, b [E,O,D/group]; ids [n] int32; out [n,O] act
+ * Workspace: nvm_grouped_linear_workspace_size.
+ */
+int nvm_grouped_linear_workspace_size(int64_t n, int64_t D, int64_t O, int64_t E, size_t *bytes);
+int nvm_grouped_expert_linear(const void *x, int64_t n, int64_t D, const uint32_t *w,
+                              const void *s, const void *b, int64_t E, int64_t O,
+                              int group_size, int bits, const int32_t *ids, int dtype,
+                              void *out, int regime, void *workspace, size_t workspace_bytes,
+                              nvm_stream_t stream);
+
+/*
+ * The whole sparse-MoE block: route -> dispatch -> gate/up products with
+ * fused SwiGLU -> down product -> weighted combine.  Replaces `Moe.__call__`
+ * (layers/moe.py:69-86).
+ *   x [T,H] act -> y [T,H] act
+ *   wr/sr/br router [E,H/8], [E,H/group]
+ *   wg/sg/bg, wu/su/bu gate and up [E,I,H/8], [E,I,H/group]
+ *   wd/sd/bd down [E,H,I/8], [E,H,I/group]
+ *   ids_out [T,k] int32 and scores_out [T,k] act are optional (NULL).
+ * Workspace: nvm_moe_workspace_size.
+ */
+int nvm_moe_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, size_t *bytes);
+int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int top_k,
+                    int norm_topk_prob, int group_size, int bits, int dtype,
+                    const uint32_t *wr, const void *sr, const void *br,
+                    const uint32_t *wg, const void *sg, const void *bg,
+                    const uint32_t *wu, const void *su, const void *bu,
+                    const uint32_t *wd, const void *sd, const void *bd,
+                    void *y, int32_t *ids_out, void *scores_out, int regime,
+                    void *workspace, size_t workspace_bytes, nvm_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NVM_MOE_H */

@@ -1,0 +1,327 @@
+// C ABI entry points (declared in include/nvm_moe.h): argument validation,
+// workspace layout and the launch sequence of the MoE block.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "internal.h"
+#include "nvm_moe.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define NVM_TRY_HIP(expr)                                                              \
+  do {                                                                                 \
+    const hipError_t e_ = (expr);                                                      \
+    if (e_ != hipSuccess) return fail(NVM_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+
+#define NVM_REQUIRE(cond, ...)                                  \
+  do {                                                          \
+    if (!(cond)) return fail(NVM_ERR_INVALID, __VA_ARGS__);     \
+  } while (0)
+
+#define NVM_SUPPORTED(cond, ...)                                \
+  do {                                                          \
+    if (!(cond)) return fail(NVM_ERR_UNSUPPORTED, __VA_ARGS__); \
+  } while (0)
+
+constexpr int64_t kMaxExperts = 512;
+constexpr int kMaxTopK = 64;
+
+// Bump allocator over the caller's workspace (256-byte aligned slices).
+struct Carve {
+  size_t off = 0;
+  char *base;
+  explicit Carve(void *b) : base((char *)b) {}
+  template <class T>
+  T *take(size_t count) {
+    off = (off + 255) & ~(size_t)255;
+    T *p = base ? (T *)(base + off) : nullptr;
+    off += count * sizeof(T);
+    return p;
+  }
+};
+
+int check_quant(int group_size, int bits, int dtype) {
+  NVM_SUPPORTED(bits == 4, "bits must be 4 (got %d)", bits);
+  NVM_SUPPORTED(group_size == 64 || group_size == 128, "group_size must be 64 or 128 (got %d)",
+                group_size);
+  NVM_REQUIRE(dtype == NVM_DTYPE_F16 || dtype == NVM_DTYPE_BF16, "dtype must be f16 or bf16");
+  return NVM_OK;
+}
+
+bool use_decode(int regime, int64_t pairs, int64_t E) {
+  if (regime == NVM_REGIME_DECODE) return true;
+  if (regime == NVM_REGIME_PREFILL) return false;
+  return pairs <= 16 * E;  // up to 16 routed rows per expert on average
+}
+
+// Workspace of the whole block; with base == nullptr only the size is computed.
+struct MoeWs {
+  double *partial;
+  int32_t *ids;
+  uint16_t *scores;
+  int32_t *offsets, *tile_offsets, *sorted;
+  uint16_t *h, *down;
+  size_t bytes;
+};
+
+MoeWs carve_moe(void *base, int64_t T, int64_t H, int64_t I, int64_t E, int k) {
+  Carve c(base);
+  MoeWs w;
+  const int64_t N = T * k;
+  w.partial = c.take<double>((size_t)nvm::route_splits(T, H) * T * E);
+  w.ids = c.take<int32_t>(N);
+  w.scores = c.take<uint16_t>(N);
+  w.offsets = c.take<int32_t>(E + 1);
+  w.tile_offsets = c.take<int32_t>(E + 1);
+  w.sorted = c.take<int32_t>(N);
+  w.h = c.take<uint16_t>((size_t)N * I);
+  w.down = c.take<uint16_t>((size_t)N * H);
+  w.bytes = (c.off + 255) & ~(size_t)255;
+  return w;
+}
+
+int run_products(int dtype, bool decode, bool dual, nvm::GroupedArgs &g, int64_t pairs,
+                 hipStream_t st) {
+  if (decode) {
+    NVM_TRY_HIP(nvm::launch_gemv(dtype, dual, g, st));
+  } else {
+    const int64_t max_tiles = pairs / nvm::kGemmBM + g.E;
+    NVM_TRY_HIP(nvm::launch_gemm(dtype, dual, g, max_tiles, st));
+  }
+  return NVM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nvm_abi_version(void) { return NVM_ABI_VERSION; }
+
+const char *nvm_last_error(void) { return g_err.c_str(); }
+
+int nvm_quantized_matmul(const void *scales, const void *biases, int group_size, int bits,
+                         const void *a, const uint32_t *b, int transpose_b, void *out, int64_t M,
+                         int64_t N, int64_t K, int dtype, nvm_stream_t stream) {
+  if (int r = check_quant(group_size, bits, dtype)) return r;
+  NVM_SUPPORTED(transpose_b == 1, "quantized_matmul: b must be transposed");
+  NVM_REQUIRE(scales && biases && a && b && out, "quantized_matmul: null pointer");
+  NVM_REQUIRE(M >= 0 && N > 0 && K > 0, "quantized_matmul: bad shape M=%lld N=%lld K=%lld",
+              (long long)M, (long long)N, (long long)K);
+  NVM_REQUIRE(N % group_size == 0, "quantized_matmul: N=%lld not divisible by group_size %d",
+              (long long)N, group_size);
+  if (M == 0) return NVM_OK;
+  NVM_TRY_HIP(nvm::launch_route_partial(dtype, a, M, N, b, scales, biases, K, group_size, 1,
+                                        nullptr, out, (hipStream_t)stream));
+  return NVM_OK;
+}
+
+int nvm_route_workspace_size(int64_t T, int64_t H, int64_t E, size_t *bytes) {
+  NVM_REQUIRE(bytes, "route_workspace_size: null output");
+  NVM_REQUIRE(T >= 0 && H > 0 && E > 0, "route_workspace_size: bad shape");
+  *bytes = sizeof(double) * (size_t)nvm::route_splits(T, H) * (size_t)T * (size_t)E;
+  return NVM_OK;
+}
+
+int nvm_moe_route(const void *x, int64_t T, int64_t H, const uint32_t *wr, const void *sr,
+                  const void *br, int64_t E, int group_size, int bits, int top_k,
+                  int norm_topk_prob, int dtype, void *probs, int32_t *ids, void *scores,
+                  void *workspace, size_t workspace_bytes, nvm_stream_t stream) {
+  if (int r = check_quant(group_size, bits, dtype)) return r;
+  NVM_REQUIRE(x && wr && sr && br && ids && scores, "route: null pointer");
+  NVM_REQUIRE(T >= 0 && H > 0 && E > 0, "route: bad shape");
+  NVM_REQUIRE(H % group_size == 0, "route: H=%lld not divisible by group_size %d",
+              (long long)H, group_size);
+  NVM_SUPPORTED(E <= kMaxExperts, "route: at most %lld experts", (long long)kMaxExperts);
+  NVM_REQUIRE(top_k >= 1 && top_k <= E, "route: top_k=%d outside [1, E=%lld]", top_k,
+              (long long)E);
+  NVM_SUPPORTED(top_k <= kMaxTopK, "route: top_k at most %d", kMaxTopK);
+  if (T == 0) return NVM_OK;
+  size_t need = 0;
+  nvm_route_workspace_size(T, H, E, &need);
+  if (!workspace || workspace_bytes < need)
+    return fail(NVM_ERR_WORKSPACE, "route: workspace of %zu bytes needed", need);
+  const int splits = nvm::route_splits(T, H);
+  hipStream_t st = (hipStream_t)stream;
+  NVM_TRY_HIP(nvm::launch_route_partial(dtype, x, T, H, wr, sr, br, E, group_size, splits,
+                                        (double *)workspace, nullptr, st));
+  NVM_TRY_HIP(nvm::launch_route_finalize(dtype, (const double *)workspace, splits, T, E, top_k,
+                                         norm_topk_prob, probs, ids, scores, st));
+  return NVM_OK;
+}
+
+int nvm_moe_dispatch(const int32_t *ids, int64_t n, int64_t E, int32_t *expert_offsets,
+                     int32_t *sorted_pairs, nvm_stream_t stream) {
+  NVM_REQUIRE(expert_offsets && (n == 0 || (ids && sorted_pairs)), "dispatch: null pointer");
+  NVM_REQUIRE(n >= 0 && E > 0, "dispatch: bad shape");
+  NVM_SUPPORTED(E <= kMaxExperts, "dispatch: at most %lld experts", (long long)kMaxExperts);
+  NVM_SUPPORTED(n < (1ll << 31), "dispatch: too many pairs");
+  NVM_TRY_HIP(nvm::launch_dispatch(ids, n, E, expert_offsets, sorted_pairs, nullptr, 0,
+                                   (hipStream_t)stream));
+  return NVM_OK;
+}
+
+int nvm_grouped_linear_workspace_size(int64_t n, int64_t D, int64_t O, int64_t E, size_t *bytes) {
+  NVM_REQUIRE(bytes, "grouped_linear_workspace_size: null output");
+  NVM_REQUIRE(n >= 0 && E > 0, "grouped_linear_workspace_size: bad shape");
+  (void)D;
+  (void)O;
+  Carve c(nullptr);
+  c.take<int32_t>(E + 1);
+  c.take<int32_t>(E + 1);
+  c.take<int32_t>(n);
+  *bytes = (c.off + 255) & ~(size_t)255;
+  return NVM_OK;
+}
+
+int nvm_grouped_expert_linear(const void *x, int64_t n, int64_t D, const uint32_t *w,
+                              const void *s, const void *b, int64_t E, int64_t O, int group_size,
+                              int bits, const int32_t *ids, int dtype, void *out, int regime,
+                              void *workspace, size_t workspace_bytes, nvm_stream_t stream) {
+  if (int r = check_quant(group_size, bits, dtype)) return r;
+  NVM_REQUIRE(n >= 0 && D > 0 && O > 0 && E > 0, "grouped_linear: bad shape");
+  NVM_REQUIRE(n == 0 || (x && w && s && b && ids && out), "grouped_linear: null pointer");
+  NVM_REQUIRE(D % 64 == 0 && D % group_size == 0,
+              "grouped_linear: D=%lld must be a multiple of 64 and of group_size",
+              (long long)D);
+  NVM_REQUIRE(O % 16 == 0, "grouped_linear: output dim %lld must be a multiple of 16",
+              (long long)O);
+  NVM_SUPPORTED(E <= kMaxExperts, "grouped_linear: at most %lld experts", (long long)kMaxExperts);
+  if (n == 0) return NVM_OK;
+  size_t need = 0;
+  nvm_grouped_linear_workspace_size(n, D, O, E, &need);
+  if (!workspace || workspace_bytes < need)
+    return fail(NVM_ERR_WORKSPACE, "grouped_linear: workspace of %zu bytes needed", need);
+  Carve c(workspace);
+  int32_t *offsets = c.take<int32_t>(E + 1);
+  int32_t *tiles = c.take<int32_t>(E + 1);
+  int32_t *sorted = c.take<int32_t>(n);
+  hipStream_t st = (hipStream_t)stream;
+  NVM_TRY_HIP(nvm::launch_dispatch(ids, n, E, offsets, sorted, tiles, nvm::kGemmBM, st));
+  nvm::GroupedArgs g{};
+  g.act = (const uint16_t *)x;
+  g.act_ld = D;
+  g.a_map = sorted;
+  g.a_div = 1;
+  g.offsets = offsets;
+  g.tile_offsets = tiles;
+  g.w0 = w;
+  g.s0 = (const uint16_t *)s;
+  g.b0 = (const uint16_t *)b;
+  g.R = (int)O;
+  g.K = (int)D;
+  g.gs = group_size;
+  g.E = (int)E;
+  g.out = (uint16_t *)out;
+  g.o_map = sorted;
+  g.out_ld = O;
+  return run_products(dtype, use_decode(regime, n, E), false, g, n, st);
+}
+
+int nvm_moe_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, size_t *bytes) {
+  NVM_REQUIRE(bytes, "moe_workspace_size: null output");
+  NVM_REQUIRE(T >= 0 && H > 0 && I > 0 && E > 0 && top_k > 0, "moe_workspace_size: bad shape");
+  *bytes = carve_moe(nullptr, T, H, I, E, top_k).bytes;
+  return NVM_OK;
+}
+
+int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int top_k,
+                    int norm_topk_prob, int group_size, int bits, int dtype, const uint32_t *wr,
+                    const void *sr, const void *br, const uint32_t *wg, const void *sg,
+                    const void *bg, const uint32_t *wu, const void *su, const void *bu,
+                    const uint32_t *wd, const void *sd, const void *bd, void *y, int32_t *ids_out,
+                    void *scores_out, int regime, void *workspace, size_t workspace_bytes,
+                    nvm_stream_t stream) {
+  if (int r = check_quant(group_size, bits, dtype)) return r;
+  NVM_REQUIRE(T >= 0 && H > 0 && I > 0 && E > 0, "moe: bad shape");
+  NVM_REQUIRE(x && y && wr && sr && br && wg && sg && bg && wu && su && bu && wd && sd && bd,
+              "moe: null pointer");
+  NVM_REQUIRE(H % 64 == 0 && H % group_size == 0,
+              "moe: hidden %lld must be a multiple of 64 and of group_size", (long long)H);
+  NVM_REQUIRE(I % 64 == 0 && I % group_size == 0,
+              "moe: intermediate %lld must be a multiple of 64 and of group_size", (long long)I);
+  NVM_SUPPORTED(E <= kMaxExperts, "moe: at most %lld experts", (long long)kMaxExperts);
+  NVM_REQUIRE(top_k >= 1 && top_k <= E, "moe: top_k=%d outside [1, E=%lld]", top_k,
+              (long long)E);
+  NVM_SUPPORTED(top_k <= kMaxTopK, "moe: top_k at most %d", kMaxTopK);
+  NVM_REQUIRE(regime >= NVM_REGIME_AUTO && regime <= NVM_REGIME_PREFILL, "moe: bad regime %d",
+              regime);
+  if (T == 0) return NVM_OK;
+  const size_t need = carve_moe(nullptr, T, H, I, E, top_k).bytes;
+  if (!workspace || workspace_bytes < need)
+    return fail(NVM_ERR_WORKSPACE, "moe: workspace of %zu bytes needed", need);
+  MoeWs ws = carve_moe(workspace, T, H, I, E, top_k);
+  int32_t *ids = ids_out ? ids_out : ws.ids;
+  uint16_t *scores = scores_out ? (uint16_t *)scores_out : ws.scores;
+  const int64_t N = T * top_k;
+  hipStream_t st = (hipStream_t)stream;
+
+  const int splits = nvm::route_splits(T, H);
+  NVM_TRY_HIP(nvm::launch_route_partial(dtype, x, T, H, wr, sr, br, E, group_size, splits,
+                                        ws.partial, nullptr, st));
+  NVM_TRY_HIP(nvm::launch_route_finalize(dtype, ws.partial, splits, T, E, top_k, norm_topk_prob,
+                                         nullptr, ids, scores, st));
+  NVM_TRY_HIP(nvm::launch_dispatch(ids, N, E, ws.offsets, ws.sorted, ws.tile_offsets,
+                                   nvm::kGemmBM, st));
+  const bool decode = use_decode(regime, N, E);
+
+  nvm::GroupedArgs g{};
+  g.act = (const uint16_t *)x;
+  g.act_ld = H;
+  g.a_map = ws.sorted;
+  g.a_div = top_k;
+  g.offsets = ws.offsets;
+  g.tile_offsets = ws.tile_offsets;
+  g.w0 = wg;
+  g.s0 = (const uint16_t *)sg;
+  g.b0 = (const uint16_t *)bg;
+  g.w1 = wu;
+  g.s1 = (const uint16_t *)su;
+  g.b1 = (const uint16_t *)bu;
+  g.R = (int)I;
+  g.K = (int)H;
+  g.gs = group_size;
+  g.E = (int)E;
+  g.out = ws.h;
+  g.o_map = nullptr;
+  g.out_ld = I;
+  if (int r = run_products(dtype, decode, true, g, N, st)) return r;
+
+  nvm::GroupedArgs d{};
+  d.act = ws.h;
+  d.act_ld = I;
+  d.a_map = nullptr;
+  d.a_div = 1;
+  d.offsets = ws.offsets;
+  d.tile_offsets = ws.tile_offsets;
+  d.w0 = wd;
+  d.s0 = (const uint16_t *)sd;
+  d.b0 = (const uint16_t *)bd;
+  d.R = (int)H;
+  d.K = (int)I;
+  d.gs = group_size;
+  d.E = (int)E;
+  d.out = ws.down;
+  d.o_map = ws.sorted;
+  d.out_ld = H;
+  if (int r = run_products(dtype, decode, false, d, N, st)) return r;
+
+  NVM_TRY_HIP(nvm::launch_combine(dtype, ws.down, scores, T, top_k, H, y, st));
+  return NVM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,57 @@
+// Combine: y[t] = sum_j score[t,j] * expert_output[t,j], back in token order.
+//
+// Restates `mx.sum(expert_output * expand_dims(expert_scores, -1), axis=-2)`
+// (layers/moe.py:85-86).  The product is an activation-dtype tensor in the
+// reference, so each term is rounded to act before the float32 sum, which is
+// rounded once.  The per-pair expert outputs were already written in flat pair
+// order (t*k + j) by the down product, so each thread reads k contiguous
+// 16-byte chunks and no atomics are needed: the sum order is fixed.
+#include "common.h"
+#include "internal.h"
+
+namespace nvm {
+
+namespace {
+
+template <int DT>
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict__ down,
+                                                      const uint16_t *__restrict__ scores,
+                                                      int64_t T, int k, int64_t H,
+                                                      uint16_t *__restrict__ y) {
+  using A = Act<DT>;
+  const int64_t chunks = H / 8;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= T * chunks) return;
+  const int64_t t = idx / chunks, c = idx - t * chunks;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < k; ++j) {
+    const float s = A::to_f32(scores[t * k + j]);
+    const u32x4 v = ldg16(down + ((t * k + j) * H + 8 * c));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[2 * i] += round_act<DT>(A::lo(v[i]) * s);
+      acc[2 * i + 1] += round_act<DT>(A::hi(v[i]) * s);
+    }
+  }
+  u32x4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = A::pack2(acc[2 * i], acc[2 * i + 1]);
+  *(u32x4 *)(y + t * H + 8 * c) = o;
+}
+
+}  // namespace
+
+hipError_t launch_combine(int dtype, const void *down, const void *scores, int64_t T, int k,
+                          int64_t H, void *y, hipStream_t st) {
+  const int64_t work = T * (H / 8);
+  dim3 grid((unsigned)((work + 255) / 256));
+  if (dtype == DT_BF16)
+    hipLaunchKernelGGL(combine_kernel<DT_BF16>, grid, dim3(256), 0, st, (const uint16_t *)down,
+                       (const uint16_t *)scores, T, k, H, (uint16_t *)y);
+  else
+    hipLaunchKernelGGL(combine_kernel<DT_F16>, grid, dim3(256), 0, st, (const uint16_t *)down,
+                       (const uint16_t *)scores, T, k, H, (uint16_t *)y);
+  return hipGetLastError();
+}
+
+}  // namespace nvm

@@ -1,0 +1,58 @@
+// Host-side launch interface shared between the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace nvm {
+
+// Arguments of the grouped expert products (decode GEMV and prefill GEMM).
+//   Sorted slot n (expert-major, see dispatch) reads activation row
+//   a_map ? a_map[n] / a_div : n  and writes output row  o_map ? o_map[n] : n.
+//   mat0 = (w0, s0, b0) and, for the fused gate/up product, mat1 = (w1, s1, b1)
+//   are [E, R, K/8] words with [E, R, K/gs] scales and biases.
+struct GroupedArgs {
+  const uint16_t *act;
+  int64_t act_ld;
+  const int32_t *a_map;
+  int a_div;
+  const int32_t *offsets;       // [E+1] slot ranges per expert
+  const int32_t *tile_offsets;  // [E+1] prefill m-tile ranges per expert
+  const uint32_t *w0;
+  const uint16_t *s0, *b0;
+  const uint32_t *w1;
+  const uint16_t *s1, *b1;
+  int R, K, gs, E;
+  uint16_t *out;
+  const int32_t *o_map;
+  int64_t out_ld;
+};
+
+// Router.  Partial float64 logits over an H-split, then per-token finalise.
+int route_splits(int64_t T, int64_t H);
+int route_experts_per_block(int64_t T);
+hipError_t launch_route_partial(int dtype, const void *x, int64_t T, int64_t H, const uint32_t *wr,
+                                const void *sr, const void *br, int64_t E, int gs, int splits,
+                                double *partial, void *final_out, hipStream_t st);
+hipError_t launch_route_finalize(int dtype, const double *partial, int splits, int64_t T,
+                                 int64_t E, int k, int norm, void *probs, int32_t *ids,
+                                 void *scores, hipStream_t st);
+
+// Dispatch: counting sort of ids into expert order; tile_offsets (optional)
+// receives the prefix sum of ceil(count/bm).
+hipError_t launch_dispatch(const int32_t *ids, int64_t n, int64_t E, int32_t *offsets,
+                           int32_t *sorted, int32_t *tile_offsets, int bm, hipStream_t st);
+
+// Grouped products.  dual = fused gate/up with SwiGLU epilogue.
+hipError_t launch_gemv(int dtype, bool dual, const GroupedArgs &a, hipStream_t st);
+constexpr int kGemmBM = 128;   // prefill tile rows (routed pairs)
+constexpr int kGemmBN = 128;   // prefill tile columns per weight matrix
+hipError_t launch_gemm(int dtype, bool dual, const GroupedArgs &a, int64_t max_m_tiles,
+                       hipStream_t st);
+
+// Combine: y[t] = rnd(sum_j rnd(down[t*k+j] * score[t,j])).
+hipError_t launch_combine(int dtype, const void *down, const void *scores, int64_t T, int k,
+                          int64_t H, void *y, hipStream_t st);
+
+}  // namespace nvm

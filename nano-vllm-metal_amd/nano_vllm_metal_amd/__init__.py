@@ -1,0 +1,23 @@
+"""MI355X-native Qwen3 sparse-MoE block with nano-vllm-metal's MoE interface.
+
+Public names mirror the reference's package root for this path
+(``src/nano_vllm_metal/__init__.py:6,8``): ``QuantizedWeights``,
+``quantized_matmul``, ``quantized_linear``, ``route_topk``,
+``grouped_expert_linear`` and ``Moe``.  All compute runs in HIP kernels on the
+GPU (libnvm_moe.so); nothing falls back to the CPU.
+"""
+
+from .linear import QuantizedWeights, dequantize, quantize, quantized_linear, quantized_matmul
+from .moe import Moe, grouped_expert_linear, moe_dispatch, route_topk
+
+__all__ = [
+    "QuantizedWeights",
+    "quantize",
+    "dequantize",
+    "quantized_matmul",
+    "quantized_linear",
+    "route_topk",
+    "grouped_expert_linear",
+    "moe_dispatch",
+    "Moe",
+]

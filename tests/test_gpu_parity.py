@@ -1,0 +1,224 @@
+"""GPU parity of the HIP path against the CPU oracle (run on an MI355X).
+
+Integer outputs (top-k ids, dispatch permutations) must match bit for bit;
+activation-dtype outputs within the tolerances stated in helpers.py.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (assert_moe_close, make_moe, qweights, to_act, to_np, to_words)
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _route_case(seed, T, H, E, k, act, gs, norm, x_std=1.0, router_std=0.02):
+    rng = np.random.default_rng(seed)
+    x = O.round_act(rng.standard_normal((T, H)) * x_std, act)
+    wr = O.round_act(rng.standard_normal((E, H)) * router_std, act)
+    router = O.quantize(wr, gs, 4, act)
+    return x, router
+
+
+# ---------------------------------------------------------------- router
+
+
+@pytest.mark.parametrize("T,H,E,k,act,gs", [
+    (32, 256, 16, 4, "float16", 64),       # tiny parity config
+    (4, 128, 4, 2, "float16", 128),        # reference test_router_topk shape
+    (1, 2048, 128, 8, "bfloat16", 64),     # 30B-A3B decode batches
+    (8, 2048, 128, 8, "bfloat16", 64),
+    (32, 2048, 128, 8, "bfloat16", 64),
+    (64, 2048, 128, 8, "bfloat16", 64),
+    (600, 2048, 128, 8, "bfloat16", 64),   # large-T router tiling
+    (32, 4096, 128, 8, "bfloat16", 64),    # 235B-A22B shape
+])
+@pytest.mark.parametrize("norm", [False, True])
+def test_route_bit_exact(T, H, E, k, act, gs, norm):
+    from nano_vllm_metal_amd import route_topk
+
+    x, router = _route_case(1000 + T + H + E, T, H, E, k, act, gs, norm)
+    _, probs_ref, ids_ref, sc_ref = O.route_topk(x, *router, gs, k, norm, act)
+    w = qweights(router, act, gs, DEV)
+    probs, ids, scores = route_topk(to_act(x, act, DEV), w, k, norm)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy(), ids_ref), "top-k ids differ"
+    assert np.array_equal(to_np(probs), probs_ref), "probs differ"
+    assert np.array_equal(to_np(scores), sc_ref), "scores differ"
+
+
+def test_route_ties_pick_lower_index():
+    """All-zero router weights: every prob is 1/E, ids must be 0..k-1."""
+    from nano_vllm_metal_amd import QuantizedWeights, route_topk
+
+    T, H, E, k = 5, 256, 16, 4
+    x = torch.randn(T, H, device=DEV).to(torch.bfloat16)
+    w = QuantizedWeights(torch.zeros(E, H // 64, dtype=torch.bfloat16, device=DEV),
+                         torch.zeros(E, H // 64, dtype=torch.bfloat16, device=DEV), 64, 4,
+                         torch.zeros(E, H // 8, dtype=torch.int32, device=DEV))
+    probs, ids, scores = route_topk(x, w, k, norm_topk_prob=True)
+    assert ids.tolist() == [list(range(k))] * T
+    assert torch.all(probs == probs[0, 0]).item()
+    assert torch.all(scores.float() == 0.25).item()
+
+
+def test_quantized_matmul_identity_known_answer():
+    """Identity activations return the dequantised rows (test_quantized_matmul.py:13-14)."""
+    from nano_vllm_metal_amd import quantized_matmul
+
+    for act, gs in (("float16", 128), ("bfloat16", 128), ("bfloat16", 64)):
+        rng = np.random.default_rng(7)
+        w = O.round_act(rng.standard_normal((5, gs)), act)
+        wq, s, b = O.quantize(w, gs, 4, act)
+        eye = np.eye(gs)
+        out = quantized_matmul(to_act(s, act, DEV), to_act(b, act, DEV), gs, 4,
+                               to_act(eye, act, DEV), to_words(wq, DEV), transpose_b=True)
+        ref = O.round_act(O.dequantize(wq, s, b, gs).T, act)
+        assert np.array_equal(to_np(out), ref)
+
+
+@pytest.mark.parametrize("M,N,K,act,gs", [(3, 128, 5, "float16", 128), (300, 512, 96, "bfloat16", 64),
+                                          (7, 2048, 128, "bfloat16", 64)])
+def test_quantized_matmul_matches_oracle(M, N, K, act, gs):
+    from nano_vllm_metal_amd import quantized_matmul
+
+    rng = np.random.default_rng(M * N + K)
+    a = O.round_act(rng.standard_normal((M, N)), act)
+    w = O.round_act(rng.standard_normal((K, N)), act)
+    wq, s, b = O.quantize(w, gs, 4, act)
+    out = quantized_matmul(to_act(s, act, DEV), to_act(b, act, DEV), gs, 4, to_act(a, act, DEV),
+                           to_words(wq, DEV), transpose_b=True)
+    assert np.array_equal(to_np(out), O.quantized_matmul(a, wq, s, b, gs, act))
+
+
+# ---------------------------------------------------------------- dispatch
+
+
+@pytest.mark.parametrize("n,E", [(0, 8), (1, 1), (256, 128), (100, 3), (32768, 128), (5000, 512),
+                                 (4096, 1)])
+def test_dispatch_matches_stable_argsort(n, E):
+    from nano_vllm_metal_amd import moe_dispatch
+
+    rng = np.random.default_rng(n + E)
+    ids = rng.integers(0, E, size=n).astype(np.int32)
+    off, srt = moe_dispatch(torch.from_numpy(ids).to(DEV), E)
+    off_ref, srt_ref = O.dispatch(ids, E)
+    assert np.array_equal(off.cpu().numpy(), off_ref)
+    assert np.array_equal(srt.cpu().numpy(), srt_ref)
+
+
+def test_dispatch_skewed_and_out_of_range():
+    from nano_vllm_metal_amd import moe_dispatch
+
+    E = 128
+    rng = np.random.default_rng(5)
+    ids = np.where(rng.random(20000) < 0.9, 3, rng.integers(0, E, 20000)).astype(np.int32)
+    off, srt = moe_dispatch(torch.from_numpy(ids).to(DEV), E)
+    off_ref, srt_ref = O.dispatch(ids, E)
+    assert np.array_equal(off.cpu().numpy(), off_ref)
+    assert np.array_equal(srt.cpu().numpy(), srt_ref)
+    # ids outside [0, E) are dropped; the rest keep their stable order
+    bad = ids.copy()
+    bad[::7] = E + 5
+    bad[1::11] = -1
+    off, srt = moe_dispatch(torch.from_numpy(bad).to(DEV), E)
+    keep = np.nonzero((bad >= 0) & (bad < E))[0]
+    o2, s2 = O.dispatch(bad[keep], E)
+    assert np.array_equal(off.cpu().numpy(), o2)
+    assert np.array_equal(srt.cpu().numpy()[: len(keep)], keep[s2])
+
+
+# ---------------------------------------------------------------- grouped linear
+
+
+@pytest.mark.parametrize("regime", ["decode", "prefill"])
+def test_grouped_expert_linear_reference_shape(regime):
+    """test_moe.py:19-49 shape: x [2,3,128], 3 experts of [64,128], group 128."""
+    from nano_vllm_metal_amd import grouped_expert_linear
+
+    act, gs = "float16", 128
+    rng = np.random.default_rng(1)
+    x = O.round_act(rng.standard_normal((2, 3, 128)) * 0.25, act)
+    w = O.round_act(rng.standard_normal((3, 64, 128)) * 0.25, act)
+    wq, s, b = O.quantize(w, gs, 4, act)
+    ids = np.array([[2, 0, 1], [1, 2, 0]], dtype=np.int32)
+    out = grouped_expert_linear(to_act(x, act, DEV), qweights((wq, s, b), act, gs, DEV),
+                                torch.from_numpy(ids).to(DEV), regime=regime)
+    ref = O.grouped_expert_linear(x, wq, s, b, gs, ids, act)
+    assert out.shape == (2, 3, 64)
+    assert_moe_close(out, ref, act, f"grouped linear {regime}")
+
+
+@pytest.mark.parametrize("regime", ["decode", "prefill"])
+@pytest.mark.parametrize("n,D,O_,E,act", [(200, 512, 256, 8, "bfloat16"), (77, 768, 2048, 16, "bfloat16"),
+                                          (300, 256, 128, 4, "float16")])
+def test_grouped_expert_linear_matches_oracle(regime, n, D, O_, E, act):
+    from nano_vllm_metal_amd import grouped_expert_linear
+
+    gs = 64
+    rng = np.random.default_rng(n + D)
+    x = O.round_act(rng.standard_normal((n, D)), act)
+    w = O.round_act(rng.standard_normal((E, O_, D)) * 0.02, act)
+    wq, s, b = O.quantize(w, gs, 4, act)
+    ids = rng.integers(0, E, n).astype(np.int32)
+    out = grouped_expert_linear(to_act(x, act, DEV), qweights((wq, s, b), act, gs, DEV),
+                                torch.from_numpy(ids).to(DEV), regime=regime)
+    ref = O.grouped_expert_linear(x, wq, s, b, gs, ids, act)
+    assert_moe_close(out, ref, act, f"grouped linear {regime}")
+
+
+# ---------------------------------------------------------------- full block
+
+
+def _moe_case(seed, T, H, E, I, act, gs=64):
+    return O.make_inputs(seed, T, H, E, I, act, gs)
+
+
+def _check_moe(x, weights, k, norm, act, gs, regime="auto", rows=None):
+    moe = make_moe(weights, act, gs, k, norm, DEV)
+    moe.regime = regime
+    y, ids, scores = moe.forward(to_act(x, act, DEV), return_routing=True)
+    torch.cuda.synchronize()
+    sel = slice(None) if rows is None else rows
+    y_ref, ids_ref, sc_ref = O.moe_forward(x[sel], weights, k, norm, act, gs)
+    assert np.array_equal(ids.cpu().numpy()[sel], ids_ref), "ids differ"
+    assert np.array_equal(to_np(scores)[sel], sc_ref), "scores differ"
+    return assert_moe_close(to_np(y)[sel], y_ref, act, f"moe {regime}")
+
+
+@pytest.mark.parametrize("regime", ["auto", "decode", "prefill"])
+def test_moe_tiny_config(regime):
+    x, w = _moe_case(11, 32, 256, 16, 128, "float16")
+    _check_moe(x, w, 4, True, "float16", 64, regime)
+
+
+@pytest.mark.parametrize("regime", ["decode", "prefill"])
+def test_moe_reference_test_shape(regime):
+    """test_moe.py:93-131 shape: hidden 128, inter 128, 3 experts, top-2, renorm, g128."""
+    act, gs = "float16", 128
+    rng = np.random.default_rng(3)
+    s = 0.25
+    x = O.round_act(rng.standard_normal((6, 128)) * s, act)
+    w = {"router": O.quantize(O.round_act(rng.standard_normal((3, 128)) * s, act), gs, 4, act),
+         "gate": O.quantize(O.round_act(rng.standard_normal((3, 128, 128)) * s, act), gs, 4, act),
+         "up": O.quantize(O.round_act(rng.standard_normal((3, 128, 128)) * s, act), gs, 4, act),
+         "down": O.quantize(O.round_act(rng.standard_normal((3, 128, 128)) * s, act), gs, 4, act)}
+    _check_moe(x, w, 2, True, act, gs, regime)
+
+
+@pytest.mark.parametrize("T", [1, 8, 32, 64])
+def test_moe_30b_decode(T):
+    x, w = _moe_case(100 + T, T, 2048, 128, 768, "bfloat16")
+    _check_moe(x, w, 8, True, "bfloat16", 64, "auto")
+
+
+def test_moe_30b_prefill_sampled_rows():
+    """T=512 through the prefill GEMM, every row checked; T=4096 rows sampled."""
+    x, w = _moe_case(200, 512, 2048, 128, 768, "bfloat16")
+    _check_moe(x, w, 8, True, "bfloat16", 64, "prefill")
