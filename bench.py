@@ -1,0 +1,453 @@
+#!/usr/bin/env python
+"""Benchmark of the Qwen3 sparse-MoE block on one MI355X.
+
+Headline: MoE-layer tokens/s at the Qwen3-30B-A3B shape (hidden 2048, 128
+experts, top-8 with renormalisation, moe_intermediate 768, MLX-affine int4
+with group 64 and bf16 scale/bias), decode batch of 32 tokens.  One step is
+one full MoE layer (route -> dispatch -> gate/up+SwiGLU -> down -> combine)
+over one batch whose activations are already resident in HBM.  Eight distinct
+layers of weights (2.7 GB packed) are cycled so the 256 MB MALL cannot hold
+them.  The decode value is timed over HIP-graph replays of the layer calls;
+per-kernel durations come from HIP events around each stage in an eager pass.
+
+Also reported: decode batches 1/8/64, prefill of 4096 tokens with uniform and
+Zipf(1.1) routing (MFMA roofline), and the CPU baseline (the C restatement of
+the reference algorithm in oracle/, timed on a bounded sample).
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "nano-vllm-metal_amd"))
+
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # dense bf16 MFMA
+METRIC = "MoE-layer tokens/s + HBM GB/s, 30B-A3B shape, decode B=32 / prefill 4K"
+SHAPE = dict(H=2048, E=128, I=768, k=8, gs=64)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def bytes_per_expert(H, I, gs):
+    """Packed int4 codes plus bf16 scale and bias, split (gate+up, down)."""
+    gateup = 2 * (I * H // 2 + 2 * 2 * I * (H // gs))
+    down = H * I // 2 + 2 * 2 * H * (I // gs)
+    return gateup, down
+
+
+def router_bytes(H, E, gs):
+    return E * H // 2 + 2 * 2 * E * (H // gs)
+
+
+def make_layers(n_layers, H, E, I, gs, dev, seed=1234, zipf_s=None):
+    import torch
+    from nano_vllm_metal_amd import Moe, QuantizedWeights, quantize
+
+    gen = torch.Generator(device=dev)
+    layers = []
+    for li in range(n_layers):
+        gen.manual_seed(seed + li)
+
+        def q(shape, std=0.02, router_bias=None):
+            w = (torch.randn(shape, generator=gen, device=dev) * std)
+            if router_bias is not None:
+                # one 64-wide activation group is held at 1.0 by the Zipf
+                # inputs; these router columns then add log-popularity offsets
+                w[:, :64] = (router_bias / 64.0)[:, None]
+            wq, s, b = quantize(w.to(torch.bfloat16), gs, 4)
+            return QuantizedWeights(s, b, gs, 4, wq)
+
+        bias = None
+        if zipf_s is not None:
+            ranks = torch.arange(1, E + 1, device=dev, dtype=torch.float32)
+            p = ranks ** (-zipf_s)
+            bias = torch.log(p / p.sum())
+        moe = Moe(q((E, H), router_bias=bias), q((E, I, H)), q((E, I, H)), q((E, H, I)),
+                  num_experts_per_tok=SHAPE["k"], norm_topk_prob=True)
+        layers.append(moe)
+    torch.cuda.synchronize()
+    return layers
+
+
+def make_inputs(n, T, H, dev, seed=99, zipf=False):
+    import torch
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    xs = []
+    for _ in range(n):
+        x = torch.randn((T, H), generator=gen, device=dev)
+        if zipf:
+            x[:, :64] = 1.0
+        xs.append(x.to(torch.bfloat16))
+    return xs
+
+
+class Stages:
+    """Stage-level calls of the block (the kernels nvm_moe_forward runs)."""
+
+    def __init__(self, moe, T, dev):
+        import torch
+        from nano_vllm_metal_amd import _lib
+
+        self.lib = _lib.load()
+        self.L = _lib
+        self.moe = moe
+        self.dev = dev
+        E = moe.w_router.weight.shape[0]
+        H = moe.w_router.weight.shape[1] * 8
+        I = moe.w_gate.weight.shape[1]
+        k = moe.num_experts_per_tok
+        self.T, self.H, self.I, self.E, self.k = T, H, I, E, k
+        N = T * k
+        bf = torch.bfloat16
+        self.ids = torch.empty((T, k), dtype=torch.int32, device=dev)
+        self.scores = torch.empty((T, k), dtype=bf, device=dev)
+        self.offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+        self.sorted = torch.empty(N, dtype=torch.int32, device=dev)
+        self.h = torch.empty((N, I), dtype=bf, device=dev)
+        self.down = torch.empty((N, H), dtype=bf, device=dev)
+        self.y = torch.empty((T, H), dtype=bf, device=dev)
+        size = ctypes.c_size_t()
+        self.L.check(self.lib.nvm_route_workspace_size(T, H, E, ctypes.byref(size)))
+        self.rws = torch.empty(max(size.value, 1), dtype=torch.uint8, device=dev)
+
+    def run(self, x, events=None):
+        lib, L, m = self.lib, self.L, self.moe
+        st = L.stream_of(self.dev)
+        T, H, I, E, k = self.T, self.H, self.I, self.E, self.k
+        gs = m.w_gate.group_size
+        r, g, u, d = m.w_router, m.w_gate, m.w_up, m.w_down
+        ev = events or [None] * 6
+
+        def rec(i):
+            if ev[i] is not None:
+                ev[i].record()
+
+        rec(0)
+        L.check(lib.nvm_moe_route(x.data_ptr(), T, H, r.weight.data_ptr(), r.scales.data_ptr(),
+                                  r.biases.data_ptr(), E, gs, 4, k, 1, 1, None,
+                                  self.ids.data_ptr(), self.scores.data_ptr(),
+                                  self.rws.data_ptr(), self.rws.numel(), st))
+        rec(1)
+        L.check(lib.nvm_moe_dispatch(self.ids.data_ptr(), T * k, E, self.offsets.data_ptr(),
+                                     self.sorted.data_ptr(), st))
+        rec(2)
+        L.check(lib.nvm_moe_expert_gateup(
+            x.data_ptr(), T, H, I, E, k, gs, 4, 1, g.weight.data_ptr(), g.scales.data_ptr(),
+            g.biases.data_ptr(), u.weight.data_ptr(), u.scales.data_ptr(), u.biases.data_ptr(),
+            self.offsets.data_ptr(), self.sorted.data_ptr(), self.h.data_ptr(), 0, st))
+        rec(3)
+        L.check(lib.nvm_moe_expert_down(
+            self.h.data_ptr(), T * k, H, I, E, gs, 4, 1, d.weight.data_ptr(),
+            d.scales.data_ptr(), d.biases.data_ptr(), self.offsets.data_ptr(),
+            self.sorted.data_ptr(), self.down.data_ptr(), 0, st))
+        rec(4)
+        L.check(lib.nvm_moe_combine(self.down.data_ptr(), self.scores.data_ptr(), T, k, H, 1,
+                                    self.y.data_ptr(), st))
+        rec(5)
+        return self.y
+
+
+STAGE_NAMES = ["route", "dispatch", "gateup", "down", "combine"]
+
+
+def eager_stage_pass(layers, xs, steps, warmup, dev):
+    """Per-stage HIP-event durations (us) and touched-expert counts per step."""
+    import torch
+
+    T = xs[0].shape[0]
+    stages = [Stages(m, T, dev) for m in layers]
+    for i in range(warmup):
+        stages[i % len(layers)].run(xs[i % len(xs)])
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(steps)]
+    touched = []
+    ids_snap = []
+    for i in range(steps):
+        s = stages[i % len(layers)]
+        s.run(xs[i % len(xs)], evs[i])
+        ids_snap.append(s.ids.clone())
+    torch.cuda.synchronize()
+    dur = {n: 0.0 for n in STAGE_NAMES}
+    total = 0.0
+    for i in range(steps):
+        for j, n in enumerate(STAGE_NAMES):
+            dur[n] += evs[i][j].elapsed_time(evs[i][j + 1]) * 1e3
+        total += evs[i][0].elapsed_time(evs[i][5]) * 1e3
+    for i in range(steps):
+        touched.append(int(torch.unique(ids_snap[i]).numel()))
+    return {n: v / steps for n, v in dur.items()}, total / steps, touched, ids_snap
+
+
+def graph_pass(layers, xs, steps, warmup, dev):
+    """Layer time (us) over HIP-graph replays of len(layers) fused layer calls."""
+    import torch
+
+    L = len(layers)
+    for i in range(max(warmup, L)):
+        layers[i % L](xs[i % len(xs)])
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(L):
+            layers[i](xs[i % len(xs)])
+    torch.cuda.synchronize()
+    reps = max(1, steps // L)
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * L)
+    return us, reps * L
+
+
+def eager_fused_pass(layers, xs, steps, warmup, dev):
+    import torch
+
+    L = len(layers)
+    for i in range(warmup):
+        layers[i % L](xs[i % len(xs)])
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        layers[i % L](xs[i % len(xs)])
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / steps
+
+
+def decode_bench(layers, T, steps, warmup, dev, use_graph=True):
+    H, E, I, k, gs = (SHAPE[n] for n in ("H", "E", "I", "k", "gs"))
+    xs = make_inputs(8, T, H, dev)
+    stage_us, eager_layer_us, touched, _ = eager_stage_pass(layers, xs, steps, warmup, dev)
+    fused_us = eager_fused_pass(layers, xs, steps, warmup, dev)
+    graph_us, graph_steps = graph_pass(layers, xs, steps, warmup, dev) if use_graph else (None, 0)
+    gu_b, dn_b = bytes_per_expert(H, I, gs)
+    avg_touched = sum(touched) / len(touched)
+    layer_bytes = avg_touched * (gu_b + dn_b) + router_bytes(H, E, gs) + 2 * T * H * 2
+    gateup_bytes = avg_touched * gu_b + T * H * 2
+    layer_us = graph_us if graph_us is not None else fused_us
+    return {
+        "tokens": T,
+        "tokens_per_s": T / (layer_us * 1e-6),
+        "layer_us": layer_us,
+        "timing": "hipGraph replay" if graph_us is not None else "eager",
+        "eager_layer_us": fused_us,
+        "eager_staged_layer_us": eager_layer_us,
+        "kernel_us": stage_us,
+        "touched_experts_avg": avg_touched,
+        "layer_algorithmic_bytes": layer_bytes,
+        "hbm_gbs": layer_bytes / (layer_us * 1e-6) / 1e9,
+        "gateup_algorithmic_bytes": gateup_bytes,
+        "gateup_gbs": gateup_bytes / (stage_us["gateup"] * 1e-6) / 1e9,
+        "down_gbs": avg_touched * dn_b / (stage_us["down"] * 1e-6) / 1e9,
+        "graph_steps": graph_steps,
+    }
+
+
+def prefill_bench(layers, T, steps, warmup, dev, zipf):
+    import torch
+
+    H, E, I, k, gs = (SHAPE[n] for n in ("H", "E", "I", "k", "gs"))
+    xs = make_inputs(2, T, H, dev, seed=7 if zipf else 5, zipf=zipf)
+    stage_us, layer_us, touched, ids = eager_stage_pass(layers, xs, steps, warmup, dev)
+    N = T * k
+    gateup_flops = 2.0 * N * H * 2 * I
+    down_flops = 2.0 * N * I * H
+    layer_flops = gateup_flops + down_flops + 2.0 * T * H * E
+    counts = torch.bincount(ids[0].reshape(-1).long(), minlength=E).float()
+    return {
+        "tokens": T,
+        "routing": "zipf(1.1)" if zipf else "uniform",
+        "tokens_per_s": T / (layer_us * 1e-6),
+        "layer_us": layer_us,
+        "timing": "eager",
+        "kernel_us": stage_us,
+        "layer_tflops": layer_flops / (layer_us * 1e-6) / 1e12,
+        "gateup_tflops": gateup_flops / (stage_us["gateup"] * 1e-6) / 1e12,
+        "down_tflops": down_flops / (stage_us["down"] * 1e-6) / 1e12,
+        "layer_mfma_frac": layer_flops / (layer_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+        "expert_load_max_over_mean": float(counts.max() / counts.mean()),
+        "experts_touched": int((counts > 0).sum()),
+    }
+
+
+def cpu_baseline(layer, T, seconds, dev):
+    """The C restatement of the reference path (oracle/moe_ref.c) on host cores."""
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, str(ROOT))
+    from oracle import moe_ref as R
+
+    R.build()
+    threads = R.threads(min(16, len(os.sched_getaffinity(0))))
+    ops = []
+    for w in (layer.w_router, layer.w_gate, layer.w_up, layer.w_down):
+        ops += [w.weight.cpu().numpy().view(np.uint32),
+                w.scales.view(torch.int16).cpu().numpy().view(np.uint16),
+                w.biases.view(torch.int16).cpu().numpy().view(np.uint16)]
+    cl = R.Layer.from_arrays(ops, "bfloat16")
+    xs = make_inputs(4, T, SHAPE["H"], dev, seed=31)
+    xb = [x.view(torch.int16).cpu().numpy().view(np.uint16) for x in xs]
+    # routing agreement of the CPU restatement and the GPU path on the sample
+    _, gids, _ = layer.forward(xs[0], return_routing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    cids = None
+    while True:
+        _, ids, _ = R.forward(xb[n % len(xb)], cl, SHAPE["k"], True, SHAPE["gs"])
+        if n == 0:
+            cids = ids
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= 2:
+            break
+    return {
+        "value": T * n / el,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n} decode layers of {T} tokens at the 30B-A3B shape (one weight set), "
+                  f"{el:.1f} s, OpenMP over routed pairs",
+        "routing_matches_gpu": bool(np.array_equal(cids, gids.cpu().numpy())),
+    }
+
+
+def read_traffic(name):
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get(name)
+    except (ValueError, OSError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--layers", type=int, default=8, help="distinct weight sets cycled")
+    ap.add_argument("--no-extra", action="store_true", help="headline decode line only")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-graph", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the MoE block is benchmarked on a single MI355X "
+              "(multi-GPU expert/tensor sharding is not part of this build); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    H, E, I, k, gs = (SHAPE[n] for n in ("H", "E", "I", "k", "gs"))
+    log(f"[bench] building {args.layers} layers of 30B-A3B MoE weights")
+    layers = make_layers(args.layers, H, E, I, gs, dev)
+
+    log(f"[bench] decode B={args.batch}: {args.steps} steps, {args.warmup} warmup")
+    head = decode_bench(layers, args.batch, args.steps, args.warmup, dev, not args.no_graph)
+    log(f"[bench] decode B={args.batch}: {head['layer_us']:.1f} us/layer, "
+        f"{head['hbm_gbs']:.0f} GB/s, kernels {head['kernel_us']}")
+
+    gu_b, _ = bytes_per_expert(H, I, gs)
+    achieved = head["gateup_gbs"]
+    out = {
+        "metric": METRIC,
+        "value": head["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["layer_us"] / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) bf16 activations, N(0,0.02) weights MLX-affine "
+                f"int4 g64 with bf16 scale/bias, {args.layers} distinct layers cycled",
+        "config": {"workload": f"Qwen3-30B-A3B-shaped MoE layer, decode batch {args.batch}",
+                   "tokens": args.batch, "hidden": H, "experts": E, "top_k": k,
+                   "moe_intermediate": I, "group_size": gs, "bits": 4,
+                   "weight_sets": args.layers, "timing": head["timing"]},
+        "hbm_gbs": head["hbm_gbs"],
+        "roofline": {
+            "kernel": "gemv_kernel<bf16, gate/up+SwiGLU> (nvm_moe_expert_gateup, decode)",
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": read_traffic("decode_gateup"),
+            "algorithmic_bytes_per_launch": head["gateup_algorithmic_bytes"],
+            "avg_launch_us": head["kernel_us"]["gateup"],
+        },
+        "layer_roofline": {"bound": "hbm", "achieved": head["hbm_gbs"], "peak": HBM_PEAK_GBS,
+                           "unit": "GB/s", "frac": head["hbm_gbs"] / HBM_PEAK_GBS,
+                           "algorithmic_bytes": head["layer_algorithmic_bytes"]},
+        "decode": {str(args.batch): head},
+    }
+    if not args.no_extra:
+        for T in (1, 8, 64):
+            log(f"[bench] decode B={T}")
+            r = decode_bench(layers, T, max(args.steps // 2, 16), args.warmup // 2, dev,
+                             not args.no_graph)
+            out["decode"][str(T)] = r
+            log(f"[bench] decode B={T}: {r['layer_us']:.1f} us/layer, {r['hbm_gbs']:.0f} GB/s")
+        out["prefill"] = {}
+        psteps = max(args.steps // 20, 8)
+        for zipf in (False, True):
+            lay = layers if not zipf else make_layers(2, H, E, I, gs, dev, seed=777, zipf_s=1.1)
+            log(f"[bench] prefill 4096 {'zipf' if zipf else 'uniform'}: {psteps} steps")
+            r = prefill_bench(lay, 4096, psteps, 3, dev, zipf)
+            out["prefill"][r["routing"]] = r
+            log(f"[bench] prefill {r['routing']}: {r['layer_us']:.1f} us/layer, "
+                f"{r['layer_tflops']:.0f} TFLOP/s, kernels {r['kernel_us']}")
+            if zipf:
+                del lay
+        u = out["prefill"]["uniform"]
+        out["prefill_roofline"] = {
+            "kernel": "gemm_kernel<bf16, gate/up+SwiGLU> (nvm_moe_expert_gateup, prefill)",
+            "bound": "mfma", "achieved": u["gateup_tflops"], "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": u["gateup_tflops"] / MFMA_BF16_PEAK_TFLOPS,
+            "traffic": read_traffic("prefill_gateup"),
+        }
+    if not args.no_cpu:
+        log(f"[bench] CPU baseline (~{args.cpu_seconds:.0f} s)")
+        out["cpu_baseline"] = cpu_baseline(layers[0], args.batch, args.cpu_seconds, dev)
+        log(f"[bench] CPU baseline: {out['cpu_baseline']['value']:.0f} tokens/s on "
+            f"{out['cpu_baseline']['cores']} threads")
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

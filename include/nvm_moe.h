@@ -114,6 +114,44 @@ int nvm_grouped_expert_linear(const void *x, int64_t n, int64_t D, const uint32_
                               nvm_stream_t stream);
 
 /*
+ * Stages of the block after routing and dispatch, callable one at a time
+ * (the fused nvm_moe_forward runs exactly these).  `expert_offsets` and
+ * `sorted_pairs` are the outputs of nvm_moe_dispatch over the T*k flat ids.
+ *
+ * Gate/up products with fused SwiGLU: for sorted slot n (pair p =
+ * sorted_pairs[n], token p / k, expert e), h[n] = rnd(silu(rnd(x.Wg[e]^T)) *
+ * rnd(x.Wu[e]^T)).  Replaces the gate and up `grouped_expert_linear` calls and
+ * `silu(gate) * up` of layers/moe.py:81-84 (layers/activation.py:21-24).
+ *   x [T,H] act; wg/wu [E,I,H/8]; sg,bg,su,bu [E,I,H/group]; h [T*k, I] act
+ */
+int nvm_moe_expert_gateup(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int top_k,
+                          int group_size, int bits, int dtype, const uint32_t *wg,
+                          const void *sg, const void *bg, const uint32_t *wu, const void *su,
+                          const void *bu, const int32_t *expert_offsets,
+                          const int32_t *sorted_pairs, void *h, int regime,
+                          nvm_stream_t stream);
+
+/*
+ * Down product: down[sorted_pairs[n]] = rnd(h[n] . Wd[e]^T), written in flat
+ * pair order (the `out[inv_sort_idx]` un-permute of layers/moe.py:33).
+ * Replaces the down `grouped_expert_linear` call of layers/moe.py:83-85.
+ *   h [n_pairs, I] act; wd [E,H,I/8]; sd,bd [E,H,I/group]; down [n_pairs, H] act
+ */
+int nvm_moe_expert_down(const void *h, int64_t n_pairs, int64_t H, int64_t I, int64_t E,
+                        int group_size, int bits, int dtype, const uint32_t *wd, const void *sd,
+                        const void *bd, const int32_t *expert_offsets,
+                        const int32_t *sorted_pairs, void *down, int regime,
+                        nvm_stream_t stream);
+
+/*
+ * Combine: y[t] = rnd(sum_j rnd(down[t*k+j] * scores[t,j])), j in slot order.
+ * Replaces `mx.sum(expert_output * expert_scores[..., None], axis=-2)`
+ * (layers/moe.py:85-86).  H must be a multiple of 8.
+ */
+int nvm_moe_combine(const void *down, const void *scores, int64_t T, int top_k, int64_t H,
+                    int dtype, void *y, nvm_stream_t stream);
+
+/*
  * The whole sparse-MoE block: route -> dispatch -> gate/up products with
  * fused SwiGLU -> down product -> weighted combine.  Replaces `Moe.__call__`
  * (layers/moe.py:69-86).

@@ -38,7 +38,7 @@ int fail(int code, const char *fmt, ...) {
     if (!(cond)) return fail(NVM_ERR_UNSUPPORTED, __VA_ARGS__); \
   } while (0)
 
-constexpr int64_t kMaxExperts = 512;
+constexpr int64_t kMaxExperts = nvm::kMaxExperts;
 constexpr int kMaxTopK = 64;
 
 // Bump allocator over the caller's workspace (256-byte aligned slices).
@@ -69,12 +69,31 @@ bool use_decode(int regime, int64_t pairs, int64_t E) {
   return pairs <= 16 * E;  // up to 16 routed rows per expert on average
 }
 
+// Shapes the expert products handle: K dims in whole 64-wide groups, output
+// rows in whole 16-row MFMA tiles (both implied by multiples of 64).
+int check_products(int64_t H, int64_t I, int64_t E, int top_k, int group_size, int bits,
+                   int dtype, int regime) {
+  if (int r = check_quant(group_size, bits, dtype)) return r;
+  NVM_REQUIRE(H > 0 && I > 0 && E > 0, "moe: bad shape");
+  NVM_REQUIRE(H % 64 == 0 && H % group_size == 0,
+              "moe: hidden %lld must be a multiple of 64 and of group_size", (long long)H);
+  NVM_REQUIRE(I % 64 == 0 && I % group_size == 0,
+              "moe: intermediate %lld must be a multiple of 64 and of group_size", (long long)I);
+  NVM_SUPPORTED(E <= kMaxExperts, "moe: at most %lld experts", (long long)kMaxExperts);
+  NVM_REQUIRE(top_k >= 1 && top_k <= E, "moe: top_k=%d outside [1, E=%lld]", top_k,
+              (long long)E);
+  NVM_SUPPORTED(top_k <= kMaxTopK, "moe: top_k at most %d", kMaxTopK);
+  NVM_REQUIRE(regime >= NVM_REGIME_AUTO && regime <= NVM_REGIME_PREFILL, "moe: bad regime %d",
+              regime);
+  return NVM_OK;
+}
+
 // Workspace of the whole block; with base == nullptr only the size is computed.
 struct MoeWs {
   double *partial;
   int32_t *ids;
   uint16_t *scores;
-  int32_t *offsets, *tile_offsets, *sorted;
+  int32_t *offsets, *sorted;
   uint16_t *h, *down;
   size_t bytes;
 };
@@ -87,7 +106,6 @@ MoeWs carve_moe(void *base, int64_t T, int64_t H, int64_t I, int64_t E, int k) {
   w.ids = c.take<int32_t>(N);
   w.scores = c.take<uint16_t>(N);
   w.offsets = c.take<int32_t>(E + 1);
-  w.tile_offsets = c.take<int32_t>(E + 1);
   w.sorted = c.take<int32_t>(N);
   w.h = c.take<uint16_t>((size_t)N * I);
   w.down = c.take<uint16_t>((size_t)N * H);
@@ -170,8 +188,7 @@ int nvm_moe_dispatch(const int32_t *ids, int64_t n, int64_t E, int32_t *expert_o
   NVM_REQUIRE(n >= 0 && E > 0, "dispatch: bad shape");
   NVM_SUPPORTED(E <= kMaxExperts, "dispatch: at most %lld experts", (long long)kMaxExperts);
   NVM_SUPPORTED(n < (1ll << 31), "dispatch: too many pairs");
-  NVM_TRY_HIP(nvm::launch_dispatch(ids, n, E, expert_offsets, sorted_pairs, nullptr, 0,
-                                   (hipStream_t)stream));
+  NVM_TRY_HIP(nvm::launch_dispatch(ids, n, E, expert_offsets, sorted_pairs, (hipStream_t)stream));
   return NVM_OK;
 }
 
@@ -181,7 +198,6 @@ int nvm_grouped_linear_workspace_size(int64_t n, int64_t D, int64_t O, int64_t E
   (void)D;
   (void)O;
   Carve c(nullptr);
-  c.take<int32_t>(E + 1);
   c.take<int32_t>(E + 1);
   c.take<int32_t>(n);
   *bytes = (c.off + 255) & ~(size_t)255;
@@ -208,17 +224,15 @@ int nvm_grouped_expert_linear(const void *x, int64_t n, int64_t D, const uint32_
     return fail(NVM_ERR_WORKSPACE, "grouped_linear: workspace of %zu bytes needed", need);
   Carve c(workspace);
   int32_t *offsets = c.take<int32_t>(E + 1);
-  int32_t *tiles = c.take<int32_t>(E + 1);
   int32_t *sorted = c.take<int32_t>(n);
   hipStream_t st = (hipStream_t)stream;
-  NVM_TRY_HIP(nvm::launch_dispatch(ids, n, E, offsets, sorted, tiles, nvm::kGemmBM, st));
+  NVM_TRY_HIP(nvm::launch_dispatch(ids, n, E, offsets, sorted, st));
   nvm::GroupedArgs g{};
   g.act = (const uint16_t *)x;
   g.act_ld = D;
   g.a_map = sorted;
   g.a_div = 1;
   g.offsets = offsets;
-  g.tile_offsets = tiles;
   g.w0 = w;
   g.s0 = (const uint16_t *)s;
   g.b0 = (const uint16_t *)b;
@@ -239,6 +253,80 @@ int nvm_moe_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int top_k
   return NVM_OK;
 }
 
+int nvm_moe_expert_gateup(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int top_k,
+                          int group_size, int bits, int dtype, const uint32_t *wg,
+                          const void *sg, const void *bg, const uint32_t *wu, const void *su,
+                          const void *bu, const int32_t *expert_offsets,
+                          const int32_t *sorted_pairs, void *h, int regime,
+                          nvm_stream_t stream) {
+  if (int r = check_products(H, I, E, top_k, group_size, bits, dtype, regime)) return r;
+  NVM_REQUIRE(x && wg && sg && bg && wu && su && bu && expert_offsets && sorted_pairs && h,
+              "expert_gateup: null pointer");
+  if (T == 0) return NVM_OK;
+  nvm::GroupedArgs g{};
+  g.act = (const uint16_t *)x;
+  g.act_ld = H;
+  g.a_map = sorted_pairs;
+  g.a_div = top_k;
+  g.offsets = expert_offsets;
+  g.w0 = wg;
+  g.s0 = (const uint16_t *)sg;
+  g.b0 = (const uint16_t *)bg;
+  g.w1 = wu;
+  g.s1 = (const uint16_t *)su;
+  g.b1 = (const uint16_t *)bu;
+  g.R = (int)I;
+  g.K = (int)H;
+  g.gs = group_size;
+  g.E = (int)E;
+  g.out = (uint16_t *)h;
+  g.o_map = nullptr;
+  g.out_ld = I;
+  const int64_t N = T * top_k;
+  return run_products(dtype, use_decode(regime, N, E), true, g, N, (hipStream_t)stream);
+}
+
+int nvm_moe_expert_down(const void *h, int64_t n_pairs, int64_t H, int64_t I, int64_t E,
+                        int group_size, int bits, int dtype, const uint32_t *wd, const void *sd,
+                        const void *bd, const int32_t *expert_offsets,
+                        const int32_t *sorted_pairs, void *down, int regime,
+                        nvm_stream_t stream) {
+  if (int r = check_products(H, I, E, 1, group_size, bits, dtype, regime)) return r;
+  NVM_REQUIRE(n_pairs >= 0, "expert_down: bad shape");
+  NVM_REQUIRE(h && wd && sd && bd && expert_offsets && sorted_pairs && down,
+              "expert_down: null pointer");
+  if (n_pairs == 0) return NVM_OK;
+  nvm::GroupedArgs d{};
+  d.act = (const uint16_t *)h;
+  d.act_ld = I;
+  d.a_map = nullptr;
+  d.a_div = 1;
+  d.offsets = expert_offsets;
+  d.w0 = wd;
+  d.s0 = (const uint16_t *)sd;
+  d.b0 = (const uint16_t *)bd;
+  d.R = (int)H;
+  d.K = (int)I;
+  d.gs = group_size;
+  d.E = (int)E;
+  d.out = (uint16_t *)down;
+  d.o_map = sorted_pairs;
+  d.out_ld = H;
+  return run_products(dtype, use_decode(regime, n_pairs, E), false, d, n_pairs,
+                      (hipStream_t)stream);
+}
+
+int nvm_moe_combine(const void *down, const void *scores, int64_t T, int top_k, int64_t H,
+                    int dtype, void *y, nvm_stream_t stream) {
+  NVM_REQUIRE(dtype == NVM_DTYPE_F16 || dtype == NVM_DTYPE_BF16, "dtype must be f16 or bf16");
+  NVM_REQUIRE(T >= 0 && top_k >= 1 && H > 0 && H % 8 == 0,
+              "combine: bad shape (H must be a multiple of 8)");
+  NVM_REQUIRE(T == 0 || (down && scores && y), "combine: null pointer");
+  if (T == 0) return NVM_OK;
+  NVM_TRY_HIP(nvm::launch_combine(dtype, down, scores, T, top_k, H, y, (hipStream_t)stream));
+  return NVM_OK;
+}
+
 int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int top_k,
                     int norm_topk_prob, int group_size, int bits, int dtype, const uint32_t *wr,
                     const void *sr, const void *br, const uint32_t *wg, const void *sg,
@@ -246,20 +334,10 @@ int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, i
                     const uint32_t *wd, const void *sd, const void *bd, void *y, int32_t *ids_out,
                     void *scores_out, int regime, void *workspace, size_t workspace_bytes,
                     nvm_stream_t stream) {
-  if (int r = check_quant(group_size, bits, dtype)) return r;
-  NVM_REQUIRE(T >= 0 && H > 0 && I > 0 && E > 0, "moe: bad shape");
+  if (int r = check_products(H, I, E, top_k, group_size, bits, dtype, regime)) return r;
+  NVM_REQUIRE(T >= 0, "moe: bad shape");
   NVM_REQUIRE(x && y && wr && sr && br && wg && sg && bg && wu && su && bu && wd && sd && bd,
               "moe: null pointer");
-  NVM_REQUIRE(H % 64 == 0 && H % group_size == 0,
-              "moe: hidden %lld must be a multiple of 64 and of group_size", (long long)H);
-  NVM_REQUIRE(I % 64 == 0 && I % group_size == 0,
-              "moe: intermediate %lld must be a multiple of 64 and of group_size", (long long)I);
-  NVM_SUPPORTED(E <= kMaxExperts, "moe: at most %lld experts", (long long)kMaxExperts);
-  NVM_REQUIRE(top_k >= 1 && top_k <= E, "moe: top_k=%d outside [1, E=%lld]", top_k,
-              (long long)E);
-  NVM_SUPPORTED(top_k <= kMaxTopK, "moe: top_k at most %d", kMaxTopK);
-  NVM_REQUIRE(regime >= NVM_REGIME_AUTO && regime <= NVM_REGIME_PREFILL, "moe: bad regime %d",
-              regime);
   if (T == 0) return NVM_OK;
   const size_t need = carve_moe(nullptr, T, H, I, E, top_k).bytes;
   if (!workspace || workspace_bytes < need)
@@ -275,53 +353,14 @@ int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, i
                                         ws.partial, nullptr, st));
   NVM_TRY_HIP(nvm::launch_route_finalize(dtype, ws.partial, splits, T, E, top_k, norm_topk_prob,
                                          nullptr, ids, scores, st));
-  NVM_TRY_HIP(nvm::launch_dispatch(ids, N, E, ws.offsets, ws.sorted, ws.tile_offsets,
-                                   nvm::kGemmBM, st));
-  const bool decode = use_decode(regime, N, E);
-
-  nvm::GroupedArgs g{};
-  g.act = (const uint16_t *)x;
-  g.act_ld = H;
-  g.a_map = ws.sorted;
-  g.a_div = top_k;
-  g.offsets = ws.offsets;
-  g.tile_offsets = ws.tile_offsets;
-  g.w0 = wg;
-  g.s0 = (const uint16_t *)sg;
-  g.b0 = (const uint16_t *)bg;
-  g.w1 = wu;
-  g.s1 = (const uint16_t *)su;
-  g.b1 = (const uint16_t *)bu;
-  g.R = (int)I;
-  g.K = (int)H;
-  g.gs = group_size;
-  g.E = (int)E;
-  g.out = ws.h;
-  g.o_map = nullptr;
-  g.out_ld = I;
-  if (int r = run_products(dtype, decode, true, g, N, st)) return r;
-
-  nvm::GroupedArgs d{};
-  d.act = ws.h;
-  d.act_ld = I;
-  d.a_map = nullptr;
-  d.a_div = 1;
-  d.offsets = ws.offsets;
-  d.tile_offsets = ws.tile_offsets;
-  d.w0 = wd;
-  d.s0 = (const uint16_t *)sd;
-  d.b0 = (const uint16_t *)bd;
-  d.R = (int)H;
-  d.K = (int)I;
-  d.gs = group_size;
-  d.E = (int)E;
-  d.out = ws.down;
-  d.o_map = ws.sorted;
-  d.out_ld = H;
-  if (int r = run_products(dtype, decode, false, d, N, st)) return r;
-
-  NVM_TRY_HIP(nvm::launch_combine(dtype, ws.down, scores, T, top_k, H, y, st));
-  return NVM_OK;
+  NVM_TRY_HIP(nvm::launch_dispatch(ids, N, E, ws.offsets, ws.sorted, st));
+  if (int r = nvm_moe_expert_gateup(x, T, H, I, E, top_k, group_size, bits, dtype, wg, sg, bg,
+                                    wu, su, bu, ws.offsets, ws.sorted, ws.h, regime, stream))
+    return r;
+  if (int r = nvm_moe_expert_down(ws.h, N, H, I, E, group_size, bits, dtype, wd, sd, bd,
+                                  ws.offsets, ws.sorted, ws.down, regime, stream))
+    return r;
+  return nvm_moe_combine(ws.down, scores, T, top_k, H, dtype, y, stream);
 }
 
 }  // extern "C"

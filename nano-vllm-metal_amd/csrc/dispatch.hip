@@ -39,7 +39,7 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 // One block of 1024 threads.  Pairs with ids outside [0, E) are dropped.
 __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
     const int32_t *__restrict__ ids, int n, int E, int nbits, int32_t *__restrict__ offsets,
-    int32_t *__restrict__ sorted, int32_t *__restrict__ tile_offsets, int bm) {
+    int32_t *__restrict__ sorted) {
   extern __shared__ int lds[];
   const int W = blockDim.x >> 6;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -75,27 +75,20 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
   }
   __syncthreads();
 
-  // exclusive scan of the totals (and of the m-tile counts) by wavefront 0
+  // exclusive scan of the totals by wavefront 0
   if (wv == 0) {
-    int carry = 0, tcarry = 0;
+    int carry = 0;
     for (int c0 = 0; c0 < E; c0 += 64) {
       const int e = c0 + lane;
       const int v = e < E ? base[e] : 0;
-      const int tv = (bm > 0 && e < E) ? (v + bm - 1) / bm : 0;
       const int inc = wave_incl_scan(v, lane);
-      const int tinc = wave_incl_scan(tv, lane);
       if (e < E) {
         base[e] = carry + inc - v;
         offsets[e] = carry + inc - v;
-        if (tile_offsets) tile_offsets[e] = tcarry + tinc - tv;
       }
       carry += __shfl(inc, 63);
-      tcarry += __shfl(tinc, 63);
     }
-    if (lane == 0) {
-      offsets[E] = carry;
-      if (tile_offsets) tile_offsets[E] = tcarry;
-    }
+    if (lane == 0) offsets[E] = carry;
   }
   __syncthreads();
 
@@ -120,13 +113,13 @@ __global__ __launch_bounds__(kDispatchThreads) void dispatch_kernel(
 }  // namespace
 
 hipError_t launch_dispatch(const int32_t *ids, int64_t n, int64_t E, int32_t *offsets,
-                           int32_t *sorted, int32_t *tile_offsets, int bm, hipStream_t st) {
+                           int32_t *sorted, hipStream_t st) {
   int nbits = 0;
   while ((1ll << nbits) < E) ++nbits;
   const int W = kDispatchThreads / 64;
   const size_t lds = sizeof(int) * (size_t)(W * E + E);
   hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(kDispatchThreads), lds, st, ids, (int)n,
-                     (int)E, nbits, offsets, sorted, tile_offsets, bm);
+                     (int)E, nbits, offsets, sorted);
   return hipGetLastError();
 }
 

@@ -3,7 +3,7 @@
 // Replaces `mx.gather_qmm` inside grouped_expert_linear (layers/moe.py:21-32)
 // for prefill-sized batches, with SwiGLU (layers/moe.py:84) fused into the
 // gate/up epilogue.  Work is a list of (expert, 128-row m-tile) pairs built on
-// the device by the dispatch kernel (prefix sum of ceil(count_e / 128)), so no
+// the device from the expert offsets (prefix sum of ceil(count_e / 128)), so no
 // host synchronisation is needed and empty experts cost nothing.
 //
 // Per 64-wide k-step a 256-thread block gathers 128 activation rows into LDS,
@@ -27,21 +27,41 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GroupedArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t As[BM * PITCH];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[2 * BN * PITCH];
   __shared__ int s_arow[BM];
+  __shared__ int s_tiles[kMaxExperts + 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int mt = blockIdx.y;
-  if (mt >= a.tile_offsets[a.E]) return;
+  // m-tile list: exclusive prefix over experts of ceil(count / BM), built by
+  // wavefront 0 from the expert offsets (E <= kMaxExperts)
+  if (wv == 0) {
+    int carry = 0;
+    for (int c0 = 0; c0 < a.E; c0 += 64) {
+      const int e = c0 + lane;
+      const int tv = e < a.E ? (a.offsets[e + 1] - a.offsets[e] + BM - 1) / BM : 0;
+      int inc = tv;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(inc, o);
+        if (lane >= o) inc += u;
+      }
+      if (e < a.E) s_tiles[e] = carry + inc - tv;
+      carry += __shfl(inc, 63);
+    }
+    if (lane == 0) s_tiles[a.E] = carry;
+  }
+  __syncthreads();
+  if (mt >= s_tiles[a.E]) return;
   // largest expert whose first tile is <= mt (skips experts with no tiles)
   int lo = 0, hi = a.E - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (a.tile_offsets[mid] <= mt)
+    if (s_tiles[mid] <= mt)
       lo = mid;
     else
       hi = mid - 1;
   }
   const int e = lo;
-  const int m0 = a.offsets[e] + (mt - a.tile_offsets[e]) * BM;
+  const int m0 = a.offsets[e] + (mt - s_tiles[e]) * BM;
   const int mcnt = min(BM, a.offsets[e + 1] - m0);
   const int n0 = blockIdx.x * (DUAL ? BN : 2 * BN);
   const int n1 = DUAL ? n0 : n0 + BN;  // first row of the second weight tile

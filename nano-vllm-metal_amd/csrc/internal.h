@@ -17,8 +17,7 @@ struct GroupedArgs {
   int64_t act_ld;
   const int32_t *a_map;
   int a_div;
-  const int32_t *offsets;       // [E+1] slot ranges per expert
-  const int32_t *tile_offsets;  // [E+1] prefill m-tile ranges per expert
+  const int32_t *offsets;  // [E+1] slot ranges per expert
   const uint32_t *w0;
   const uint16_t *s0, *b0;
   const uint32_t *w1;
@@ -39,10 +38,11 @@ hipError_t launch_route_finalize(int dtype, const double *partial, int splits, i
                                  int64_t E, int k, int norm, void *probs, int32_t *ids,
                                  void *scores, hipStream_t st);
 
-// Dispatch: counting sort of ids into expert order; tile_offsets (optional)
-// receives the prefix sum of ceil(count/bm).
+constexpr int kMaxExperts = 512;
+
+// Dispatch: stable counting sort of ids into expert order.
 hipError_t launch_dispatch(const int32_t *ids, int64_t n, int64_t E, int32_t *offsets,
-                           int32_t *sorted, int32_t *tile_offsets, int bm, hipStream_t st);
+                           int32_t *sorted, hipStream_t st);
 
 // Grouped products.  dual = fused gate/up with SwiGLU epilogue.
 hipError_t launch_gemv(int dtype, bool dual, const GroupedArgs &a, hipStream_t st);

@@ -39,6 +39,10 @@ SIGNATURES = {
     "nvm_grouped_linear_workspace_size": [_I64, _I64, _I64, _I64, ctypes.POINTER(_SZ)],
     "nvm_grouped_expert_linear": [_P, _I64, _I64, _P, _P, _P, _I64, _I64, _I, _I, _P, _I, _P, _I, _P, _SZ, _P],
     "nvm_moe_workspace_size": [_I64, _I64, _I64, _I64, _I, ctypes.POINTER(_SZ)],
+    "nvm_moe_expert_gateup": [_P, _I64, _I64, _I64, _I64, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P,
+                              _P, _P, _P, _I, _P],
+    "nvm_moe_expert_down": [_P, _I64, _I64, _I64, _I64, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P],
+    "nvm_moe_combine": [_P, _P, _I64, _I, _I64, _I, _P, _P],
     "nvm_moe_forward": [_P, _I64, _I64, _I64, _I64, _I, _I, _I, _I, _I,
                         _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                         _P, _P, _P, _I, _P, _SZ, _P],
