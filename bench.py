@@ -358,6 +358,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain 256 MiB device copy (calibrates HBM byte counters)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -371,6 +373,13 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     H, E, I, k, gs = (SHAPE[n] for n in ("H", "E", "I", "k", "gs"))
+    if args.copy_probe:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     log(f"[bench] building {args.layers} layers of 30B-A3B MoE weights")
     layers = make_layers(args.layers, H, E, I, gs, dev)
 

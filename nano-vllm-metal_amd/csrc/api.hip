@@ -40,6 +40,8 @@ int fail(int code, const char *fmt, ...) {
 
 constexpr int64_t kMaxExperts = nvm::kMaxExperts;
 constexpr int kMaxTopK = 64;
+// the decode products stage 8 activation rows of length K in LDS
+constexpr int64_t kMaxProductK = 8192;
 
 // Bump allocator over the caller's workspace (256-byte aligned slices).
 struct Carve {
@@ -66,7 +68,7 @@ int check_quant(int group_size, int bits, int dtype) {
 bool use_decode(int regime, int64_t pairs, int64_t E) {
   if (regime == NVM_REGIME_DECODE) return true;
   if (regime == NVM_REGIME_PREFILL) return false;
-  return pairs <= 16 * E;  // up to 16 routed rows per expert on average
+  return pairs <= 8 * E;  // up to 8 routed rows per expert on average
 }
 
 // Shapes the expert products handle: K dims in whole 64-wide groups, output
@@ -85,6 +87,8 @@ int check_products(int64_t H, int64_t I, int64_t E, int top_k, int group_size, i
   NVM_SUPPORTED(top_k <= kMaxTopK, "moe: top_k at most %d", kMaxTopK);
   NVM_REQUIRE(regime >= NVM_REGIME_AUTO && regime <= NVM_REGIME_PREFILL, "moe: bad regime %d",
               regime);
+  NVM_SUPPORTED(H <= kMaxProductK && I <= kMaxProductK, "moe: H and I at most %lld",
+                (long long)kMaxProductK);
   return NVM_OK;
 }
 
@@ -102,7 +106,7 @@ MoeWs carve_moe(void *base, int64_t T, int64_t H, int64_t I, int64_t E, int k) {
   Carve c(base);
   MoeWs w;
   const int64_t N = T * k;
-  w.partial = c.take<double>((size_t)nvm::route_splits(T, H) * T * E);
+  w.partial = c.take<double>((size_t)nvm::route_splits(T, H, E) * T * E);
   w.ids = c.take<int32_t>(N);
   w.scores = c.take<uint16_t>(N);
   w.offsets = c.take<int32_t>(E + 1);
@@ -143,7 +147,7 @@ int nvm_quantized_matmul(const void *scales, const void *biases, int group_size,
   NVM_REQUIRE(N % group_size == 0, "quantized_matmul: N=%lld not divisible by group_size %d",
               (long long)N, group_size);
   if (M == 0) return NVM_OK;
-  NVM_TRY_HIP(nvm::launch_route_partial(dtype, a, M, N, b, scales, biases, K, group_size, 1,
+  NVM_TRY_HIP(nvm::launch_route_partial(dtype, a, M, N, b, scales, biases, K, group_size, true,
                                         nullptr, out, (hipStream_t)stream));
   return NVM_OK;
 }
@@ -151,7 +155,7 @@ int nvm_quantized_matmul(const void *scales, const void *biases, int group_size,
 int nvm_route_workspace_size(int64_t T, int64_t H, int64_t E, size_t *bytes) {
   NVM_REQUIRE(bytes, "route_workspace_size: null output");
   NVM_REQUIRE(T >= 0 && H > 0 && E > 0, "route_workspace_size: bad shape");
-  *bytes = sizeof(double) * (size_t)nvm::route_splits(T, H) * (size_t)T * (size_t)E;
+  *bytes = sizeof(double) * (size_t)nvm::route_splits(T, H, E) * (size_t)T * (size_t)E;
   return NVM_OK;
 }
 
@@ -173,9 +177,9 @@ int nvm_moe_route(const void *x, int64_t T, int64_t H, const uint32_t *wr, const
   nvm_route_workspace_size(T, H, E, &need);
   if (!workspace || workspace_bytes < need)
     return fail(NVM_ERR_WORKSPACE, "route: workspace of %zu bytes needed", need);
-  const int splits = nvm::route_splits(T, H);
+  const int splits = nvm::route_splits(T, H, E);
   hipStream_t st = (hipStream_t)stream;
-  NVM_TRY_HIP(nvm::launch_route_partial(dtype, x, T, H, wr, sr, br, E, group_size, splits,
+  NVM_TRY_HIP(nvm::launch_route_partial(dtype, x, T, H, wr, sr, br, E, group_size, false,
                                         (double *)workspace, nullptr, st));
   NVM_TRY_HIP(nvm::launch_route_finalize(dtype, (const double *)workspace, splits, T, E, top_k,
                                          norm_topk_prob, probs, ids, scores, st));
@@ -216,6 +220,7 @@ int nvm_grouped_expert_linear(const void *x, int64_t n, int64_t D, const uint32_
               (long long)D);
   NVM_REQUIRE(O % 16 == 0, "grouped_linear: output dim %lld must be a multiple of 16",
               (long long)O);
+  NVM_SUPPORTED(D <= kMaxProductK, "grouped_linear: D at most %lld", (long long)kMaxProductK);
   NVM_SUPPORTED(E <= kMaxExperts, "grouped_linear: at most %lld experts", (long long)kMaxExperts);
   if (n == 0) return NVM_OK;
   size_t need = 0;
@@ -230,6 +235,7 @@ int nvm_grouped_expert_linear(const void *x, int64_t n, int64_t D, const uint32_
   nvm::GroupedArgs g{};
   g.act = (const uint16_t *)x;
   g.act_ld = D;
+  g.act_rows = n;
   g.a_map = sorted;
   g.a_div = 1;
   g.offsets = offsets;
@@ -266,6 +272,7 @@ int nvm_moe_expert_gateup(const void *x, int64_t T, int64_t H, int64_t I, int64_
   nvm::GroupedArgs g{};
   g.act = (const uint16_t *)x;
   g.act_ld = H;
+  g.act_rows = T;
   g.a_map = sorted_pairs;
   g.a_div = top_k;
   g.offsets = expert_offsets;
@@ -299,6 +306,7 @@ int nvm_moe_expert_down(const void *h, int64_t n_pairs, int64_t H, int64_t I, in
   nvm::GroupedArgs d{};
   d.act = (const uint16_t *)h;
   d.act_ld = I;
+  d.act_rows = n_pairs;
   d.a_map = nullptr;
   d.a_div = 1;
   d.offsets = expert_offsets;
@@ -348,8 +356,8 @@ int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, i
   const int64_t N = T * top_k;
   hipStream_t st = (hipStream_t)stream;
 
-  const int splits = nvm::route_splits(T, H);
-  NVM_TRY_HIP(nvm::launch_route_partial(dtype, x, T, H, wr, sr, br, E, group_size, splits,
+  const int splits = nvm::route_splits(T, H, E);
+  NVM_TRY_HIP(nvm::launch_route_partial(dtype, x, T, H, wr, sr, br, E, group_size, false,
                                         ws.partial, nullptr, st));
   NVM_TRY_HIP(nvm::launch_route_finalize(dtype, ws.partial, splits, T, E, top_k, norm_topk_prob,
                                          nullptr, ids, scores, st));

@@ -149,4 +149,69 @@ __device__ __forceinline__ u32x4 nibble_pairs(uint32_t w) {
 __device__ __forceinline__ u32x4 ldg16(const void *p) { return *(const u32x4 *)p; }
 __device__ __forceinline__ u32x2 ldg8(const void *p) { return *(const u32x2 *)p; }
 
+// Raw buffer loads: a uniform descriptor (base, size in bytes) plus a 32-bit
+// per-lane byte offset and a uniform offset.  Reads at or beyond `bytes`
+// return zero, which the kernels use to mask lanes without branches.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kBufferFlags = 0x00020000u;  // raw 32-bit data format (gfx9 family)
+constexpr int kMaskedOffset = 0x7FFFFFF0;      // beyond every descriptor the kernels build
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                           (int)kBufferFlags);
+}
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ u32x2 bload8(rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
+__device__ __forceinline__ uint32_t bload4(rsrc_t r, int voff, int soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+__device__ __forceinline__ uint32_t bload2(rsrc_t r, int voff, int soff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+
+// Wavefront reductions: DPP butterflies inside each 16-lane row (quad_perm
+// [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror), then the four
+// row results combined from scalar readlanes.  The combination order is fixed,
+// so the result is the same in every lane and on every run.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint64_t lo = dpp_u32<CTRL>((uint32_t)u), hi = dpp_u32<CTRL>((uint32_t)(u >> 32));
+  return __builtin_bit_cast(double, lo | (hi << 32));
+}
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+  return __builtin_bit_cast(double, lo | (hi << 32));
+}
+
+template <class Op>
+__device__ __forceinline__ double wave_reduce_f64(double v, Op op) {
+  v = op(v, dpp_f64<0xB1>(v));
+  v = op(v, dpp_f64<0x4E>(v));
+  v = op(v, dpp_f64<0x141>(v));
+  v = op(v, dpp_f64<0x140>(v));
+  return op(op(readlane_f64(v, 0), readlane_f64(v, 16)), op(readlane_f64(v, 32), readlane_f64(v, 48)));
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));
+  v = max(v, dpp_u32<0x4E>(v));
+  v = max(v, dpp_u32<0x141>(v));
+  v = max(v, dpp_u32<0x140>(v));
+  const uint32_t a = max((uint32_t)__builtin_amdgcn_readlane((int)v, 0),
+                         (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
+  const uint32_t b = max((uint32_t)__builtin_amdgcn_readlane((int)v, 32),
+                         (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+  return max(a, b);
+}
+
 }  // namespace nvm

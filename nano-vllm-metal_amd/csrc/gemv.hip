@@ -14,11 +14,19 @@
 // which is the reference's w = q*s + b (metal/src/quantized_matmul.cpp:135).
 //
 // MFMA roles (16x16x32): A = activations [16 rows x 32 k], B = weights
-// [32 k x 16 output features], C[row][feature].  Lane l supplies A row l%16
-// and B column l%16 for k-slots 8*(l/16)..+7, and holds C rows 4*(l/16)..+3
-// of column l%16.  Within a 64-element group, lane group G = l/16 takes packed
-// words 2G (first MFMA) and 2G+1 (second MFMA): 8 bytes per lane per row,
-// 32 contiguous bytes per row across the four lane groups.
+// [32 k x 16 output features], C[row][feature].  Lane l = (c, G), c = l%16,
+// G = l/16, supplies A row c and B column c for k-slots 8G..8G+7 and holds C
+// rows 4G..4G+3 of column c.
+//
+// Memory shape: lane (c, G) loads 16 contiguous bytes (4 packed words) of
+// weight row c per load, so the four lane groups read 64 contiguous bytes of
+// each of 16 rows -- two quantisation groups.  Lane groups 0-1 then hold the
+// first group and 2-3 the second, so each word position feeds two MFMAs, one
+// whose activation operand is zero in lane groups 2-3 (first group) and one
+// zero in lane groups 0-1 (second group).  The activations of the block's
+// routed rows are staged once per block in LDS, already in the pair order of
+// nibble_pairs(), together with their 64-wide group sums; masked lanes read a
+// row of zeros, so the masking costs no arithmetic.
 #include "common.h"
 #include "internal.h"
 
@@ -26,133 +34,222 @@ namespace nvm {
 
 namespace {
 
-template <int DT, bool DUAL, int NT>
-__global__ __launch_bounds__(256) void gemv_kernel(const GroupedArgs a) {
+constexpr int GI = 4;  // 64-wide groups per pipeline stage: one 128-byte line per row
+
+// Scale/bias loads of one pipeline stage: 4 consecutive bf16/fp16 values
+// (group 64, rows a multiple of 4 groups long), 2 values (group 128), or one
+// value per group.
+enum { SB_PER_GROUP = 0, SB_VEC4 = 1, SB_VEC2 = 2 };
+
+// Routed rows staged per pass (MFMA rows CH..15 stay zero).  Experts with
+// more routed rows take further passes over their weights.
+constexpr int CH = 8;
+
+// LDS bytes of a block: CH+1 activation rows (CH routed rows + one of zeros)
+// of K/8+1 sixteen-byte chunks (the extra chunk staggers the banks of
+// consecutive rows), CH group sums per 64-wide group, and 512 bytes of slack
+// that a short last stage (K not a multiple of 256) may read past the end.
+__host__ __device__ constexpr int gemv_lds_bytes(int K) {
+  return (CH + 1) * (K / 8 + 1) * 16 + (K / 64) * CH * 4 + 512;
+}
+constexpr int kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
+
+template <int DT, bool DUAL, int NT, int SB>
+__global__ __launch_bounds__(256, 3) void gemv_kernel(const GroupedArgs a) {
   using A = Act<DT>;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  constexpr int NM = DUAL ? 2 : 1;
+  extern __shared__ __attribute__((aligned(16))) u32x4 xl[];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int e = blockIdx.y;
-  const int r0 = (blockIdx.x * (blockDim.x >> 6) + wv) * (16 * NT);
-  if (r0 >= a.R) return;
   const int nb = a.offsets[e], ne = a.offsets[e + 1];
-  if (nb >= ne) return;
+  const int rb = blockIdx.x * (4 * 16 * NT);
+  if (nb >= ne || rb >= a.R) return;  // uniform over the block
+  const int r0 = rb + wv * 16 * NT;
+  const bool wave_rows = r0 < a.R;
 
   const int col = lane & 15, G = lane >> 4;
   const int KW = a.K >> 3, KG = a.K >> 6, GPR = a.K / a.gs;
-  const int gsh = a.gs == 128 ? 1 : 0;  // 64-groups per scale group: 1 or 2
+  const int gsh = a.gs == 128 ? 1 : 0;
+  const int pitch = KW + 1;  // LDS row pitch in 16-byte chunks
+  const int zero_row = CH * pitch;
+  float *sxl = (float *)(xl + (CH + 1) * pitch);  // [KG][CH]
 
-  const uint32_t *wp0[NT], *wp1[NT];
-  const uint16_t *sp0[NT], *bp0[NT], *sp1[NT], *bp1[NT];
+  for (int i = tid; i < pitch; i += blockDim.x) xl[zero_row + i] = u32x4{0, 0, 0, 0};
+
+  rsrc_t wr[NM], sr[NM], br[NM];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    const int64_t eo = (int64_t)e * a.R;
+    wr[m] = make_rsrc((m ? a.w1 : a.w0) + eo * KW, (uint32_t)(a.R * KW * 4));
+    sr[m] = make_rsrc((m ? a.s1 : a.s0) + eo * GPR, (uint32_t)(a.R * GPR * 2));
+    br[m] = make_rsrc((m ? a.b1 : a.b0) + eo * GPR, (uint32_t)(a.R * GPR * 2));
+  }
+  int wo[NT], so[NT];
   bool tv[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     tv[t] = r0 + 16 * t < a.R;
-    const int64_t row = (int64_t)e * a.R + (tv[t] ? r0 + 16 * t + col : 0);
-    wp0[t] = a.w0 + row * KW + 2 * G;
-    sp0[t] = a.s0 + row * GPR;
-    bp0[t] = a.b0 + row * GPR;
-    if (DUAL) {
-      wp1[t] = a.w1 + row * KW + 2 * G;
-      sp1[t] = a.s1 + row * GPR;
-      bp1[t] = a.b1 + row * GPR;
-    }
+    const int row = r0 + 16 * t + col;
+    wo[t] = tv[t] ? (row * KW + 4 * G) * 4 : kMaskedOffset;
+    so[t] = tv[t] ? row * GPR * 2 : kMaskedOffset;
   }
 
-  for (int nc = nb; nc < ne; nc += 16) {
-    const int cnt = min(16, ne - nc);
-    const bool has = col < cnt;
-    const int arow = has ? (a.a_map ? a.a_map[nc + col] / a.a_div : nc + col) : 0;
-    const uint16_t *ap = a.act + (int64_t)arow * a.act_ld + 16 * G;
-
-    f32x4 o0[NT], o1[NT];
+  // one pipeline stage = 4 groups: two 16-byte loads per (matrix, row tile)
+  // and packed scales/biases (value of group gi: half (gi & 1) of dword gi >> 1)
+  struct Stage {
+    u32x4 q[NM][NT][2];
+    u32x2 s[NM][NT], b[NM][NT];
+  };
+  auto load = [&](int st_idx, Stage &st) {
+    const int ws = __builtin_amdgcn_readfirstlane(128 * st_idx);
+    const int ss = __builtin_amdgcn_readfirstlane(2 * GI * st_idx);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      o0[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-      o1[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-
-    // register double buffer: loads for group g+1 are issued before the
-    // matrix work of group g
-    u32x4 xa = {0, 0, 0, 0}, xb = {0, 0, 0, 0};
-    u32x2 q0[NT], q1[NT];
-    uint16_t s0v[NT], b0v[NT], s1v[NT], b1v[NT];
-    auto load = [&](int g, u32x4 &la, u32x4 &lb, u32x2 *lq0, u32x2 *lq1, uint16_t *ls0,
-                    uint16_t *lb0, uint16_t *ls1, uint16_t *lb1) {
-      if (has) {
-        la = ldg16(ap + 64 * g);
-        lb = ldg16(ap + 64 * g + 8);
-      }
-      const int sg = g >> gsh;
+    for (int m = 0; m < NM; ++m)
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        if (!tv[t]) continue;
-        lq0[t] = ldg8(wp0[t] + 8 * g);
-        ls0[t] = sp0[t][sg];
-        lb0[t] = bp0[t][sg];
-        if (DUAL) {
-          lq1[t] = ldg8(wp1[t] + 8 * g);
-          ls1[t] = sp1[t][sg];
-          lb1[t] = bp1[t][sg];
+        st.q[m][t][0] = bload16(wr[m], wo[t], ws);
+        st.q[m][t][1] = bload16(wr[m], wo[t] + 64, ws);
+        if constexpr (SB == SB_VEC4) {
+          st.s[m][t] = bload8(sr[m], so[t], ss);
+          st.b[m][t] = bload8(br[m], so[t], ss);
+        } else if constexpr (SB == SB_VEC2) {
+          const uint32_t sv = bload4(sr[m], so[t], ss >> 1);
+          const uint32_t bv = bload4(br[m], so[t], ss >> 1);
+          st.s[m][t] = u32x2{(sv & 0xFFFFu) * 0x10001u, (sv >> 16) * 0x10001u};
+          st.b[m][t] = u32x2{(bv & 0xFFFFu) * 0x10001u, (bv >> 16) * 0x10001u};
+        } else {
+          uint32_t sv[GI], bv[GI];
+#pragma unroll
+          for (int gi = 0; gi < GI; ++gi) {
+            sv[gi] = bload2(sr[m], so[t] + 2 * ((GI * st_idx + gi) >> gsh), 0);
+            bv[gi] = bload2(br[m], so[t] + 2 * ((GI * st_idx + gi) >> gsh), 0);
+          }
+          st.s[m][t] = u32x2{sv[0] | (sv[1] << 16), sv[2] | (sv[3] << 16)};
+          st.b[m][t] = u32x2{bv[0] | (bv[1] << 16), bv[2] | (bv[3] << 16)};
         }
+      }
+  };
+
+  for (int nc = nb; nc < ne; nc += CH) {
+    const int cnt = min(CH, ne - nc);
+    __syncthreads();  // the previous token chunk is done with the LDS rows
+    // stage the routed activation rows (pair order) and their group sums
+    for (int it = tid; it < cnt * KW; it += blockDim.x) {
+      const int c = it / KW, ch = it - c * KW;
+      const int arow = a.a_map ? a.a_map[nc + c] / a.a_div : nc + c;
+      const u32x4 v = ldg16(a.act + (int64_t)arow * a.act_ld + 8 * ch);
+      xl[c * pitch + ch] = pair_order(v);
+      float sx = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sx = A::dot2(v[i], A::kOne2, sx);
+      // 8 consecutive items (lanes) form one 64-wide group
+      sx += __shfl_xor(sx, 1);
+      sx += __shfl_xor(sx, 2);
+      sx += __shfl_xor(sx, 4);
+      if ((ch & 7) == 0) sxl[(ch >> 3) * CH + c] = sx;
+    }
+    __syncthreads();
+    if (!wave_rows) continue;
+
+    const bool tok_ok = col < cnt;
+    const int lo_base = (tok_ok && G < 2) ? col * pitch + 4 * G : zero_row + 4 * G;
+    const int hi_base = (tok_ok && G >= 2) ? col * pitch + 4 * G : zero_row + 4 * G;
+
+    f32x4 o[NM][NT];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) o[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // ng = valid groups of the stage (GI except in a short last stage)
+    auto compute = [&](int st_idx, const Stage &st, int ng) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (2 * j >= ng) break;
+        const bool has_b = 2 * j + 1 < ng;
+        const int cbase = 32 * st_idx + 16 * j;
+        f32x4 acc_a[NM][NT], acc_b[NM][NT];
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            acc_a[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            acc_b[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const u32x4 alo = xl[lo_base + cbase + k];
+          const u32x4 ahi = xl[hi_base + cbase + k];
+#pragma unroll
+          for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+              if (!tv[t]) continue;
+              const u32x4 bq = nibble_pairs<DT>(st.q[m][t][j][k]);
+              acc_a[m][t] = A::mfma16(alo, bq, acc_a[m][t]);
+              acc_b[m][t] = A::mfma16(ahi, bq, acc_b[m][t]);
+            }
+        }
+        // group sums of the lane's C rows 4G..4G+3 (rows >= CH are never stored)
+        const int ga = GI * st_idx + 2 * j;
+        const int gq = min(4 * G, CH - 4);
+        const f32x4 sxa = *(const f32x4 *)(sxl + ga * CH + gq);
+        const f32x4 sxb = *(const f32x4 *)(sxl + (ga + 1) * CH + gq);
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            if (!tv[t]) continue;
+            const uint32_t sd = st.s[m][t][j], bd = st.b[m][t][j];
+            const float s0 = A::lo(sd), b0 = A::lo(bd);
+            const float bp0 = fmaf(-A::kMagic, s0, b0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) o[m][t][v] = fmaf(s0, acc_a[m][t][v], fmaf(bp0, sxa[v], o[m][t][v]));
+            if (has_b) {
+              const float s1 = A::hi(sd), b1 = A::hi(bd);
+              const float bp1 = fmaf(-A::kMagic, s1, b1);
+#pragma unroll
+              for (int v = 0; v < 4; ++v)
+                o[m][t][v] = fmaf(s1, acc_b[m][t][v], fmaf(bp1, sxb[v], o[m][t][v]));
+            }
+          }
       }
     };
-    load(0, xa, xb, q0, q1, s0v, b0v, s1v, b1v);
 
-    for (int g = 0; g < KG; ++g) {
-      const u32x4 ca = xa, cb = xb;
-      u32x2 cq0[NT], cq1[NT];
-      uint16_t cs0[NT], cb0[NT], cs1[NT], cb1[NT];
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        cq0[t] = q0[t];
-        cs0[t] = s0v[t];
-        cb0[t] = b0v[t];
-        if (DUAL) {
-          cq1[t] = q1[t];
-          cs1[t] = s1v[t];
-          cb1[t] = b1v[t];
-        }
-      }
-      if (g + 1 < KG) load(g + 1, xa, xb, q0, q1, s0v, b0v, s1v, b1v);
-
-      const u32x4 A0 = pair_order(ca), A1 = pair_order(cb);
-      // sum of this lane's 16 activations, then of the row's 64 (4 lane groups)
-      float sx = 0.f;
-      sx = A::dot2(ca.x, A::kOne2, sx);
-      sx = A::dot2(ca.y, A::kOne2, sx);
-      sx = A::dot2(ca.z, A::kOne2, sx);
-      sx = A::dot2(ca.w, A::kOne2, sx);
-      sx = A::dot2(cb.x, A::kOne2, sx);
-      sx = A::dot2(cb.y, A::kOne2, sx);
-      sx = A::dot2(cb.z, A::kOne2, sx);
-      sx = A::dot2(cb.w, A::kOne2, sx);
-      sx += __shfl_xor(sx, 16);
-      sx += __shfl_xor(sx, 32);
-      float sxv[4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) sxv[v] = __shfl(sx, 4 * G + v);
-
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        if (!tv[t]) continue;
-        {
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-          acc = A::mfma16(A0, nibble_pairs<DT>(cq0[t].x), acc);
-          acc = A::mfma16(A1, nibble_pairs<DT>(cq0[t].y), acc);
-          const float s = A::to_f32(cs0[t]), b = A::to_f32(cb0[t]);
-          const float bp = fmaf(-A::kMagic, s, b);
-#pragma unroll
-          for (int v = 0; v < 4; ++v) o0[t][v] = fmaf(s, acc[v], fmaf(bp, sxv[v], o0[t][v]));
-        }
-        if (DUAL) {
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-          acc = A::mfma16(A0, nibble_pairs<DT>(cq1[t].x), acc);
-          acc = A::mfma16(A1, nibble_pairs<DT>(cq1[t].y), acc);
-          const float s = A::to_f32(cs1[t]), b = A::to_f32(cb1[t]);
-          const float bp = fmaf(-A::kMagic, s, b);
-#pragma unroll
-          for (int v = 0; v < 4; ++v) o1[t][v] = fmaf(s, acc[v], fmaf(bp, sxv[v], o1[t][v]));
-        }
-      }
+    // Three stage buffers in rotation keep two stages of weights in flight
+    // while one is multiplied; nothing is copied between buffers.  Every pass
+    // of the main loop issues the same loads, which lets the compiler wait
+    // only for the stage about to be used.  Wavefronts start at different
+    // stages of their rows so that concurrent wavefronts do not sweep the
+    // same column offsets (and memory channels) in lockstep.
+    const int NS = (KG + GI - 1) / GI;
+    const int rot = __builtin_amdgcn_readfirstlane(
+        (int)((blockIdx.x * (blockDim.x >> 6) + wv + 3u * blockIdx.y) % (unsigned)NS));
+    auto st_at = [&](int i) {
+      const int st = rot + i;
+      return st >= NS ? st - NS : st;
+    };
+    auto run = [&](int i, const Stage &st) { compute(st_at(i), st, min(GI, KG - GI * st_at(i))); };
+    Stage sa, sb, sc;
+    load(st_at(0), sa);
+    if (NS > 1) load(st_at(1), sb);
+    int i = 0;
+    for (; i + 4 < NS; i += 3) {
+      load(st_at(i + 2), sc);
+      run(i, sa);
+      load(st_at(i + 3), sa);
+      run(i + 1, sb);
+      load(st_at(i + 4), sb);
+      run(i + 2, sc);
+    }
+    // 1 to 4 stages remain: sa holds stage i, sb stage i + 1
+    if (i + 2 < NS) load(st_at(i + 2), sc);
+    run(i, sa);
+    if (i + 1 < NS) {
+      if (i + 3 < NS) load(st_at(i + 3), sa);
+      run(i + 1, sb);
+      if (i + 2 < NS) run(i + 2, sc);
+      if (i + 3 < NS) run(i + 3, sa);
     }
 
 #pragma unroll
@@ -169,11 +266,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GroupedArgs a) {
         if (DUAL) {
           // reference rounding points: gate and up outputs are act tensors,
           // silu(gate) * up is rounded once more
-          const float gv = round_act<DT>(o0[t][v]);
-          const float uv = round_act<DT>(o1[t][v]);
+          const float gv = round_act<DT>(o[0][t][v]);
+          const float uv = round_act<DT>(o[NM - 1][t][v]);
           r = A::from_f32(gv / (1.0f + __expf(-gv)) * uv);
         } else {
-          r = A::from_f32(o0[t][v]);
+          r = A::from_f32(o[0][t][v]);
         }
         a.out[orow * a.out_ld + rowc] = r;
       }
@@ -181,16 +278,41 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GroupedArgs a) {
   }
 }
 
-template <int DT>
-hipError_t launch_t(bool dual, const GroupedArgs &a, hipStream_t st) {
-  constexpr int NT = 2, WAVES = 4;
+template <int DT, bool DUAL, int NT>
+hipError_t launch_nt(const GroupedArgs &a, int sb_mode, hipStream_t st) {
+  constexpr int WAVES = 4;
   const int rows_per_block = 16 * NT * WAVES;
   dim3 grid((unsigned)((a.R + rows_per_block - 1) / rows_per_block), (unsigned)a.E);
-  if (dual)
-    hipLaunchKernelGGL((gemv_kernel<DT, true, NT>), grid, dim3(64 * WAVES), 0, st, a);
+  const size_t lds = gemv_lds_bytes(a.K);
+  if (lds > (size_t)kMaxLds) return hipErrorInvalidValue;
+  // allow dynamic LDS beyond the 64 KiB default (once per instantiation)
+  static const hipError_t attr[3] = {
+      hipFuncSetAttribute((const void *)gemv_kernel<DT, DUAL, NT, SB_PER_GROUP>,
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds),
+      hipFuncSetAttribute((const void *)gemv_kernel<DT, DUAL, NT, SB_VEC4>,
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds),
+      hipFuncSetAttribute((const void *)gemv_kernel<DT, DUAL, NT, SB_VEC2>,
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds)};
+  for (hipError_t e : attr)
+    if (e != hipSuccess) return e;
+  if (sb_mode == SB_VEC4)
+    hipLaunchKernelGGL((gemv_kernel<DT, DUAL, NT, SB_VEC4>), grid, dim3(64 * WAVES), lds, st, a);
+  else if (sb_mode == SB_VEC2)
+    hipLaunchKernelGGL((gemv_kernel<DT, DUAL, NT, SB_VEC2>), grid, dim3(64 * WAVES), lds, st, a);
   else
-    hipLaunchKernelGGL((gemv_kernel<DT, false, NT>), grid, dim3(64 * WAVES), 0, st, a);
+    hipLaunchKernelGGL((gemv_kernel<DT, DUAL, NT, SB_PER_GROUP>), grid, dim3(64 * WAVES), lds,
+                       st, a);
   return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_t(bool dual, const GroupedArgs &a, hipStream_t st) {
+  const int gpr = a.K / a.gs;
+  const int sb_mode = (a.gs == 64 && gpr % 4 == 0)    ? SB_VEC4
+                      : (a.gs == 128 && gpr % 2 == 0) ? SB_VEC2
+                                                      : SB_PER_GROUP;
+  // gate/up: one 16-row tile of both matrices per wavefront; down: two tiles
+  return dual ? launch_nt<DT, true, 1>(a, sb_mode, st) : launch_nt<DT, false, 2>(a, sb_mode, st);
 }
 
 }  // namespace

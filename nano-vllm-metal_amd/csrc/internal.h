@@ -15,6 +15,7 @@ namespace nvm {
 struct GroupedArgs {
   const uint16_t *act;
   int64_t act_ld;
+  int64_t act_rows;  // rows of `act` (bounds of the activation buffer)
   const int32_t *a_map;
   int a_div;
   const int32_t *offsets;  // [E+1] slot ranges per expert
@@ -28,11 +29,11 @@ struct GroupedArgs {
   int64_t out_ld;
 };
 
-// Router.  Partial float64 logits over an H-split, then per-token finalise.
-int route_splits(int64_t T, int64_t H);
-int route_experts_per_block(int64_t T);
+// Router.  Partial float64 logits over hidden splits, then per-token finalise.
+// With final_act the logits are rounded and stored as act [T, E] directly.
+int route_splits(int64_t T, int64_t H, int64_t E);
 hipError_t launch_route_partial(int dtype, const void *x, int64_t T, int64_t H, const uint32_t *wr,
-                                const void *sr, const void *br, int64_t E, int gs, int splits,
+                                const void *sr, const void *br, int64_t E, int gs, bool final_act,
                                 double *partial, void *final_out, hipStream_t st);
 hipError_t launch_route_finalize(int dtype, const double *partial, int splits, int64_t T,
                                  int64_t E, int k, int norm, void *probs, int32_t *ids,

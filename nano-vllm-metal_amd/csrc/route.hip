@@ -5,8 +5,9 @@
 //
 // Every value the reference materialises in the activation dtype (logits,
 // probabilities, scores) is produced here as the correctly rounded value of
-// the exact mathematical result: the dot products and the softmax run in
-// float64 and are rounded once, directly from float64.  A float64 sum of at
+// the exact mathematical result: the dot products (on the float64 matrix
+// cores) and the softmax run in float64 and are rounded once, directly from
+// float64.  A float64 sum of at
 // most a few thousand products of a bf16/fp16 activation and an fp32-exact
 // weight is within ~2^-40 relative of the exact sum, so the rounded logits,
 // and with them the top-k ids, do not depend on summation order.
@@ -17,101 +18,122 @@ namespace nvm {
 
 namespace {
 
-constexpr int kRouteChunk = 256;  // H elements staged per LDS pass
+typedef double f64x4 __attribute__((ext_vector_type(4)));
 
-// part[z][t][e] (or the final act logits when `fin`) for tokens of this block
-// (one per lane), experts [e0, e0+EG) and hidden range of split z.
-template <int DT, int EG>
-__global__ void route_partial_kernel(const uint16_t *__restrict__ x, int T, int H,
-                                     const uint32_t *__restrict__ wr,
-                                     const uint16_t *__restrict__ sr,
-                                     const uint16_t *__restrict__ br, int E, int gs, int HR,
-                                     double *__restrict__ part, uint16_t *__restrict__ fin) {
-  extern __shared__ double wlds[];  // [EG][kRouteChunk]
-  const int tid = threadIdx.x;
-  const int t = blockIdx.x * blockDim.x + tid;
-  const int e0 = blockIdx.y * EG;
-  const int z = blockIdx.z;
-  const int h_begin = z * HR;
-  const int words_per_row = H / 8;
-  const int groups_per_row = H / gs;
+// Partial float64 logits on the matrix cores (v_mfma_f64_16x16x4_f64).
+//
+// One wavefront owns a tile of 16 tokens x (16*EB) experts over the hidden
+// range [z*KR, (z+1)*KR).  Per 32-wide hidden chunk, lane (c, G) (c = l%16,
+// G = l/16) supplies activations x[t0+c][k] and dequantised weights
+// w[e0+c][k] = q*s + b (exact in float64) for k = chunk + 8G + m, m = 0..7, so
+// MFMA m covers hidden columns {chunk + m, +8, +16, +24}: every column of the
+// chunk exactly once, 8 consecutive bf16/fp16 values and one packed word per
+// lane.  The D fragment of the float64 MFMA is row-interleaved: element i of
+// lane (c, G) is token t0+G+4i of expert e0+c.
+template <int DT, int EB, bool SB_VEC>
+__global__ __launch_bounds__(256) void route_mfma_kernel(
+    const uint16_t *__restrict__ x, int T, int H, const uint32_t *__restrict__ wr,
+    const uint16_t *__restrict__ sr, const uint16_t *__restrict__ br, int E, int gs, int KR,
+    int n_tt, int n_eb, int splits, double *__restrict__ part,
+    uint16_t *__restrict__ fin) {
+  using A = Act<DT>;
+  constexpr int NC = 8;  // 32-wide chunks per batch; all loads of a batch are in flight together
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (item >= n_tt * n_eb * splits) return;
+  const int tt = item % n_tt;
+  const int eb = (item / n_tt) % n_eb;
+  const int z = item / (n_tt * n_eb);
+  const int col = lane & 15, G = lane >> 4;
+  const int t = tt * 16 + col;
+  const int k_begin = z * KR;
+  const int HW = H / 8, GPR = H / gs;
 
-  double acc[EG];
+  const rsrc_t xr = make_rsrc(x, (uint32_t)((int64_t)T * H * 2));
+  const rsrc_t wrr = make_rsrc(wr, (uint32_t)((int64_t)E * HW * 4));
+  const rsrc_t srr = make_rsrc(sr, (uint32_t)((int64_t)E * GPR * 2));
+  const rsrc_t brr = make_rsrc(br, (uint32_t)((int64_t)E * GPR * 2));
+  // lanes of tokens >= T or experts >= E read zeros
+  const int xo = t < T ? (t * H + k_begin + 8 * G) * 2 : kMaskedOffset;
+  int wo[EB], so[EB];
+  bool e_ok[EB];
 #pragma unroll
-  for (int e = 0; e < EG; ++e) acc[e] = 0.0;
+  for (int b = 0; b < EB; ++b) {
+    const int e = (eb * EB + b) * 16 + col;
+    e_ok[b] = e < E;
+    wo[b] = e_ok[b] ? (e * HW + k_begin / 8 + G) * 4 : kMaskedOffset;
+    so[b] = e_ok[b] ? e * GPR * 2 : kMaskedOffset;
+  }
 
-  const uint16_t *xrow = x + (int64_t)(t < T ? t : 0) * H;
-
-  for (int c0 = 0; c0 < HR; c0 += kRouteChunk) {
-    const int len = min(kRouteChunk, HR - c0);
-    const int wpr = len / 8;  // words per expert in this chunk
-    __syncthreads();
-    for (int idx = tid; idx < EG * wpr; idx += blockDim.x) {
-      const int e = idx / wpr, wj = idx - e * wpr;
-      const int ge = e0 + e;
-      double *dst = wlds + e * kRouteChunk + wj * 8;
-      if (ge < E) {
-        const int col = h_begin + c0 + wj * 8;
-        const uint32_t q = wr[(int64_t)ge * words_per_row + col / 8];
-        const int g = col / gs;
-        const double s = (double)Act<DT>::to_f32(sr[(int64_t)ge * groups_per_row + g]);
-        const double b = (double)Act<DT>::to_f32(br[(int64_t)ge * groups_per_row + g]);
+  f64x4 acc[EB];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dst[j] = fma((double)((q >> (4 * j)) & 0xFu), s, b);
+  for (int b = 0; b < EB; ++b) acc[b] = f64x4{0.0, 0.0, 0.0, 0.0};
+
+  for (int kb = 0; kb < KR; kb += 32 * NC) {
+    const int kbs = __builtin_amdgcn_readfirstlane(kb);
+    // group of chunk c for every lane: (k_begin + kb)/gs + c*32/gs
+    const int g0 = (k_begin + kbs) / gs;
+    u32x4 xv[NC];
+    uint32_t qv[EB][NC];
+    // packed scales/biases: the 16-bit value of group i is half (i & 1) of dword i >> 1
+    u32x2 sv[EB], bv[EB];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) xv[c] = bload16(xr, xo + 64 * c, 2 * kbs);
+#pragma unroll
+    for (int b = 0; b < EB; ++b) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) qv[b][c] = bload4(wrr, wo[b] + 16 * c, kbs / 2);
+      if constexpr (SB_VEC) {
+        sv[b] = bload8(srr, so[b], 2 * g0);
+        bv[b] = bload8(brr, so[b], 2 * g0);
       } else {
+        uint32_t s4[4], b4[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dst[j] = 0.0;
+        for (int i = 0; i < 4; ++i) {
+          s4[i] = bload2(srr, so[b] + 2 * i, 2 * g0);
+          b4[i] = bload2(brr, so[b] + 2 * i, 2 * g0);
+        }
+        sv[b] = u32x2{s4[0] | (s4[1] << 16), s4[2] | (s4[3] << 16)};
+        bv[b] = u32x2{b4[0] | (b4[1] << 16), b4[2] | (b4[3] << 16)};
       }
     }
-    __syncthreads();
-    if (t < T) {
-      const uint16_t *xp = xrow + h_begin + c0;
-      for (int h = 0; h < len; h += 8) {
-        const u32x4 xv = ldg16(xp + h);
-        double xd[8];
-        xd[0] = Act<DT>::lo(xv.x);
-        xd[1] = Act<DT>::hi(xv.x);
-        xd[2] = Act<DT>::lo(xv.y);
-        xd[3] = Act<DT>::hi(xv.y);
-        xd[4] = Act<DT>::lo(xv.z);
-        xd[5] = Act<DT>::hi(xv.z);
-        xd[6] = Act<DT>::lo(xv.w);
-        xd[7] = Act<DT>::hi(xv.w);
 #pragma unroll
-        for (int e = 0; e < EG; ++e) {
-          const double *w = wlds + e * kRouteChunk + h;
+    for (int c = 0; c < NC; ++c) {
+      if (kb + 32 * c >= KR) break;
+      double xd[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) acc[e] = fma(xd[j], w[j], acc[e]);
+      for (int i = 0; i < 4; ++i) {
+        xd[2 * i] = (double)A::lo(xv[c][i]);
+        xd[2 * i + 1] = (double)A::hi(xv[c][i]);
+      }
+      const int gi = (32 * c) / gs;  // 0..3 (group 64) or 0..1 (group 128)
+#pragma unroll
+      for (int b = 0; b < EB; ++b) {
+        const uint32_t sd = sv[b][gi >> 1], bd = bv[b][gi >> 1];
+        const double s = (double)((gi & 1) ? A::hi(sd) : A::lo(sd));
+        const double bb = (double)((gi & 1) ? A::hi(bd) : A::lo(bd));
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          const double w = fma((double)((qv[b][c] >> (4 * m)) & 0xFu), s, bb);
+          acc[b] = __builtin_amdgcn_mfma_f64_16x16x4f64(xd[m], w, acc[b], 0, 0, 0);
         }
       }
     }
   }
-  if (t >= T) return;
 #pragma unroll
-  for (int e = 0; e < EG; ++e) {
-    const int ge = e0 + e;
-    if (ge >= E) break;
-    if (fin)
-      fin[(int64_t)t * E + ge] = act_from_f64<DT>(acc[e]);
-    else
-      part[((int64_t)z * T + t) * E + ge] = acc[e];
+  for (int b = 0; b < EB; ++b) {
+    const int e = (eb * EB + b) * 16 + col;
+    if (!e_ok[b]) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tok = tt * 16 + G + 4 * i;
+      if (tok >= T) continue;
+      if (fin)
+        fin[(int64_t)tok * E + e] = act_from_f64<DT>(acc[b][i]);
+      else
+        part[((int64_t)z * T + tok) * E + e] = acc[b][i];
+    }
   }
-}
-
-__device__ __forceinline__ double wave_max(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o));
-  return v;
-}
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o));
-  return v;
 }
 
 constexpr int kMaxExpertSlots = 8;  // experts per lane: E <= 512
@@ -140,7 +162,7 @@ __global__ __launch_bounds__(256) void route_finalize_kernel(
       mloc = fmax(mloc, lg[j]);
     }
   }
-  const double m = wave_max(mloc);
+  const double m = wave_reduce_f64(mloc, [](double a, double b) { return fmax(a, b); });
   double p[kMaxExpertSlots];
   double sloc = 0.0;
 #pragma unroll
@@ -149,7 +171,7 @@ __global__ __launch_bounds__(256) void route_finalize_kernel(
     p[j] = (e < E) ? exp(lg[j] - m) : 0.0;
     sloc += p[j];
   }
-  const double sum = wave_sum(sloc);
+  const double sum = wave_reduce_f64(sloc, [](double a, double b) { return a + b; });
   uint32_t key[kMaxExpertSlots];
 #pragma unroll
   for (int j = 0; j < kMaxExpertSlots; ++j) {
@@ -194,44 +216,72 @@ __global__ __launch_bounds__(256) void route_finalize_kernel(
   }
 }
 
-template <int DT, int EG>
-hipError_t launch_partial_t(const void *x, int64_t T, int64_t H, const uint32_t *wr,
-                            const void *sr, const void *br, int64_t E, int gs, int splits,
-                            double *partial, void *fin, hipStream_t st) {
-  const int waves = (int)std::min<int64_t>(4, (T + 63) / 64);
-  const int threads = 64 * waves;
-  dim3 grid((unsigned)((T + threads - 1) / threads), (unsigned)((E + EG - 1) / EG),
-            (unsigned)splits);
-  const size_t lds = sizeof(double) * EG * kRouteChunk;
-  hipLaunchKernelGGL((route_partial_kernel<DT, EG>), grid, dim3(threads), lds, st,
-                     (const uint16_t *)x, (int)T, (int)H, wr, (const uint16_t *)sr,
-                     (const uint16_t *)br, (int)E, gs, (int)(H / splits), partial,
-                     (uint16_t *)fin);
+struct RoutePlan {
+  int eb, n_tt, n_eb, splits;
+};
+
+// Work split of the router: expert tiles per wavefront and hidden splits
+// chosen so that roughly 2048 wavefronts share the work.
+RoutePlan route_plan(int64_t T, int64_t H, int64_t E) {
+  RoutePlan p;
+  const int64_t n_tt = (T + 15) / 16;
+  p.eb = (T >= 256 && E >= 64) ? 4 : 1;
+  p.n_tt = (int)n_tt;
+  p.n_eb = (int)((E + 16 * p.eb - 1) / (16 * p.eb));
+  p.splits = 1;
+  // hidden slices of at least 256 columns keep the finalise pass short
+  const int64_t chunks = H / 32;
+  while (p.splits * 2 <= chunks / 8 && chunks % (p.splits * 2) == 0 &&
+         n_tt * p.n_eb * p.splits * 2 <= 2048)
+    p.splits *= 2;
+  return p;
+}
+
+template <int DT, int EB>
+hipError_t launch_mfma_t(const void *x, int64_t T, int64_t H, const uint32_t *wr, const void *sr,
+                         const void *br, int64_t E, int gs, const RoutePlan &p, double *partial,
+                         void *fin, hipStream_t st) {
+  const int64_t items = (int64_t)p.n_tt * p.n_eb * p.splits;
+  dim3 grid((unsigned)((items + 3) / 4));
+  // 8-byte scale loads need 4 groups (group 64) or 2 groups (group 128) of
+  // whole dwords at every 256-column batch start
+  const int64_t gpr = H / gs;
+  const int sb_vec =
+      (H / p.splits) % 256 == 0 && ((gs == 64 && gpr % 4 == 0) || (gs == 128 && gpr % 2 == 0));
+  if (sb_vec)
+    hipLaunchKernelGGL((route_mfma_kernel<DT, EB, true>), grid, dim3(256), 0, st,
+                       (const uint16_t *)x, (int)T, (int)H, wr, (const uint16_t *)sr,
+                       (const uint16_t *)br, (int)E, gs, (int)(H / p.splits), p.n_tt, p.n_eb,
+                       p.splits, partial, (uint16_t *)fin);
+  else
+    hipLaunchKernelGGL((route_mfma_kernel<DT, EB, false>), grid, dim3(256), 0, st,
+                       (const uint16_t *)x, (int)T, (int)H, wr, (const uint16_t *)sr,
+                       (const uint16_t *)br, (int)E, gs, (int)(H / p.splits), p.n_tt, p.n_eb,
+                       p.splits, partial, (uint16_t *)fin);
   return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_route_t(const void *x, int64_t T, int64_t H, const uint32_t *wr, const void *sr,
+                          const void *br, int64_t E, int gs, const RoutePlan &p, double *partial,
+                          void *fin, hipStream_t st) {
+  return p.eb == 4 ? launch_mfma_t<DT, 4>(x, T, H, wr, sr, br, E, gs, p, partial, fin, st)
+                   : launch_mfma_t<DT, 1>(x, T, H, wr, sr, br, E, gs, p, partial, fin, st);
 }
 
 }  // namespace
 
-int route_experts_per_block(int64_t T) { return T >= 512 ? 16 : 4; }
-
-int route_splits(int64_t T, int64_t H) {
-  // enough blocks to fill the chip: long H ranges for big token counts,
-  // short ones (more splits) for decode-sized batches
-  const int64_t target = T >= 512 ? 512 : 128;
-  for (int s = 16; s > 1; s >>= 1)
-    if (H % s == 0 && (H / s) % 8 == 0 && H / s >= target) return s;
-  return 1;
-}
+int route_splits(int64_t T, int64_t H, int64_t E) { return route_plan(T, H, E).splits; }
 
 hipError_t launch_route_partial(int dtype, const void *x, int64_t T, int64_t H,
                                 const uint32_t *wr, const void *sr, const void *br, int64_t E,
-                                int gs, int splits, double *partial, void *fin, hipStream_t st) {
-  const bool big = route_experts_per_block(T) == 16;
-  if (dtype == DT_BF16)
-    return big ? launch_partial_t<DT_BF16, 16>(x, T, H, wr, sr, br, E, gs, splits, partial, fin, st)
-               : launch_partial_t<DT_BF16, 4>(x, T, H, wr, sr, br, E, gs, splits, partial, fin, st);
-  return big ? launch_partial_t<DT_F16, 16>(x, T, H, wr, sr, br, E, gs, splits, partial, fin, st)
-             : launch_partial_t<DT_F16, 4>(x, T, H, wr, sr, br, E, gs, splits, partial, fin, st);
+                                int gs, bool final_act, double *partial, void *fin,
+                                hipStream_t st) {
+  RoutePlan p = route_plan(T, H, E);
+  if (final_act) p.splits = 1;
+  return dtype == DT_BF16
+             ? launch_route_t<DT_BF16>(x, T, H, wr, sr, br, E, gs, p, partial, fin, st)
+             : launch_route_t<DT_F16>(x, T, H, wr, sr, br, E, gs, p, partial, fin, st);
 }
 
 hipError_t launch_route_finalize(int dtype, const double *partial, int splits, int64_t T,
