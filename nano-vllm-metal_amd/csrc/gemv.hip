@@ -36,10 +36,13 @@ namespace {
 
 constexpr int GI = 4;  // 64-wide groups per pipeline stage: one 128-byte line per row
 
-// Scale/bias loads of one pipeline stage: 4 consecutive bf16/fp16 values
-// (group 64, rows a multiple of 4 groups long), 2 values (group 128), or one
-// value per group.
-enum { SB_PER_GROUP = 0, SB_VEC4 = 1, SB_VEC2 = 2 };
+// Scales and biases.  SB_ROW: each lane loads 16 bytes (8 values) of its
+// row's scales and biases once per tile -- lane group G holds scale groups
+// 8G..8G+7 -- and the stage fetches the value it needs from the holding lane
+// with ds_bpermute.  Needs rows of an even number of scale groups (4-byte
+// aligned rows) and at most 32 of them.  SB_PER_GROUP: 16-bit loads per group
+// and stage, for the remaining shapes.
+enum { SB_PER_GROUP = 0, SB_ROW = 1 };
 
 // Routed rows staged per pass (MFMA rows CH..15 stay zero).  Experts with
 // more routed rows take further passes over their weights.
@@ -52,20 +55,35 @@ constexpr int CH = 8;
 __host__ __device__ constexpr int gemv_lds_bytes(int K) {
   return (CH + 1) * (K / 8 + 1) * 16 + (K / 64) * CH * 4 + 512;
 }
-constexpr int kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
+// LDS per workgroup on gfx950 is 160 KiB; 4 KiB stay for static LDS
+constexpr int kMaxLds = 156 * 1024;
 
+// Compute units of the current device (cached per device).
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Persistent grid: block b walks a contiguous share of the work items
+// (active expert, 64*NT-row block) in expert order, so the activation rows of
+// an expert are staged once per block and the grid drains evenly.
 template <int DT, bool DUAL, int NT, int SB>
 __global__ __launch_bounds__(256, 3) void gemv_kernel(const GroupedArgs a) {
   using A = Act<DT>;
   constexpr int NM = DUAL ? 2 : 1;
+  constexpr int ROWS = 4 * 16 * NT;  // output rows of one work item
   extern __shared__ __attribute__((aligned(16))) u32x4 xl[];
+  __shared__ int s_act[kMaxExperts];  // active experts, ascending
+  __shared__ int s_nact;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int e = blockIdx.y;
-  const int nb = a.offsets[e], ne = a.offsets[e + 1];
-  const int rb = blockIdx.x * (4 * 16 * NT);
-  if (nb >= ne || rb >= a.R) return;  // uniform over the block
-  const int r0 = rb + wv * 16 * NT;
-  const bool wave_rows = r0 < a.R;
 
   const int col = lane & 15, G = lane >> 4;
   const int KW = a.K >> 3, KG = a.K >> 6, GPR = a.K / a.gs;
@@ -75,6 +93,30 @@ __global__ __launch_bounds__(256, 3) void gemv_kernel(const GroupedArgs a) {
   float *sxl = (float *)(xl + (CH + 1) * pitch);  // [KG][CH]
 
   for (int i = tid; i < pitch; i += blockDim.x) xl[zero_row + i] = u32x4{0, 0, 0, 0};
+  if (wv == 0) {
+    int base = 0;
+    for (int c0 = 0; c0 < a.E; c0 += 64) {
+      const int e = c0 + lane;
+      const bool act = e < a.E && a.offsets[e + 1] > a.offsets[e];
+      const uint64_t m = __ballot(act);
+      if (act) s_act[base + __popcll(m & ((1ull << lane) - 1ull))] = e;
+      base += __popcll(m);
+    }
+    if (lane == 0) s_nact = base;
+  }
+  __syncthreads();
+  const int RBPE = (a.R + ROWS - 1) / ROWS;
+  const int W = s_nact * RBPE;
+  const int i0 = (int)((int64_t)blockIdx.x * W / gridDim.x);
+  const int i1 = (int)((int64_t)(blockIdx.x + 1) * W / gridDim.x);
+  const int NS = (KG + GI - 1) / GI;
+  int staged_e = -1, staged_nc = -1;
+
+  for (int item = i0; item < i1; ++item) {
+  const int e = s_act[item / RBPE];
+  const int r0 = (item % RBPE) * ROWS + wv * 16 * NT;
+  const bool wave_rows = r0 < a.R;
+  const int nb = a.offsets[e], ne = a.offsets[e + 1];
 
   rsrc_t wr[NM], sr[NM], br[NM];
 #pragma unroll
@@ -94,30 +136,22 @@ __global__ __launch_bounds__(256, 3) void gemv_kernel(const GroupedArgs a) {
     so[t] = tv[t] ? row * GPR * 2 : kMaskedOffset;
   }
 
-  // one pipeline stage = 4 groups: two 16-byte loads per (matrix, row tile)
-  // and packed scales/biases (value of group gi: half (gi & 1) of dword gi >> 1)
+  // one pipeline stage = 4 groups: two 16-byte loads per (matrix, row tile);
+  // with SB_PER_GROUP also the stage's scales/biases, packed (value of group
+  // gi in half (gi & 1) of dword gi >> 1)
   struct Stage {
     u32x4 q[NM][NT][2];
     u32x2 s[NM][NT], b[NM][NT];
   };
   auto load = [&](int st_idx, Stage &st) {
     const int ws = __builtin_amdgcn_readfirstlane(128 * st_idx);
-    const int ss = __builtin_amdgcn_readfirstlane(2 * GI * st_idx);
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         st.q[m][t][0] = bload16(wr[m], wo[t], ws);
         st.q[m][t][1] = bload16(wr[m], wo[t] + 64, ws);
-        if constexpr (SB == SB_VEC4) {
-          st.s[m][t] = bload8(sr[m], so[t], ss);
-          st.b[m][t] = bload8(br[m], so[t], ss);
-        } else if constexpr (SB == SB_VEC2) {
-          const uint32_t sv = bload4(sr[m], so[t], ss >> 1);
-          const uint32_t bv = bload4(br[m], so[t], ss >> 1);
-          st.s[m][t] = u32x2{(sv & 0xFFFFu) * 0x10001u, (sv >> 16) * 0x10001u};
-          st.b[m][t] = u32x2{(bv & 0xFFFFu) * 0x10001u, (bv >> 16) * 0x10001u};
-        } else {
+        if constexpr (SB == SB_PER_GROUP) {
           uint32_t sv[GI], bv[GI];
 #pragma unroll
           for (int gi = 0; gi < GI; ++gi) {
@@ -129,10 +163,51 @@ __global__ __launch_bounds__(256, 3) void gemv_kernel(const GroupedArgs a) {
         }
       }
   };
+  // SB_ROW: the tile's scales/biases, resident for the whole wavefront
+  u32x4 srow[NM][NT], brow[NM][NT];
+  if constexpr (SB == SB_ROW) {
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        srow[m][t] = bload16(sr[m], so[t] + 16 * G, 0);
+        brow[m][t] = bload16(br[m], so[t] + 16 * G, 0);
+      }
+  }
+  // dword holding the scale/bias values of 64-wide groups (g, g + 1), g even:
+  // both share one 32-bit word of the resident row (group 64) or are the same
+  // value (group 128, duplicated into both halves)
+  auto sb_pair = [&](const u32x4 &row, int g) -> uint32_t {
+    const int sg = g >> gsh;  // scale group of g
+    const int src = col + 16 * (sg >> 3);
+    const int w = (sg & 7) >> 1;
+    const uint32_t mine = w == 0 ? row.x : w == 1 ? row.y : w == 2 ? row.z : row.w;
+    const uint32_t d = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)mine);
+    if (gsh == 0) return d;
+    const uint32_t h = (sg & 1) ? (d >> 16) : (d & 0xFFFFu);
+    return h * 0x10001u;
+  };
+
+  const int rot = __builtin_amdgcn_readfirstlane(
+      (int)((item * 4u + wv + 3u * e) % (unsigned)NS));
+  auto st_at = [&](int i) {
+    const int st = rot + i;
+    return st >= NS ? st - NS : st;
+  };
 
   for (int nc = nb; nc < ne; nc += CH) {
     const int cnt = min(CH, ne - nc);
-    __syncthreads();  // the previous token chunk is done with the LDS rows
+    // the first two weight stages do not depend on the activations: issue
+    // them before staging so their latency overlaps the staging
+    Stage sa, sb, sc;
+    if (wave_rows) {
+      load(st_at(0), sa);
+      if (NS > 1) load(st_at(1), sb);
+    }
+    if (e != staged_e || nc != staged_nc) {
+    staged_e = e;
+    staged_nc = nc;
+    __syncthreads();  // every wavefront is done with the previous rows
     // stage the routed activation rows (pair order) and their group sums
     for (int it = tid; it < cnt * KW; it += blockDim.x) {
       const int c = it / KW, ch = it - c * KW;
@@ -149,6 +224,7 @@ __global__ __launch_bounds__(256, 3) void gemv_kernel(const GroupedArgs a) {
       if ((ch & 7) == 0) sxl[(ch >> 3) * CH + c] = sx;
     }
     __syncthreads();
+    }
     if (!wave_rows) continue;
 
     const bool tok_ok = col < cnt;
@@ -200,7 +276,14 @@ __global__ __launch_bounds__(256, 3) void gemv_kernel(const GroupedArgs a) {
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
             if (!tv[t]) continue;
-            const uint32_t sd = st.s[m][t][j], bd = st.b[m][t][j];
+            uint32_t sd, bd;
+            if constexpr (SB == SB_ROW) {
+              sd = sb_pair(srow[m][t], ga);
+              bd = sb_pair(brow[m][t], ga);
+            } else {
+              sd = st.s[m][t][j];
+              bd = st.b[m][t][j];
+            }
             const float s0 = A::lo(sd), b0 = A::lo(bd);
             const float bp0 = fmaf(-A::kMagic, s0, b0);
 #pragma unroll
@@ -222,17 +305,7 @@ __global__ __launch_bounds__(256, 3) void gemv_kernel(const GroupedArgs a) {
     // only for the stage about to be used.  Wavefronts start at different
     // stages of their rows so that concurrent wavefronts do not sweep the
     // same column offsets (and memory channels) in lockstep.
-    const int NS = (KG + GI - 1) / GI;
-    const int rot = __builtin_amdgcn_readfirstlane(
-        (int)((blockIdx.x * (blockDim.x >> 6) + wv + 3u * blockIdx.y) % (unsigned)NS));
-    auto st_at = [&](int i) {
-      const int st = rot + i;
-      return st >= NS ? st - NS : st;
-    };
     auto run = [&](int i, const Stage &st) { compute(st_at(i), st, min(GI, KG - GI * st_at(i))); };
-    Stage sa, sb, sc;
-    load(st_at(0), sa);
-    if (NS > 1) load(st_at(1), sb);
     int i = 0;
     for (; i + 4 < NS; i += 3) {
       load(st_at(i + 2), sc);
@@ -276,29 +349,29 @@ __global__ __launch_bounds__(256, 3) void gemv_kernel(const GroupedArgs a) {
       }
     }
   }
+  }
 }
 
 template <int DT, bool DUAL, int NT>
 hipError_t launch_nt(const GroupedArgs &a, int sb_mode, hipStream_t st) {
   constexpr int WAVES = 4;
   const int rows_per_block = 16 * NT * WAVES;
-  dim3 grid((unsigned)((a.R + rows_per_block - 1) / rows_per_block), (unsigned)a.E);
+  // work items can number at most E * ceil(R / rows); three blocks per CU
+  // are resident at once (register-limited), so launch no more than that
+  const int64_t items = (int64_t)a.E * ((a.R + rows_per_block - 1) / rows_per_block);
+  dim3 grid((unsigned)std::min<int64_t>(items, 3 * (int64_t)cu_count()));
   const size_t lds = gemv_lds_bytes(a.K);
   if (lds > (size_t)kMaxLds) return hipErrorInvalidValue;
   // allow dynamic LDS beyond the 64 KiB default (once per instantiation)
-  static const hipError_t attr[3] = {
+  static const hipError_t attr[2] = {
       hipFuncSetAttribute((const void *)gemv_kernel<DT, DUAL, NT, SB_PER_GROUP>,
                           hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds),
-      hipFuncSetAttribute((const void *)gemv_kernel<DT, DUAL, NT, SB_VEC4>,
-                          hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds),
-      hipFuncSetAttribute((const void *)gemv_kernel<DT, DUAL, NT, SB_VEC2>,
+      hipFuncSetAttribute((const void *)gemv_kernel<DT, DUAL, NT, SB_ROW>,
                           hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds)};
   for (hipError_t e : attr)
     if (e != hipSuccess) return e;
-  if (sb_mode == SB_VEC4)
-    hipLaunchKernelGGL((gemv_kernel<DT, DUAL, NT, SB_VEC4>), grid, dim3(64 * WAVES), lds, st, a);
-  else if (sb_mode == SB_VEC2)
-    hipLaunchKernelGGL((gemv_kernel<DT, DUAL, NT, SB_VEC2>), grid, dim3(64 * WAVES), lds, st, a);
+  if (sb_mode == SB_ROW)
+    hipLaunchKernelGGL((gemv_kernel<DT, DUAL, NT, SB_ROW>), grid, dim3(64 * WAVES), lds, st, a);
   else
     hipLaunchKernelGGL((gemv_kernel<DT, DUAL, NT, SB_PER_GROUP>), grid, dim3(64 * WAVES), lds,
                        st, a);
@@ -308,9 +381,7 @@ hipError_t launch_nt(const GroupedArgs &a, int sb_mode, hipStream_t st) {
 template <int DT>
 hipError_t launch_t(bool dual, const GroupedArgs &a, hipStream_t st) {
   const int gpr = a.K / a.gs;
-  const int sb_mode = (a.gs == 64 && gpr % 4 == 0)    ? SB_VEC4
-                      : (a.gs == 128 && gpr % 2 == 0) ? SB_VEC2
-                                                      : SB_PER_GROUP;
+  const int sb_mode = (gpr % 2 == 0 && gpr <= 32) ? SB_ROW : SB_PER_GROUP;
   // gate/up: one 16-row tile of both matrices per wavefront; down: two tiles
   return dual ? launch_nt<DT, true, 1>(a, sb_mode, st) : launch_nt<DT, false, 2>(a, sb_mode, st);
 }

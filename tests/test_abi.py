@@ -1,0 +1,171 @@
+"""The C ABI and the host-side mirror, without a GPU.
+
+* libnvm_moe.so loads and exports every function declared in include/nvm_moe.h;
+* argument validation returns the documented status codes and messages
+  before any device work (so it can be exercised on a CPU-only host);
+* the Python mirror rejects CPU tensors and maps status codes to exceptions;
+* the torch MLX-layout quantizer agrees with the oracle's.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "nvm_moe.h"
+
+
+def _lib():
+    from nano_vllm_metal_amd import _lib
+
+    return _lib, _lib.load()
+
+
+def test_library_exports_every_header_function():
+    names = set(re.findall(r"^\s*(?:int|const char \*)\s*(nvm_\w+)\s*\(", HEADER.read_text(), re.M))
+    assert "nvm_moe_forward" in names and len(names) >= 12
+    _, lib = _lib()
+    for n in sorted(names):
+        assert hasattr(lib, n), f"{n} declared in the header but not exported"
+    from nano_vllm_metal_amd._lib import SIGNATURES
+
+    assert set(SIGNATURES) | {"nvm_abi_version", "nvm_last_error"} == names
+
+
+def test_abi_version():
+    L, lib = _lib()
+    assert lib.nvm_abi_version() == 1
+
+
+def _err(lib) -> str:
+    return lib.nvm_last_error().decode()
+
+
+def test_workspace_sizes():
+    L, lib = _lib()
+    sz = ctypes.c_size_t()
+    assert lib.nvm_moe_workspace_size(32, 2048, 768, 128, 8, ctypes.byref(sz)) == 0
+    # partial logits + ids/scores + dispatch + h [N, I] + down [N, H]
+    N = 32 * 8
+    assert sz.value >= N * 768 * 2 + N * 2048 * 2
+    assert lib.nvm_route_workspace_size(32, 2048, 128, ctypes.byref(sz)) == 0
+    assert sz.value % 8 == 0 and sz.value >= 32 * 128 * 8
+    assert lib.nvm_grouped_linear_workspace_size(100, 128, 64, 8, ctypes.byref(sz)) == 0
+    assert lib.nvm_moe_workspace_size(32, 2048, 768, 128, 8, None) == L.NVM_ERR_INVALID
+
+
+def _forward(lib, **kw):
+    args = dict(x=1, T=4, H=2048, I=768, E=128, k=8, norm=1, gs=64, bits=4, dtype=1, y=1,
+                regime=0, ws=1, ws_bytes=1 << 40)
+    args.update(kw)
+    p = [1] * 12  # weight pointers (never dereferenced: validation fails first)
+    return lib.nvm_moe_forward(args["x"], args["T"], args["H"], args["I"], args["E"], args["k"],
+                               args["norm"], args["gs"], args["bits"], args["dtype"], *p,
+                               args["y"], None, None, args["regime"], args["ws"],
+                               args["ws_bytes"], None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    ({"bits": 8}, -2, "bits must be 4"),
+    ({"gs": 32}, -2, "group_size"),
+    ({"dtype": 7}, -1, "dtype"),
+    ({"H": 100}, -1, "hidden"),
+    ({"I": 96}, -1, "intermediate"),
+    ({"E": 1000}, -2, "experts"),
+    ({"k": 0}, -1, "top_k"),
+    ({"k": 200}, -1, "top_k"),
+    ({"regime": 5}, -1, "regime"),
+    ({"x": None}, -1, "null pointer"),
+    ({"ws_bytes": 10}, -3, "workspace"),
+])
+def test_forward_validation(kw, code, msg):
+    L, lib = _lib()
+    assert _forward(lib, **kw) == code
+    assert msg in _err(lib)
+
+
+def test_forward_empty_batch_is_a_no_op():
+    L, lib = _lib()
+    assert _forward(lib, T=0) == 0
+
+
+def test_quantized_matmul_validation():
+    L, lib = _lib()
+    # the reference requires transpose_b (quantized_matmul.cpp:56-58)
+    r = lib.nvm_quantized_matmul(1, 1, 128, 4, 1, 1, 0, 1, 2, 128, 5, 1, None)
+    assert r == L.NVM_ERR_UNSUPPORTED and "transposed" in _err(lib)
+    r = lib.nvm_quantized_matmul(1, 1, 128, 4, 1, 1, 1, 1, 2, 100, 5, 1, None)
+    assert r == L.NVM_ERR_INVALID and "divisible" in _err(lib)
+
+
+def test_dispatch_and_route_validation():
+    L, lib = _lib()
+    assert lib.nvm_moe_dispatch(1, 10, 0, 1, 1, None) == L.NVM_ERR_INVALID
+    assert lib.nvm_moe_dispatch(1, 10, 4096, 1, 1, None) == L.NVM_ERR_UNSUPPORTED
+    r = lib.nvm_moe_route(1, 4, 2048, 1, 1, 1, 128, 64, 4, 9, 0, 1, None, 1, 1, 1, 0, None)
+    assert r == L.NVM_ERR_WORKSPACE
+    r = lib.nvm_moe_route(1, 4, 2048, 1, 1, 1, 128, 64, 4, 129, 0, 1, None, 1, 1, 1, 1 << 30, None)
+    assert r == L.NVM_ERR_INVALID
+
+
+def test_check_maps_status_to_exceptions():
+    L, lib = _lib()
+    _forward(lib, bits=8)
+    with pytest.raises(ValueError):
+        L.check(L.NVM_ERR_UNSUPPORTED)
+    with pytest.raises(RuntimeError):
+        L.check(L.NVM_ERR_WORKSPACE)
+    L.check(L.NVM_OK)
+
+
+def test_python_mirror_rejects_cpu_tensors():
+    from nano_vllm_metal_amd import Moe, QuantizedWeights, route_topk
+
+    w = QuantizedWeights(torch.zeros(4, 2, dtype=torch.bfloat16), torch.zeros(4, 2, dtype=torch.bfloat16),
+                         64, 4, torch.zeros(4, 16, dtype=torch.int32))
+    with pytest.raises(ValueError, match="GPU only"):
+        route_topk(torch.zeros(2, 128, dtype=torch.bfloat16), w, 2)
+    moe = Moe(w, w, w, w, 2)
+    with pytest.raises(ValueError, match="GPU only"):
+        moe(torch.zeros(1, 2, 128, dtype=torch.bfloat16))
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    import nano_vllm_metal_amd._lib as L
+
+    monkeypatch.setattr(L, "_lib", None)
+    monkeypatch.setenv("NVM_MOE_LIB", str(tmp_path / "absent.so"))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        L.load()
+
+
+@pytest.mark.parametrize("act", ["float16", "bfloat16"])
+@pytest.mark.parametrize("gs", [64, 128])
+def test_torch_quantizer_agrees_with_oracle(act, gs):
+    from oracle import moe_oracle as O
+    from nano_vllm_metal_amd import dequantize, quantize
+
+    rng = np.random.default_rng(21)
+    w = O.round_act(rng.standard_normal((24, 2 * gs)) * 0.02, act)
+    dt = torch.float16 if act == "float16" else torch.bfloat16
+    wq, s, b = quantize(torch.from_numpy(w.astype(np.float32)).to(dt), gs, 4)
+    owq, os_, ob = O.quantize(w, gs, 4, act)
+    # the torch path computes in float32, the oracle in float64: scales/biases
+    # agree after rounding to act except in rare near-tie cases
+    s_t = s.float().numpy().astype(np.float64)
+    b_t = b.float().numpy().astype(np.float64)
+    assert np.mean(s_t == os_) > 0.95 and np.mean(b_t == ob) > 0.95
+    same = (s_t == os_) & (b_t == ob)
+    codes_t = O.unpack_nibbles(wq.numpy().view(np.uint32))
+    codes_o = O.unpack_nibbles(owq)
+    rows = np.repeat(same, gs, axis=1)
+    assert np.array_equal(codes_t[rows], codes_o[rows])
+    # dequantisation of the torch layout equals the oracle's formula
+    deq = dequantize(wq, s, b, gs).numpy().astype(np.float64)
+    assert np.array_equal(deq, O.dequantize(wq.numpy().view(np.uint32), s_t, b_t, gs))
