@@ -337,14 +337,100 @@ def cpu_baseline(layer, T, seconds, dev):
     }
 
 
+TRAFFIC_JSON = ROOT / "profiles" / "traffic.json"
+COPY_PROBE_BYTES = 256 << 20
+
+# rocprofv3 kernel names -> the product kernels reported in the JSON line
+KERNEL_KEYS = (
+    ("decode_gateup", "gemv_kernel<1, true"),
+    ("decode_down", "gemv_kernel<1, false"),
+    ("prefill_gateup", "gemm_kernel<1, true"),
+    ("prefill_down", "gemm_kernel<1, false"),
+    ("route_partial", "route_mfma_kernel<1"),
+    ("route_finalize", "route_finalize_kernel<1"),
+    ("dispatch", "dispatch_kernel"),
+    ("combine", "combine_kernel<1"),
+)
+
+
 def read_traffic(name):
-    p = ROOT / "profiles" / "traffic.json"
-    if not p.exists():
+    """HBM bytes per launch of a kernel, from the committed counter summary."""
+    if not TRAFFIC_JSON.exists():
         return None
     try:
-        return json.loads(p.read_text()).get(name)
+        rec = json.loads(TRAFFIC_JSON.read_text()).get(name)
     except (ValueError, OSError):
         return None
+    return None if rec is None else rec.get("hbm_bytes_per_launch")
+
+
+def rocprof_summary(root: Path, write_traffic: bool) -> str:
+    """Summarise rocprofv3 CSV output (kernel stats, FETCH_SIZE / WRITE_SIZE runs).
+
+    Counters are KiB per dispatch.  Each is scaled by what it reads for the
+    256 MiB device copy of ``--copy-probe`` (the largest copy dispatch):
+    factor = 256 MiB / (counter KiB * 1024).
+    """
+    import csv
+    from collections import defaultdict
+
+    def key_of(name):
+        for key, pat in KERNEL_KEYS:
+            if pat in name:
+                return key
+        return "copy" if "copyBuffer" in name else None
+
+    lines = []
+    stats = {}
+    for f in sorted(root.rglob("*kernel_stats.csv")):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                k = key_of(r["Name"])
+                if k and k != "copy":
+                    stats[k] = {"calls": int(r["Calls"]), "avg_us": float(r["AverageNs"]) / 1e3,
+                                "min_us": float(r["MinNs"]) / 1e3, "max_us": float(r["MaxNs"]) / 1e3}
+    if stats:
+        lines.append("kernel trace (rocprofv3 --kernel-trace --stats):")
+        for k, s in stats.items():
+            lines.append(f"  {k:16s} calls={s['calls']:5d} avg={s['avg_us']:8.2f} us "
+                         f"min={s['min_us']:8.2f} max={s['max_us']:8.2f}")
+    counters = defaultdict(lambda: defaultdict(list))
+    for f in sorted(root.rglob("*counter_collection.csv")):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                k = key_of(r["Kernel_Name"])
+                if k:
+                    counters[r["Counter_Name"]][k].append(float(r["Counter_Value"]))
+    traffic = {}
+    factors = {}
+    for cname in ("FETCH_SIZE", "WRITE_SIZE"):
+        per = counters.get(cname)
+        if not per or not per.get("copy"):
+            continue
+        probe_kib = max(per["copy"])
+        factors[cname] = COPY_PROBE_BYTES / (probe_kib * 1024.0)
+        lines.append(f"{cname}: 256 MiB copy reads {probe_kib:.0f} KiB -> factor "
+                     f"{factors[cname]:.3f}")
+        for k, vals in per.items():
+            if k == "copy":
+                continue
+            kib = sum(vals) / len(vals)
+            b = kib * 1024.0 * factors[cname]
+            traffic.setdefault(k, {})[cname.lower() + "_bytes"] = b
+            lines.append(f"  {k:16s} n={len(vals):5d} {kib:12.1f} KiB -> {b / 1e6:9.2f} MB per launch")
+    for k, rec in traffic.items():
+        if "fetch_size_bytes" in rec and "write_size_bytes" in rec:
+            rec["hbm_bytes_per_launch"] = rec["fetch_size_bytes"] + rec["write_size_bytes"]
+        if k in stats:
+            rec["avg_us"] = stats[k]["avg_us"]
+    text = "\n".join(lines)
+    if write_traffic and traffic:
+        old = json.loads(TRAFFIC_JSON.read_text()) if TRAFFIC_JSON.exists() else {}
+        old.update(traffic)
+        old["_factors"] = factors
+        TRAFFIC_JSON.parent.mkdir(exist_ok=True)
+        TRAFFIC_JSON.write_text(json.dumps(old, indent=1, sort_keys=True) + "\n")
+    return text
 
 
 def main():
@@ -360,11 +446,21 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 256 MiB device copy (calibrates HBM byte counters)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="measure only the 4096-token prefill with uniform routing")
+    ap.add_argument("--rocprof-summary", metavar="DIR",
+                    help="summarise rocprofv3 CSV output under DIR and exit (no GPU)")
+    ap.add_argument("--write-traffic", action="store_true",
+                    help="with --rocprof-summary: store HBM bytes per launch in profiles/traffic.json")
     args = ap.parse_args()
+
+    if args.rocprof_summary:
+        print(rocprof_summary(Path(args.rocprof_summary), args.write_traffic))
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the MoE block is benchmarked on a single MI355X "
-              "(multi-GPU expert/tensor sharding is not part of this build); run with --gpus 1",
+              "(expert/tensor sharding across GPUs is not implemented); run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)
 
@@ -380,6 +476,20 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.prefill_only:
+        log("[bench] building 2 layers of 30B-A3B MoE weights")
+        layers = make_layers(2, H, E, I, gs, dev)
+        r = prefill_bench(layers, 4096, max(args.steps // 20, 8), 3, dev, False)
+        log(f"[bench] prefill {r['routing']}: {r['layer_us']:.1f} us/layer, "
+            f"{r['layer_tflops']:.0f} TFLOP/s, kernels {r['kernel_us']}")
+        print(json.dumps({
+            "metric": METRIC, "value": r["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
+            "steps": max(args.steps // 20, 8), "warmup": 3, "ms_per_step": r["layer_us"] / 1e3,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic", "prefill": r,
+            "config": {"workload": "Qwen3-30B-A3B-shaped MoE layer, prefill 4096 tokens, "
+                                   "uniform routing", "tokens": 4096}}), flush=True)
+        return
     log(f"[bench] building {args.layers} layers of 30B-A3B MoE weights")
     layers = make_layers(args.layers, H, E, I, gs, dev)
 

@@ -92,9 +92,9 @@ int nvm_moe_route(const void *x, int64_t T, int64_t H, const uint32_t *wr, const
  * `grouped_expert_linear` (layers/moe.py:16-17).
  *   ids [n] int32 in [0,E); expert_offsets [E+1] int32 (exclusive prefix of
  *   the histogram); sorted_pairs [n] int32 (pair indices, expert-major).
- * Out-of-range ids make the call fail only if detected on the host (E is
- * validated); the kernel clamps nothing, so ids must be in range.
- * Needs no workspace.
+ * Pairs whose id lies outside [0,E) are left out: they fall in no expert's
+ * range, offsets[E] counts only the valid pairs, and sorted_pairs[offsets[E]..n)
+ * is not written.  1 <= E <= 512.  Needs no workspace.
  */
 int nvm_moe_dispatch(const int32_t *ids, int64_t n, int64_t E, int32_t *expert_offsets,
                      int32_t *sorted_pairs, nvm_stream_t stream);
