@@ -119,6 +119,10 @@ MoeWs carve_moe(void *base, int64_t T, int64_t H, int64_t I, int64_t E, int k) {
 
 int run_products(int dtype, bool decode, bool dual, nvm::GroupedArgs &g, int64_t pairs,
                  hipStream_t st) {
+  // the kernels address activations through 32-bit buffer offsets
+  NVM_SUPPORTED(g.act_rows * g.act_ld * 2 <= 0x7FFF0000ll,
+                "expert products: activation buffer of %lld bytes exceeds 2 GiB; split the batch",
+                (long long)(g.act_rows * g.act_ld * 2));
   if (decode) {
     NVM_TRY_HIP(nvm::launch_gemv(dtype, dual, g, st));
   } else {

@@ -2,16 +2,27 @@
 //
 // Replaces `mx.gather_qmm` inside grouped_expert_linear (layers/moe.py:21-32)
 // for prefill-sized batches, with SwiGLU (layers/moe.py:84) fused into the
-// gate/up epilogue.  Work is a list of (expert, 128-row m-tile) pairs built on
-// the device from the expert offsets (prefix sum of ceil(count_e / 128)), so no
-// host synchronisation is needed and empty experts cost nothing.
+// gate/up epilogue.  Work is a list of (expert, 128-row m-tile, n-tile)
+// triples built on the device from the expert offsets (prefix sum of
+// ceil(count_e / 128)), so no host synchronisation is needed and empty experts
+// cost nothing.
 //
-// Per 64-wide k-step a 256-thread block gathers 128 activation rows into LDS,
-// dequantises 2 x 128 weight rows (w = q*s + b in float32, rounded to the
-// activation dtype, as MLX's own GPU quantised matmul does) into LDS, and four
-// wavefronts (2 x 2) each run 2 x 2 x 2 v_mfma_f32_32x32x16 per 16-wide k
-// slice.  Rows are padded to 144 bytes so the 16-byte fragment reads of 32
-// consecutive rows hit distinct LDS banks.
+// A tile is 128 routed rows x 256 weight rows (gate/up: 128 columns of each
+// matrix; down: 256 columns).  Per 64-wide k-step the block stages the
+// gathered activation rows (bf16/fp16) and the *packed* int4 weight rows in
+// LDS, double-buffered, with the next k-step's global loads in flight during
+// the current k-step's MFMAs.  The four wavefronts split the tile along N: a
+// wavefront owns 2 x 32 weight rows (gate/up: the same 32 columns of both
+// matrices, so the SwiGLU pair lands in one lane) and all 128 routed rows
+// (4 x 2 tiles of v_mfma_f32_32x32x16).  Each weight word is dequantised once
+// per tile, in registers, right before its MFMA: w = q*s + b in float32,
+// rounded to the activation dtype.
+//
+// k-order inside a k-step: MFMA chunk c (16 wide) and lane half h cover
+// k = 8*(4h + c) + i, i = 0..7, in both operands.  A lane's B operand for
+// chunk c is then packed word 4h + c of its weight row (one 16-byte LDS read
+// serves all four chunks) and its A operand is 16 bytes at offset
+// 16*(4h + c) of the activation row.
 #include "common.h"
 #include "internal.h"
 
@@ -19,18 +30,49 @@ namespace nvm {
 
 namespace {
 
-constexpr int BM = kGemmBM, BN = kGemmBN, BK = 64, PITCH = BK + 8;
+constexpr int BM = kGemmBM;       // routed rows per tile
+constexpr int WROWS = 256;        // weight rows per tile
+constexpr int BK = 64;            // k per stage
+constexpr int A_PITCH = 144;      // bytes per staged activation row (128 + 16 pad)
+constexpr int B_PITCH = 48;       // bytes per staged weight row (32 + 16 pad)
+constexpr int A_STAGE = BM * A_PITCH;
+constexpr int B_STAGE = WROWS * B_PITCH;
+constexpr int STAGE = A_STAGE + B_STAGE;
+constexpr int kGemmLds = 2 * STAGE;
+
+__device__ __forceinline__ float byte_f32(uint32_t v, int j) {
+  return (float)((v >> (8 * j)) & 0xFFu);  // v_cvt_f32_ubyte<j>
+}
+
+// One packed word (codes q0..q7, q_i at bits 4i) -> 8 act values q_i*s + b in
+// natural order: dword j holds (k = 2j, k = 2j + 1).
+template <int DT>
+__device__ __forceinline__ u32x4 dequant8(uint32_t w, float s, float b) {
+  using A = Act<DT>;
+  uint32_t lo = w & 0x0F0F0F0Fu;         // byte j = q_{2j}
+  uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // byte j = q_{2j+1}
+  // opaque to the optimiser, which would otherwise re-derive every byte with
+  // its own mask instead of converting bytes of the masked word directly
+  asm("" : "+v"(lo), "+v"(hi));
+  u32x4 o;
+  o.x = A::pack2(fmaf(byte_f32(lo, 0), s, b), fmaf(byte_f32(hi, 0), s, b));
+  o.y = A::pack2(fmaf(byte_f32(lo, 1), s, b), fmaf(byte_f32(hi, 1), s, b));
+  o.z = A::pack2(fmaf(byte_f32(lo, 2), s, b), fmaf(byte_f32(hi, 2), s, b));
+  o.w = A::pack2(fmaf(byte_f32(lo, 3), s, b), fmaf(byte_f32(hi, 3), s, b));
+  return o;
+}
 
 template <int DT, bool DUAL>
-__global__ __launch_bounds__(256) void gemm_kernel(const GroupedArgs a) {
+__global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n_tiles) {
   using A = Act<DT>;
-  __shared__ __attribute__((aligned(16))) uint16_t As[BM * PITCH];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2 * BN * PITCH];
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_arow[BM];
+  __shared__ int s_orow[BM];
   __shared__ int s_tiles[kMaxExperts + 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int mt = blockIdx.y;
+  const int l32 = lane & 31, h = lane >> 5;
+
   // m-tile list: exclusive prefix over experts of ceil(count / BM), built by
   // wavefront 0 from the expert offsets (E <= kMaxExperts)
   if (wv == 0) {
@@ -50,7 +92,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GroupedArgs a) {
     if (lane == 0) s_tiles[a.E] = carry;
   }
   __syncthreads();
-  if (mt >= s_tiles[a.E]) return;
+
+  // Workgroups are dealt to the 8 XCDs round-robin by id; give each XCD a
+  // contiguous range of (m-tile, n-tile) pairs so the tiles sharing activation
+  // rows (same m-tile) and weights (same expert and n-tile) share an L2.
+  const int total = s_tiles[a.E] * n_tiles;
+  const int per_xcd = (total + 7) >> 3;
+  const int local = blockIdx.x >> 3;
+  if (local >= per_xcd) return;
+  const int t = (blockIdx.x & 7) * per_xcd + local;
+  if (t >= total) return;
+  const int mt = t / n_tiles, nt = t - mt * n_tiles;
+
   // largest expert whose first tile is <= mt (skips experts with no tiles)
   int lo = 0, hi = a.E - 1;
   while (lo < hi) {
@@ -63,132 +116,161 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GroupedArgs a) {
   const int e = lo;
   const int m0 = a.offsets[e] + (mt - s_tiles[e]) * BM;
   const int mcnt = min(BM, a.offsets[e + 1] - m0);
-  const int n0 = blockIdx.x * (DUAL ? BN : 2 * BN);
-  const int n1 = DUAL ? n0 : n0 + BN;  // first row of the second weight tile
-  const uint32_t *W1 = DUAL ? a.w1 : a.w0;
-  const uint16_t *S1 = DUAL ? a.s1 : a.s0;
-  const uint16_t *B1 = DUAL ? a.b1 : a.b0;
-  const int KW = a.K >> 3, GPR = a.K / a.gs;
+  const int R = a.R, KW = a.K >> 3, GPR = a.K / a.gs;
+  const int n0 = nt * (DUAL ? WROWS / 2 : WROWS);
 
-  for (int i = tid; i < BM; i += 256)
-    s_arow[i] = i < mcnt ? (a.a_map ? a.a_map[m0 + i] / a.a_div : m0 + i) : -1;
+  for (int i = tid; i < BM; i += 256) {
+    const int slot = m0 + i;
+    s_arow[i] = i < mcnt ? (a.a_map ? a.a_map[slot] / a.a_div : slot) : -1;
+    s_orow[i] = i < mcnt ? (a.o_map ? a.o_map[slot] : slot) : -1;
+  }
+  __syncthreads();
 
-  const int wm = wv & 1, wn = wv >> 1;
-  const int l32 = lane & 31, kh = lane >> 5;
-  f32x16 acc[2][2][2];
-#pragma unroll
-  for (int m = 0; m < 2; ++m)
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[m][i][j][r] = 0.f;
+  // ---- descriptors and per-thread offsets of the staging loads
+  const rsrc_t ra = make_rsrc(a.act, (uint32_t)(a.act_rows * a.act_ld * 2));
+  const int64_t eoff = (int64_t)e * R;
+  const rsrc_t rw0 = make_rsrc(a.w0 + eoff * KW, (uint32_t)R * KW * 4);
+  const rsrc_t rw1 = make_rsrc((DUAL ? a.w1 : a.w0) + eoff * KW, (uint32_t)R * KW * 4);
+  const rsrc_t rs0 = make_rsrc(a.s0 + eoff * GPR, (uint32_t)R * GPR * 2);
+  const rsrc_t rb0 = make_rsrc(a.b0 + eoff * GPR, (uint32_t)R * GPR * 2);
+  const rsrc_t rs1 = make_rsrc((DUAL ? a.s1 : a.s0) + eoff * GPR, (uint32_t)R * GPR * 2);
+  const rsrc_t rb1 = make_rsrc((DUAL ? a.b1 : a.b0) + eoff * GPR, (uint32_t)R * GPR * 2);
 
-  for (int k0 = 0; k0 < a.K; k0 += BK) {
-    __syncthreads();
-    // activations: 128 rows x 8 chunks of 16 bytes
+  // activations: thread loads rows (tid >> 3) + 32c, 16-byte chunk tid & 7
+  int a_voff[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int ar = s_arow[(tid >> 3) + 32 * c];
+    a_voff[c] = ar >= 0 ? (int)(((int64_t)ar * a.act_ld) * 2) + 16 * (tid & 7) : kMaskedOffset;
+  }
+  // packed weights: thread loads staged rows (tid >> 1) + 128c, half tid & 1
+  int b_voff[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int wrow = (tid >> 1) + 128 * c;
+    const int grow = DUAL ? n0 + (wrow & 127) : n0 + wrow;
+    b_voff[c] = grow < R ? grow * KW * 4 + 16 * (tid & 1) : kMaskedOffset;
+  }
+  // this lane's two weight rows (sub 0/1) for the scale/bias loads and reads
+  int srow[2], lrow[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    lrow[s] = DUAL ? 128 * s + 32 * wv + l32 : 64 * wv + 32 * s + l32;
+    const int grow = DUAL ? n0 + 32 * wv + l32 : n0 + 64 * wv + 32 * s + l32;
+    srow[s] = grow < R ? grow * GPR * 2 : kMaskedOffset;
+  }
+
+  u32x4 ga[4], gb[2];
+  uint32_t gsc[2], gbi[2];
+  auto load_stage = [&](int k0) {
+    const int sa = __builtin_amdgcn_readfirstlane(k0 * 2);
+    const int sb = __builtin_amdgcn_readfirstlane(k0 >> 1);
+    const int sg = __builtin_amdgcn_readfirstlane((k0 / a.gs) * 2);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) ga[c] = bload16(ra, a_voff[c], sa);
+    gb[0] = bload16(rw0, b_voff[0], sb);
+    gb[1] = bload16(rw1, b_voff[1], sb);
+    gsc[0] = bload2(rs0, srow[0], sg);
+    gbi[0] = bload2(rb0, srow[0], sg);
+    gsc[1] = bload2(rs1, srow[1], sg);
+    gbi[1] = bload2(rb1, srow[1], sg);
+  };
+  auto store_stage = [&](int buf) {
+    uint8_t *As = smem + buf * STAGE;
+    uint8_t *Bs = As + A_STAGE;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      *(u32x4 *)(As + ((tid >> 3) + 32 * c) * A_PITCH + 16 * (tid & 7)) = ga[c];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      *(u32x4 *)(Bs + ((tid >> 1) + 128 * c) * B_PITCH + 16 * (tid & 1)) = gb[c];
+  };
+
+  f32x16 acc[2][4];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[s][i][r] = 0.f;
+
+  const int nk = a.K / BK;
+  load_stage(0);
+  store_stage(0);
+  float sc[2] = {A::to_f32(gsc[0]), A::to_f32(gsc[1])};
+  float bi[2] = {A::to_f32(gbi[0]), A::to_f32(gbi[1])};
+  __syncthreads();
+
+  for (int ks = 0; ks < nk; ++ks) {
+    const bool more = ks + 1 < nk;
+    if (more) load_stage((ks + 1) * BK);
+    const uint8_t *As = smem + (ks & 1) * STAGE;
+    const uint8_t *Bs = As + A_STAGE;
+    u32x4 bw[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) bw[s] = *(const u32x4 *)(Bs + lrow[s] * B_PITCH + 16 * h);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const int idx = tid + 256 * c;
-      const int row = idx >> 3, ch = idx & 7;
-      const int ar = s_arow[row];
-      u32x4 v = {0, 0, 0, 0};
-      if (ar >= 0) v = ldg16(a.act + (int64_t)ar * a.act_ld + k0 + 8 * ch);
-      *(u32x4 *)(As + row * PITCH + 8 * ch) = v;
+      u32x4 af[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        af[i] = *(const u32x4 *)(As + (32 * i + l32) * A_PITCH + 16 * (4 * h + c));
+      u32x4 bf[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) bf[s] = dequant8<DT>(bw[s][c], sc[s], bi[s]);
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[s][i] = A::mfma32(af[i], bf[s], acc[s][i]);
     }
-    // weights: 2 tiles x 128 rows x 2 halves of 32 codes
+    if (more) {
+      store_stage((ks + 1) & 1);
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int idx = tid + 256 * c;
-      const int mat = idx >> 8, row = (idx >> 1) & 127, half = idx & 1;
-      const int grow = (mat ? n1 : n0) + row;
-      u32x4 o[4];
-      if (grow < a.R) {
-        const int64_t r = (int64_t)e * a.R + grow;
-        const uint32_t *Wm = mat ? W1 : a.w0;
-        const uint16_t *Sm = mat ? S1 : a.s0;
-        const uint16_t *Bm = mat ? B1 : a.b0;
-        const u32x4 q = ldg16(Wm + r * KW + (k0 >> 3) + 4 * half);
-        const float s = A::to_f32(Sm[r * GPR + k0 / a.gs]);
-        const float b = A::to_f32(Bm[r * GPR + k0 / a.gs]);
+      for (int s = 0; s < 2; ++s) {
+        sc[s] = A::to_f32(gsc[s]);
+        bi[s] = A::to_f32(gbi[s]);
+      }
+    }
+    __syncthreads();
+  }
+
+  // C fragment of v_mfma_f32_32x32x16: lane l, register 4*q+j holds row
+  // 8*q + 4*(l/32) + j, column l%32
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const uint32_t qw = q[w];
+  for (int i = 0; i < 4; ++i) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float v0 = fmaf((float)((qw >> (8 * j)) & 0xFu), s, b);
-            const float v1 = fmaf((float)((qw >> (8 * j + 4)) & 0xFu), s, b);
-            o[w][j] = A::pack2(v0, v1);
-          }
+    for (int r = 0; r < 16; ++r) {
+      const int m = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+      if (m >= mcnt) continue;
+      uint16_t *op = a.out + (int64_t)s_orow[m] * a.out_ld;
+      if (DUAL) {
+        const int col = n0 + 32 * wv + l32;
+        if (col < R) {
+          const float gv = round_act<DT>(acc[0][i][r]);
+          const float uv = round_act<DT>(acc[1][i][r]);
+          op[col] = A::from_f32(gv / (1.0f + __expf(-gv)) * uv);
         }
       } else {
 #pragma unroll
-        for (int w = 0; w < 4; ++w) o[w] = u32x4{0, 0, 0, 0};
-      }
-      u32x4 *dst = (u32x4 *)(Bs + mat * BN * PITCH + row * PITCH + 32 * half);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) dst[w] = o[w];
-    }
-    __syncthreads();
-
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      u32x4 af[2], bf[2][2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *(const u32x4 *)(As + (64 * wm + 32 * i + l32) * PITCH + 16 * ks + 8 * kh);
-#pragma unroll
-      for (int m = 0; m < 2; ++m)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          bf[m][j] = *(const u32x4 *)(Bs + m * BN * PITCH + (64 * wn + 32 * j + l32) * PITCH +
-                                      16 * ks + 8 * kh);
-#pragma unroll
-      for (int m = 0; m < 2; ++m)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j) acc[m][i][j] = A::mfma32(af[i], bf[m][j], acc[m][i][j]);
-    }
-  }
-
-  // C fragment of v_mfma_f32_32x32x16: lane l, register 4*i+j holds
-  // row 8*i + 4*(l/32) + j, column l%32
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int nn = 64 * wn + 32 * j + l32;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
-        if (m >= mcnt) continue;
-        const int slot = m0 + m;
-        const int64_t orow = a.o_map ? a.o_map[slot] : slot;
-        uint16_t *op = a.out + orow * a.out_ld;
-        if (DUAL) {
-          if (n0 + nn < a.R) {
-            const float gv = round_act<DT>(acc[0][i][j][r]);
-            const float uv = round_act<DT>(acc[1][i][j][r]);
-            op[n0 + nn] = A::from_f32(gv / (1.0f + __expf(-gv)) * uv);
-          }
-        } else {
-          if (n0 + nn < a.R) op[n0 + nn] = A::from_f32(acc[0][i][j][r]);
-          if (n1 + nn < a.R) op[n1 + nn] = A::from_f32(acc[1][i][j][r]);
+        for (int s = 0; s < 2; ++s) {
+          const int col = n0 + 64 * wv + 32 * s + l32;
+          if (col < R) op[col] = A::from_f32(acc[s][i][r]);
         }
       }
     }
+  }
 }
 
 template <int DT>
 hipError_t launch_t(bool dual, const GroupedArgs &a, int64_t max_m_tiles, hipStream_t st) {
-  const int cols = dual ? BN : 2 * BN;
-  dim3 grid((unsigned)((a.R + cols - 1) / cols), (unsigned)max_m_tiles);
+  const int cols = dual ? WROWS / 2 : WROWS;
+  const int n_tiles = (a.R + cols - 1) / cols;
+  const int64_t total = max_m_tiles * n_tiles;
+  const unsigned grid = (unsigned)(8 * ((total + 7) / 8));
   if (dual)
-    hipLaunchKernelGGL((gemm_kernel<DT, true>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gemm_kernel<DT, true>), dim3(grid), dim3(256), kGemmLds, st, a, n_tiles);
   else
-    hipLaunchKernelGGL((gemm_kernel<DT, false>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gemm_kernel<DT, false>), dim3(grid), dim3(256), kGemmLds, st, a, n_tiles);
   return hipGetLastError();
 }
 
