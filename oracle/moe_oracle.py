@@ -60,6 +60,8 @@ Parity status (what pins each function; see tests/test_oracle.py):
 
 from __future__ import annotations
 
+import statistics
+
 import numpy as np
 
 ACT_DTYPES = ("float16", "bfloat16")
@@ -74,16 +76,44 @@ _PREC = {"float16": (11, -14), "bfloat16": (8, -126)}
 def round_act(v, act: str) -> np.ndarray:
     """Round float64 values to the activation dtype (RNE), returned as float64.
 
-    The rounding is done directly from float64 (no intermediate float32), by
-    scaling to the target ulp: both the scaling (a power of two) and ``rint``
-    (ties to even) are exact in float64.
+    The rounding is done directly from float64 (no intermediate float32):
+    on the bit pattern in the normal range, and below it by scaling to the
+    target ulp, where both the scaling (a power of two) and ``rint`` (ties to
+    even) are exact in float64.
     """
     v = np.asarray(v, dtype=np.float64)
     if act == "float16":
         return v.astype(np.float16).astype(np.float64)
     p, emin = _PREC[act]
-    out = np.zeros_like(v)
-    nz = v != 0
+    # Normal range: round-to-nearest-even on the float64 bit pattern.  The
+    # 52 - (p - 1) low mantissa bits are dropped; adding half an ulp minus one
+    # plus the kept lsb carries exactly when RNE rounds up (also into the
+    # exponent).  Values below the smallest normal take the scaling path.
+    drop = 52 - (p - 1)
+    if not v.flags.c_contiguous:
+        v = v.copy()
+    u = v.reshape(-1).view(np.uint64)
+    out = np.empty_like(v)
+    ou = out.reshape(-1).view(np.uint64)
+    half = np.uint64((1 << (drop - 1)) - 1)
+    keep = ~np.uint64((1 << drop) - 1)
+    step = 1 << 20  # chunks stay cache-resident on large weight tensors
+    for i in range(0, u.size, step):
+        c = u[i:i + step]
+        r = c >> np.uint64(drop)
+        r &= np.uint64(1)
+        r += c
+        r += half
+        r &= keep
+        ou[i:i + step] = r
+    big = np.abs(out) >= 2.0 ** 128  # past the largest bfloat16: overflow
+    if big.any():
+        out[big] = np.copysign(np.inf, v[big])
+    small = np.abs(v) < 2.0 ** emin
+    if not small.any():
+        return out
+    nz = small & (v != 0)
+    out[small & (v == 0)] = v[small & (v == 0)]
     e = np.floor(np.log2(np.abs(v[nz])))
     # guard against log2 rounding at exact powers of two
     m = np.abs(v[nz]) / np.exp2(e)
@@ -315,5 +345,47 @@ def make_inputs(seed: int, T: int, H: int, E: int, I: int, act: str, group_size:
         "gate": quantize(wg, group_size, 4, act),
         "up": quantize(wu, group_size, 4, act),
         "down": quantize(wd, group_size, 4, act),
+    }
+    return x, weights
+
+
+def random_packed(rng, shape, group_size: int, act: str, w_std: float = 0.02):
+    """Packed int4 weights of ``shape = (..., out, in)`` drawn directly in the
+    quantised domain with the statistics of quantised N(0, w_std) groups:
+    codes 7.5 + N(0, 1) * 15 / 4.8 rounded and clipped to [0, 15] (a 64-wide
+    normal group spans about 4.8 sigma), signed scales of that range over 15
+    steps and biases centring the codes, all act-representable.  Much cheaper
+    than quantising a float tensor at the 30B/235B expert shapes, and the same
+    layout."""
+    *lead, n_out, n_in = shape
+    # inverse-CDF table: a uniform byte picks the code of the normal quantile
+    # at its bin centre
+    nd = statistics.NormalDist()
+    table = np.array([min(15.0, max(0.0, round(7.5 + nd.inv_cdf((i + 0.5) / 256) * 15.0 / 4.8)))
+                      for i in range(256)], dtype=np.uint32)
+    q = table[rng.integers(0, 256, size=(*lead, n_out, n_in), dtype=np.uint8)]
+    wq = pack_nibbles(q)
+    gshape = (*lead, n_out, n_in // group_size)
+    mag = w_std * 4.8 / 15.0 * (1.0 + 0.1 * rng.standard_normal(gshape))
+    sign = np.where(rng.random(gshape) < 0.5, -1.0, 1.0)
+    scales = round_act(mag * sign, act)
+    biases = round_act(-7.5 * scales + w_std * 0.05 * rng.standard_normal(gshape), act)
+    return wq, scales, biases
+
+
+def make_packed_inputs(seed: int, T: int, H: int, E: int, I: int, act: str,
+                       group_size: int = 64, w_std: float = 0.02, x_std: float = 1.0,
+                       router_std: float = 0.02):
+    """Like :func:`make_inputs`, with the expert weights drawn by
+    :func:`random_packed` (the router is still quantised from N(0, router_std)
+    so routing follows the reference's quantizer)."""
+    rng = np.random.default_rng(seed)
+    x = round_act(rng.standard_normal((T, H)) * x_std, act)
+    wr = round_act(rng.standard_normal((E, H)) * router_std, act)
+    weights = {
+        "router": quantize(wr, group_size, 4, act),
+        "gate": random_packed(rng, (E, I, H), group_size, act, w_std),
+        "up": random_packed(rng, (E, I, H), group_size, act, w_std),
+        "down": random_packed(rng, (E, H, I), group_size, act, w_std),
     }
     return x, weights

@@ -177,6 +177,10 @@ def test_grouped_expert_linear_matches_oracle(regime, n, D, O_, E, act):
 
 
 def _moe_case(seed, T, H, E, I, act, gs=64):
+    if E * I * H > (1 << 24):
+        # 30B/235B expert shapes: weights drawn in the packed domain (seconds
+        # instead of minutes of float quantisation)
+        return O.make_packed_inputs(seed, T, H, E, I, act, gs)
     return O.make_inputs(seed, T, H, E, I, act, gs)
 
 
