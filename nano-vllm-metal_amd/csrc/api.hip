@@ -40,7 +40,7 @@ int fail(int code, const char *fmt, ...) {
 
 constexpr int64_t kMaxExperts = nvm::kMaxExperts;
 constexpr int kMaxTopK = 64;
-// the decode products stage 8 activation rows of length K in LDS
+// reduction dimensions the product kernels are built and tested for
 constexpr int64_t kMaxProductK = 8192;
 
 // Bump allocator over the caller's workspace (256-byte aligned slices).
@@ -65,7 +65,10 @@ int check_quant(int group_size, int bits, int dtype) {
   return NVM_OK;
 }
 
-bool use_decode(int regime, int64_t pairs, int64_t E) {
+// Decode GEMV or prefill GEMM for `pairs` routed rows over E experts with a
+// reduction dimension of K.  Shapes the GEMV does not tile run on the GEMM.
+bool use_decode(int regime, int64_t pairs, int64_t E, int64_t K) {
+  if (!nvm::gemv_supports((int)K)) return false;
   if (regime == NVM_REGIME_DECODE) return true;
   if (regime == NVM_REGIME_PREFILL) return false;
   return pairs <= 8 * E;  // up to 8 routed rows per expert on average
@@ -253,7 +256,7 @@ int nvm_grouped_expert_linear(const void *x, int64_t n, int64_t D, const uint32_
   g.out = (uint16_t *)out;
   g.o_map = sorted;
   g.out_ld = O;
-  return run_products(dtype, use_decode(regime, n, E), false, g, n, st);
+  return run_products(dtype, use_decode(regime, n, E, D), false, g, n, st);
 }
 
 int nvm_moe_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, size_t *bytes) {
@@ -294,7 +297,7 @@ int nvm_moe_expert_gateup(const void *x, int64_t T, int64_t H, int64_t I, int64_
   g.o_map = nullptr;
   g.out_ld = I;
   const int64_t N = T * top_k;
-  return run_products(dtype, use_decode(regime, N, E), true, g, N, (hipStream_t)stream);
+  return run_products(dtype, use_decode(regime, N, E, H), true, g, N, (hipStream_t)stream);
 }
 
 int nvm_moe_expert_down(const void *h, int64_t n_pairs, int64_t H, int64_t I, int64_t E,
@@ -324,7 +327,7 @@ int nvm_moe_expert_down(const void *h, int64_t n_pairs, int64_t H, int64_t I, in
   d.out = (uint16_t *)down;
   d.o_map = sorted_pairs;
   d.out_ld = H;
-  return run_products(dtype, use_decode(regime, n_pairs, E), false, d, n_pairs,
+  return run_products(dtype, use_decode(regime, n_pairs, E, I), false, d, n_pairs,
                       (hipStream_t)stream);
 }
 

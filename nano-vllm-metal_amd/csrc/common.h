@@ -135,6 +135,31 @@ __device__ __forceinline__ u32x4 pair_order(u32x4 d) {
 // Expand one packed word (codes q0..q7 at bits 4j) into four dwords of
 // 16-bit floats (M+q0, M+q4)(M+q1, M+q5)(M+q2, M+q6)(M+q3, M+q7), exactly,
 // where M is the dtype's magic constant (128 for bf16, 1024 for fp16).
+// With `mask` = 0x000F000F in an SGPR and `magic` (two copies of M) in a VGPR,
+// each dword is one v_and_or_b32 (after a shift for the upper three): gfx9
+// VOP3 encodings take no literal and read at most one SGPR, so with both
+// constants as literals the compiler would emit an AND and an OR.
+__device__ __forceinline__ u32x4 nibble_pairs_v(uint32_t w, uint32_t mask, uint32_t magic) {
+  u32x4 o;
+  o.x = (w & mask) | magic;
+  o.y = ((w >> 4) & mask) | magic;
+  o.z = ((w >> 8) & mask) | magic;
+  o.w = ((w >> 12) & mask) | magic;
+  return o;
+}
+// The constants above as register values the compiler cannot fold back into
+// literals (each is one move; only ordinary VALU/SALU code consumes them).
+__device__ __forceinline__ uint32_t sgpr_const(uint32_t v) {
+  uint32_t r;
+  asm volatile("s_mov_b32 %0, %1" : "=s"(r) : "i"(v));
+  return r;
+}
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(v));
+  return r;
+}
+
 template <int DT>
 __device__ __forceinline__ u32x4 nibble_pairs(uint32_t w) {
   constexpr uint32_t m = Act<DT>::kMagic2;

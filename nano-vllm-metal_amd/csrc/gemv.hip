@@ -4,29 +4,44 @@
 // for decode-sized batches, fused with SwiGLU (layers/moe.py:84,
 // layers/activation.py:21-24) for the gate/up pair.
 //
-// Weight bytes dominate, so each expert's rows are streamed from HBM once and
-// applied to every row routed to that expert (up to 16 per pass).  The inner
-// product runs on the matrix cores without rounding the weights: a 4-bit code
-// q becomes the exact 16-bit float M+q (M = 128 for bf16, 1024 for fp16) by
-// OR-ing it into a constant, v_mfma_f32_16x16x32 accumulates x.(M+q) over one
-// 64-wide quantisation group, and the group is folded in float32 as
+// Weight bytes dominate, so the kernel is shaped to stream them at HBM rate:
+//
+// * Work units are (expert, chunk of up to 16 routed rows, tile of 16*NT
+//   weight rows).  The unit list of all active experts is derived on the
+//   device from the expert offsets, and a persistent grid deals every block a
+//   contiguous, equal share of it: every block moves the same number of
+//   bytes, and consecutive units of a block share their routed rows.
+// * Inside a block the wavefronts split the reduction dimension: wavefront w
+//   owns k-slice w % KS (GPW 64-wide quantisation groups) of weight-row tile
+//   w / KS, so all wavefronts move the same bytes per unit.  The KS partial
+//   sums of a tile meet in LDS once per unit (double-buffered: one barrier per
+//   unit) and are summed in k-slice order.
+// * Each wavefront keeps DEPTH units of its weights (and their scales and
+//   biases) in flight in a register ring that runs across unit boundaries, so
+//   the memory pipe never drains between units.
+//
+// Exact inner products on the matrix cores.  A 4-bit code q becomes the exact
+// 16-bit float M+q (M = 128 for bf16, 1024 for fp16) by OR-ing it into a
+// constant; v_mfma_f32_16x16x32 accumulates x.(M+q) over one 64-wide group,
+// and the group is folded as
 //   sum_i x_i w_i = s * sum_i x_i (M + q_i) + (b - M s) * sum_i x_i,
-// which is the reference's w = q*s + b (metal/src/quantized_matmul.cpp:135).
+// the reference's w = q*s + b (metal/src/quantized_matmul.cpp:135) without
+// ever rounding a weight.  The scale term is one FMA per accumulator and
+// group; the bias terms of four groups are one v_mfma_f32_16x16x4_f32 whose A
+// operand holds the 64-wide group sums of the routed rows.
 //
-// MFMA roles (16x16x32): A = activations [16 rows x 32 k], B = weights
-// [32 k x 16 output features], C[row][feature].  Lane l = (c, G), c = l%16,
+// MFMA roles (16x16x32): A = routed rows [16 x 32 k], B = weights [32 k x 16
+// weight rows], C[routed row][weight row].  Lane l = (c, G), c = l%16,
 // G = l/16, supplies A row c and B column c for k-slots 8G..8G+7 and holds C
-// rows 4G..4G+3 of column c.
-//
-// Memory shape: lane (c, G) loads 16 contiguous bytes (4 packed words) of
-// weight row c per load, so the four lane groups read 64 contiguous bytes of
-// each of 16 rows -- two quantisation groups.  Lane groups 0-1 then hold the
-// first group and 2-3 the second, so each word position feeds two MFMAs, one
-// whose activation operand is zero in lane groups 2-3 (first group) and one
-// zero in lane groups 0-1 (second group).  The activations of the block's
-// routed rows are staged once per block in LDS, already in the pair order of
-// nibble_pairs(), together with their 64-wide group sums; masked lanes read a
-// row of zeros, so the masking costs no arithmetic.
+// rows 4G..4G+3 of column c.  Per pair of groups (64 bytes of a weight row),
+// lane group G loads the 16 bytes at 16G: lane groups 0-1 hold the first
+// group, 2-3 the second.  One v_permlane32_swap per two words trades words 2-3
+// of the lower half-wave for words 0-1 of the upper one (swap_pairs), after
+// which word j of every lane belongs to group j/2, so each MFMA step stays
+// inside one group.  The A operand of the lane holds the matching activations,
+// permuted once per chunk into the pair order that nibble_pairs() produces.
+#include <algorithm>
+
 #include "common.h"
 #include "internal.h"
 
@@ -34,29 +49,18 @@ namespace nvm {
 
 namespace {
 
-constexpr int GI = 4;  // 64-wide groups per pipeline stage: one 128-byte line per row
+constexpr int kChunk = 16;  // routed rows per chunk (MFMA rows)
+constexpr int kMaxNW = 8;   // wavefronts per block
 
-// Scales and biases.  SB_ROW: each lane loads 16 bytes (8 values) of its
-// row's scales and biases once per tile -- lane group G holds scale groups
-// 8G..8G+7 -- and the stage fetches the value it needs from the holding lane
-// with ds_bpermute.  Needs rows of an even number of scale groups (4-byte
-// aligned rows) and at most 32 of them.  SB_PER_GROUP: 16-bit loads per group
-// and stage, for the remaining shapes.
-enum { SB_PER_GROUP = 0, SB_ROW = 1 };
-
-// Routed rows staged per pass (MFMA rows CH..15 stay zero).  Experts with
-// more routed rows take further passes over their weights.
-constexpr int CH = 8;
-
-// LDS bytes of a block: CH+1 activation rows (CH routed rows + one of zeros)
-// of K/8+1 sixteen-byte chunks (the extra chunk staggers the banks of
-// consecutive rows), CH group sums per 64-wide group, and 512 bytes of slack
-// that a short last stage (K not a multiple of 256) may read past the end.
-__host__ __device__ constexpr int gemv_lds_bytes(int K) {
-  return (CH + 1) * (K / 8 + 1) * 16 + (K / 64) * CH * 4 + 512;
-}
-// LDS per workgroup on gfx950 is 160 KiB; 4 KiB stay for static LDS
-constexpr int kMaxLds = 156 * 1024;
+// Register budget: resident wavefronts per SIMD (2 -> 256 VGPRs each) and the
+// VGPRs of the weight ring.
+#ifndef NVM_GEMV_WAVES_PER_SIMD
+#define NVM_GEMV_WAVES_PER_SIMD 2
+#endif
+#ifndef NVM_GEMV_RING
+#define NVM_GEMV_RING 72
+#endif
+constexpr int kWavesPerSimd = NVM_GEMV_WAVES_PER_SIMD;
 
 // Compute units of the current device (cached per device).
 int cu_count() {
@@ -72,324 +76,408 @@ int cu_count() {
   return cached[dev];
 }
 
-// Persistent grid: block b walks a contiguous share of the work items
-// (active expert, 64*NT-row block) in expert order, so the activation rows of
-// an expert are staged once per block and the grid drains evenly.
-template <int DT, bool DUAL, int NT, int SB>
-__global__ __launch_bounds__(256, 3) void gemv_kernel(const GroupedArgs a) {
-  using A = Act<DT>;
-  constexpr int NM = DUAL ? 2 : 1;
-  constexpr int ROWS = 4 * 16 * NT;  // output rows of one work item
-  extern __shared__ __attribute__((aligned(16))) u32x4 xl[];
-  __shared__ int s_act[kMaxExperts];  // active experts, ascending
-  __shared__ int s_nact;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+// Scale or bias values of one weight row over the k-slice, read as an
+// aligned window: the 16-bit value for group g of the slice is half
+// sb_index(g) of the window (a few values on either side are read and unused).
+template <int GPW>
+struct SbVec {
+  typedef u32x2 type;  // 4 values: enough for slices of up to 3 groups
+};
+template <>
+struct SbVec<4> {
+  typedef u32x2 type;  // 4 values, 8-byte aligned (see sb window below)
+};
+template <>
+struct SbVec<6> {
+  typedef u32x4 type;
+};
+template <>
+struct SbVec<8> {
+  typedef u32x4 type;
+};
 
-  const int col = lane & 15, G = lane >> 4;
-  const int KW = a.K >> 3, KG = a.K >> 6, GPR = a.K / a.gs;
-  const int gsh = a.gs == 128 ? 1 : 0;
-  const int pitch = KW + 1;  // LDS row pitch in 16-byte chunks
-  const int zero_row = CH * pitch;
-  float *sxl = (float *)(xl + (CH + 1) * pitch);  // [KG][CH]
+__device__ __forceinline__ void load_sb(rsrc_t r, int voff, u32x2 &v) { v = bload8(r, voff, 0); }
+__device__ __forceinline__ void load_sb(rsrc_t r, int voff, u32x4 &v) { v = bload16(r, voff, 0); }
 
-  for (int i = tid; i < pitch; i += blockDim.x) xl[zero_row + i] = u32x4{0, 0, 0, 0};
-  if (wv == 0) {
-    int base = 0;
-    for (int c0 = 0; c0 < a.E; c0 += 64) {
-      const int e = c0 + lane;
-      const bool act = e < a.E && a.offsets[e + 1] > a.offsets[e];
-      const uint64_t m = __ballot(act);
-      if (act) s_act[base + __popcll(m & ((1ull << lane) - 1ull))] = e;
-      base += __popcll(m);
-    }
-    if (lane == 0) s_nact = base;
-  }
-  __syncthreads();
-  const int RBPE = (a.R + ROWS - 1) / ROWS;
-  const int W = s_nact * RBPE;
-  const int i0 = (int)((int64_t)blockIdx.x * W / gridDim.x);
-  const int i1 = (int)((int64_t)(blockIdx.x + 1) * W / gridDim.x);
-  const int NS = (KG + GI - 1) / GI;
-  int staged_e = -1, staged_nc = -1;
-
-  for (int item = i0; item < i1; ++item) {
-  const int e = s_act[item / RBPE];
-  const int r0 = (item % RBPE) * ROWS + wv * 16 * NT;
-  const bool wave_rows = r0 < a.R;
-  const int nb = a.offsets[e], ne = a.offsets[e + 1];
-
-  rsrc_t wr[NM], sr[NM], br[NM];
-#pragma unroll
-  for (int m = 0; m < NM; ++m) {
-    const int64_t eo = (int64_t)e * a.R;
-    wr[m] = make_rsrc((m ? a.w1 : a.w0) + eo * KW, (uint32_t)(a.R * KW * 4));
-    sr[m] = make_rsrc((m ? a.s1 : a.s0) + eo * GPR, (uint32_t)(a.R * GPR * 2));
-    br[m] = make_rsrc((m ? a.b1 : a.b0) + eo * GPR, (uint32_t)(a.R * GPR * 2));
-  }
-  int wo[NT], so[NT];
-  bool tv[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    tv[t] = r0 + 16 * t < a.R;
-    const int row = r0 + 16 * t + col;
-    wo[t] = tv[t] ? (row * KW + 4 * G) * 4 : kMaskedOffset;
-    so[t] = tv[t] ? row * GPR * 2 : kMaskedOffset;
-  }
-
-  // one pipeline stage = 4 groups: two 16-byte loads per (matrix, row tile);
-  // with SB_PER_GROUP also the stage's scales/biases, packed (value of group
-  // gi in half (gi & 1) of dword gi >> 1)
-  struct Stage {
-    u32x4 q[NM][NT][2];
-    u32x2 s[NM][NT], b[NM][NT];
-  };
-  auto load = [&](int st_idx, Stage &st) {
-    const int ws = __builtin_amdgcn_readfirstlane(128 * st_idx);
-#pragma unroll
-    for (int m = 0; m < NM; ++m)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        st.q[m][t][0] = bload16(wr[m], wo[t], ws);
-        st.q[m][t][1] = bload16(wr[m], wo[t] + 64, ws);
-        if constexpr (SB == SB_PER_GROUP) {
-          uint32_t sv[GI], bv[GI];
-#pragma unroll
-          for (int gi = 0; gi < GI; ++gi) {
-            sv[gi] = bload2(sr[m], so[t] + 2 * ((GI * st_idx + gi) >> gsh), 0);
-            bv[gi] = bload2(br[m], so[t] + 2 * ((GI * st_idx + gi) >> gsh), 0);
-          }
-          st.s[m][t] = u32x2{sv[0] | (sv[1] << 16), sv[2] | (sv[3] << 16)};
-          st.b[m][t] = u32x2{bv[0] | (bv[1] << 16), bv[2] | (bv[3] << 16)};
-        }
-      }
-  };
-  // SB_ROW: the tile's scales/biases, resident for the whole wavefront
-  u32x4 srow[NM][NT], brow[NM][NT];
-  if constexpr (SB == SB_ROW) {
-#pragma unroll
-    for (int m = 0; m < NM; ++m)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        srow[m][t] = bload16(sr[m], so[t] + 16 * G, 0);
-        brow[m][t] = bload16(br[m], so[t] + 16 * G, 0);
-      }
-  }
-  // dword holding the scale/bias values of 64-wide groups (g, g + 1), g even:
-  // both share one 32-bit word of the resident row (group 64) or are the same
-  // value (group 128, duplicated into both halves)
-  auto sb_pair = [&](const u32x4 &row, int g) -> uint32_t {
-    const int sg = g >> gsh;  // scale group of g
-    const int src = col + 16 * (sg >> 3);
-    const int w = (sg & 7) >> 1;
-    const uint32_t mine = w == 0 ? row.x : w == 1 ? row.y : w == 2 ? row.z : row.w;
-    const uint32_t d = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)mine);
-    if (gsh == 0) return d;
-    const uint32_t h = (sg & 1) ? (d >> 16) : (d & 0xFFFFu);
-    return h * 0x10001u;
-  };
-
-  const int rot = __builtin_amdgcn_readfirstlane(
-      (int)((item * 4u + wv + 3u * e) % (unsigned)NS));
-  auto st_at = [&](int i) {
-    const int st = rot + i;
-    return st >= NS ? st - NS : st;
-  };
-
-  for (int nc = nb; nc < ne; nc += CH) {
-    const int cnt = min(CH, ne - nc);
-    // the first two weight stages do not depend on the activations: issue
-    // them before staging so their latency overlaps the staging
-    Stage sa, sb, sc;
-    if (wave_rows) {
-      load(st_at(0), sa);
-      if (NS > 1) load(st_at(1), sb);
-    }
-    if (e != staged_e || nc != staged_nc) {
-    staged_e = e;
-    staged_nc = nc;
-    __syncthreads();  // every wavefront is done with the previous rows
-    // stage the routed activation rows (pair order) and their group sums
-    for (int it = tid; it < cnt * KW; it += blockDim.x) {
-      const int c = it / KW, ch = it - c * KW;
-      const int arow = a.a_map ? a.a_map[nc + c] / a.a_div : nc + c;
-      const u32x4 v = ldg16(a.act + (int64_t)arow * a.act_ld + 8 * ch);
-      xl[c * pitch + ch] = pair_order(v);
-      float sx = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sx = A::dot2(v[i], A::kOne2, sx);
-      // 8 consecutive items (lanes) form one 64-wide group
-      sx += __shfl_xor(sx, 1);
-      sx += __shfl_xor(sx, 2);
-      sx += __shfl_xor(sx, 4);
-      if ((ch & 7) == 0) sxl[(ch >> 3) * CH + c] = sx;
-    }
-    __syncthreads();
-    }
-    if (!wave_rows) continue;
-
-    const bool tok_ok = col < cnt;
-    const int lo_base = (tok_ok && G < 2) ? col * pitch + 4 * G : zero_row + 4 * G;
-    const int hi_base = (tok_ok && G >= 2) ? col * pitch + 4 * G : zero_row + 4 * G;
-
-    f32x4 o[NM][NT];
-#pragma unroll
-    for (int m = 0; m < NM; ++m)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) o[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // ng = valid groups of the stage (GI except in a short last stage)
-    auto compute = [&](int st_idx, const Stage &st, int ng) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        if (2 * j >= ng) break;
-        const bool has_b = 2 * j + 1 < ng;
-        const int cbase = 32 * st_idx + 16 * j;
-        f32x4 acc_a[NM][NT], acc_b[NM][NT];
-#pragma unroll
-        for (int m = 0; m < NM; ++m)
-#pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            acc_a[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-            acc_b[m][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-          }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const u32x4 alo = xl[lo_base + cbase + k];
-          const u32x4 ahi = xl[hi_base + cbase + k];
-#pragma unroll
-          for (int m = 0; m < NM; ++m)
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-              if (!tv[t]) continue;
-              const u32x4 bq = nibble_pairs<DT>(st.q[m][t][j][k]);
-              acc_a[m][t] = A::mfma16(alo, bq, acc_a[m][t]);
-              acc_b[m][t] = A::mfma16(ahi, bq, acc_b[m][t]);
-            }
-        }
-        // group sums of the lane's C rows 4G..4G+3 (rows >= CH are never stored)
-        const int ga = GI * st_idx + 2 * j;
-        const int gq = min(4 * G, CH - 4);
-        const f32x4 sxa = *(const f32x4 *)(sxl + ga * CH + gq);
-        const f32x4 sxb = *(const f32x4 *)(sxl + (ga + 1) * CH + gq);
-#pragma unroll
-        for (int m = 0; m < NM; ++m)
-#pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            if (!tv[t]) continue;
-            uint32_t sd, bd;
-            if constexpr (SB == SB_ROW) {
-              sd = sb_pair(srow[m][t], ga);
-              bd = sb_pair(brow[m][t], ga);
-            } else {
-              sd = st.s[m][t][j];
-              bd = st.b[m][t][j];
-            }
-            const float s0 = A::lo(sd), b0 = A::lo(bd);
-            const float bp0 = fmaf(-A::kMagic, s0, b0);
-#pragma unroll
-            for (int v = 0; v < 4; ++v) o[m][t][v] = fmaf(s0, acc_a[m][t][v], fmaf(bp0, sxa[v], o[m][t][v]));
-            if (has_b) {
-              const float s1 = A::hi(sd), b1 = A::hi(bd);
-              const float bp1 = fmaf(-A::kMagic, s1, b1);
-#pragma unroll
-              for (int v = 0; v < 4; ++v)
-                o[m][t][v] = fmaf(s1, acc_b[m][t][v], fmaf(bp1, sxb[v], o[m][t][v]));
-            }
-          }
-      }
-    };
-
-    // Three stage buffers in rotation keep two stages of weights in flight
-    // while one is multiplied; nothing is copied between buffers.  Every pass
-    // of the main loop issues the same loads, which lets the compiler wait
-    // only for the stage about to be used.  Wavefronts start at different
-    // stages of their rows so that concurrent wavefronts do not sweep the
-    // same column offsets (and memory channels) in lockstep.
-    auto run = [&](int i, const Stage &st) { compute(st_at(i), st, min(GI, KG - GI * st_at(i))); };
-    int i = 0;
-    for (; i + 4 < NS; i += 3) {
-      load(st_at(i + 2), sc);
-      run(i, sa);
-      load(st_at(i + 3), sa);
-      run(i + 1, sb);
-      load(st_at(i + 4), sb);
-      run(i + 2, sc);
-    }
-    // 1 to 4 stages remain: sa holds stage i, sb stage i + 1
-    if (i + 2 < NS) load(st_at(i + 2), sc);
-    run(i, sa);
-    if (i + 1 < NS) {
-      if (i + 3 < NS) load(st_at(i + 3), sa);
-      run(i + 1, sb);
-      if (i + 2 < NS) run(i + 2, sc);
-      if (i + 3 < NS) run(i + 3, sa);
-    }
-
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      if (!tv[t]) continue;
-      const int rowc = r0 + 16 * t + col;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int tok = 4 * G + v;
-        if (tok >= cnt) continue;
-        const int n = nc + tok;
-        const int64_t orow = a.o_map ? a.o_map[n] : n;
-        uint16_t r;
-        if (DUAL) {
-          // reference rounding points: gate and up outputs are act tensors,
-          // silu(gate) * up is rounded once more
-          const float gv = round_act<DT>(o[0][t][v]);
-          const float uv = round_act<DT>(o[NM - 1][t][v]);
-          r = A::from_f32(gv / (1.0f + __expf(-gv)) * uv);
-        } else {
-          r = A::from_f32(o[0][t][v]);
-        }
-        a.out[orow * a.out_ld + rowc] = r;
-      }
-    }
-  }
-  }
+// 16-bit value `idx` of the window (idx may differ between lanes).
+__device__ __forceinline__ uint32_t sb_at(const u32x2 &v, int idx) {
+  const uint32_t d = (idx >> 1) ? v.y : v.x;
+  return (idx & 1) ? (d >> 16) : (d & 0xFFFFu);
+}
+__device__ __forceinline__ uint32_t sb_at(const u32x4 &v, int idx) {
+  const int w = idx >> 1;
+  const uint32_t d = w == 0 ? v.x : w == 1 ? v.y : w == 2 ? v.z : v.w;
+  return (idx & 1) ? (d >> 16) : (d & 0xFFFFu);
 }
 
-template <int DT, bool DUAL, int NT>
-hipError_t launch_nt(const GroupedArgs &a, int sb_mode, hipStream_t st) {
-  constexpr int WAVES = 4;
-  const int rows_per_block = 16 * NT * WAVES;
-  // work items can number at most E * ceil(R / rows); three blocks per CU
-  // are resident at once (register-limited), so launch no more than that
-  const int64_t items = (int64_t)a.E * ((a.R + rows_per_block - 1) / rows_per_block);
-  dim3 grid((unsigned)std::min<int64_t>(items, 3 * (int64_t)cu_count()));
-  const size_t lds = gemv_lds_bytes(a.K);
-  if (lds > (size_t)kMaxLds) return hipErrorInvalidValue;
-  // allow dynamic LDS beyond the 64 KiB default (once per instantiation)
-  static const hipError_t attr[2] = {
-      hipFuncSetAttribute((const void *)gemv_kernel<DT, DUAL, NT, SB_PER_GROUP>,
-                          hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds),
-      hipFuncSetAttribute((const void *)gemv_kernel<DT, DUAL, NT, SB_ROW>,
-                          hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds)};
-  for (hipError_t e : attr)
-    if (e != hipSuccess) return e;
-  if (sb_mode == SB_ROW)
-    hipLaunchKernelGGL((gemv_kernel<DT, DUAL, NT, SB_ROW>), grid, dim3(64 * WAVES), lds, st, a);
-  else
-    hipLaunchKernelGGL((gemv_kernel<DT, DUAL, NT, SB_PER_GROUP>), grid, dim3(64 * WAVES), lds,
-                       st, a);
+// Words (w0, w1, w2, w3) of a 16-byte load in lane group G hold codes
+// 32G + 8j.. of a 128-code group pair.  Exchanging the lower half-wave's
+// words 2-3 with the upper half-wave's words 0-1 leaves every lane with words
+// 0-1 from the first group and words 2-3 from the second: lane group G then
+// holds codes 32(G%2) + 16(G/2) + {0, 8} (first group) and 64 + the same
+// (second group).
+__device__ __forceinline__ u32x4 swap_pairs(u32x4 w) {
+  // v_permlane32_swap: lanes 32-63 of the first operand trade places with
+  // lanes 0-31 of the second
+  const auto a = __builtin_amdgcn_permlane32_swap(w.x, w.z, false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(w.y, w.w, false, false);
+  return u32x4{a[0], b[0], a[1], b[1]};
+}
+
+template <bool DUAL, int GPW>
+struct GemvCfg {
+  static constexpr int NM = DUAL ? 2 : 1;  // weight matrices per unit
+  static constexpr int SBW = sizeof(typename SbVec<GPW>::type) / 4;
+  // VGPRs of one unit in the ring; DEPTH units make about RING
+  static constexpr int UNIT_VGPRS = NM * (2 * GPW + 2 * SBW);  // GPW/2 16-byte loads
+  static constexpr int RING = NVM_GEMV_RING;
+  static constexpr int DEPTH =
+      RING / UNIT_VGPRS < 2 ? 2 : (RING / UNIT_VGPRS > 8 ? 8 : RING / UNIT_VGPRS);
+  static constexpr int NB = (GPW + 3) / 4;  // bias MFMAs (four groups each)
+};
+
+template <int DT, bool DUAL, int GPW>
+__global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
+    const GroupedArgs a, int KS, int NT) {
+  using A = Act<DT>;
+  using Cfg = GemvCfg<DUAL, GPW>;
+  constexpr int NM = Cfg::NM, DEPTH = Cfg::DEPTH, NB = Cfg::NB;
+  typedef typename SbVec<GPW>::type SB;
+
+  __shared__ int s_off[kMaxExperts + 1];  // slot offsets of the experts
+  __shared__ int s_cb[kMaxExperts + 1];   // first chunk index of each expert
+  __shared__ int s_orow[2][kChunk];  // output rows of the unit's routed rows
+  __shared__ float s_red[2][kMaxNW][NM][4][64];
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int NW = blockDim.x >> 6;
+  const int col = lane & 15, G = lane >> 4;
+  const int E = a.E, R = a.R, KW = a.K >> 3, GPR = a.K / a.gs;
+  const int gsh = a.gs == 128 ? 1 : 0;
+
+  if (wv == 0) {
+    int carry = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + lane;
+      int n = 0;
+      if (e < E) {
+        const int o0 = a.offsets[e];
+        s_off[e] = o0;
+        n = (a.offsets[e + 1] - o0 + kChunk - 1) / kChunk;
+      }
+      int inc = n;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(inc, o);
+        if (lane >= o) inc += u;
+      }
+      if (e < E) s_cb[e] = carry + inc - n;
+      carry += __shfl(inc, 63);
+    }
+    if (lane == 0) {
+      s_off[E] = a.offsets[E];
+      s_cb[E] = carry;
+    }
+  }
+  __syncthreads();
+
+  const int rows_unit = 16 * NT;
+  const int RT = (R + rows_unit - 1) / rows_unit;
+  const int U = s_cb[E] * RT;
+  const int u0 = (int)((int64_t)blockIdx.x * U / gridDim.x);
+  const int u1 = (int)((int64_t)(blockIdx.x + 1) * U / gridDim.x);
+  const int nu = u1 - u0;
+  if (nu <= 0) return;  // uniform over the block, before any further barrier
+
+  const int ks = wv % KS, tile = wv / KS;
+
+  // ---- unit iterator (uniform): chunk it_ci of expert it_e, row tile it_rt
+  int it_ci = u0 / RT;
+  int it_rt = u0 - it_ci * RT;
+  int it_e;
+  {
+    // largest expert whose first chunk is <= it_ci (an empty expert shares its
+    // first chunk with the next one, so the search lands on a non-empty one)
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (__builtin_amdgcn_readfirstlane(s_cb[mid]) <= it_ci)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    it_e = lo;
+  }
+  auto advance = [&]() {
+    if (++it_rt == RT) {
+      it_rt = 0;
+      ++it_ci;
+      while (it_e + 1 < E && __builtin_amdgcn_readfirstlane(s_cb[it_e + 1]) <= it_ci) ++it_e;
+    }
+  };
+
+  // ---- register ring: weights, scales and biases of DEPTH units
+  constexpr int GP = GPW / 2;  // 16-byte loads (group pairs) per row and k-slice
+  u32x4 wq[DEPTH][NM][GP];
+  SB sv[DEPTH][NM], bv[DEPTH][NM];
+  int m_e[DEPTH], m_ci[DEPTH], m_r0[DEPTH];
+
+  const int kbyte = ks * GPW * 32;              // k-slice start within a row (bytes)
+  const int sidx0 = (ks * GPW) >> gsh;          // first scale value of the k-slice
+  const uint32_t mat_bytes = (uint32_t)R * KW * 4;
+  const uint32_t sb_bytes = (uint32_t)R * GPR * 2;
+  // Every ring refill issues the same loads: a unit past the block's range
+  // reads through masked offsets (zeros, no memory traffic), so the number of
+  // loads in flight after any ring slot is the same on every path and the
+  // compiler's wait counts keep DEPTH - 1 units in flight.
+  auto issue = [&](int d, bool valid) {
+    const int e = it_e, r0 = it_rt * rows_unit;
+    m_e[d] = e;
+    m_ci[d] = it_ci;
+    m_r0[d] = r0;
+    const int row = r0 + 16 * tile + col;
+    const bool ok = valid && row < R;
+    const int wo = ok ? row * KW * 4 + kbyte + 16 * G : kMaskedOffset;
+    const int sbyte = (row * GPR + sidx0) * 2;
+    const int so = ok ? (sbyte & ~3) : kMaskedOffset;  // dword-aligned window
+    const int64_t eo = (int64_t)e * R;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      const rsrc_t wr = make_rsrc((m ? a.w1 : a.w0) + eo * KW, mat_bytes);
+#pragma unroll
+      for (int h = 0; h < GP; ++h) wq[d][m][h] = bload16(wr, wo + 64 * h, 0);
+      load_sb(make_rsrc((m ? a.s1 : a.s0) + eo * GPR, sb_bytes), so, sv[d][m]);
+      load_sb(make_rsrc((m ? a.b1 : a.b0) + eo * GPR, sb_bytes), so, bv[d][m]);
+    }
+    if (valid) advance();
+  };
+
+  // ---- activation operand of the current chunk
+  u32x4 xa[GP][4];
+  float xb[NB];
+  int cur_ci = -1, cur_slot0 = 0, cur_cnt = 0, my_orow = 0;
+  const rsrc_t act_r = make_rsrc(a.act, (uint32_t)(a.act_rows * a.act_ld * 2));
+  auto load_act = [&](int e, int ci) {
+    const int slot0 =
+        __builtin_amdgcn_readfirstlane(s_off[e]) +
+        (ci - __builtin_amdgcn_readfirstlane(s_cb[e])) * kChunk;
+    const int cnt = min(kChunk, __builtin_amdgcn_readfirstlane(s_off[e + 1]) - slot0);
+    cur_slot0 = slot0;
+    cur_cnt = cnt;
+    int arow = -1;
+    if (col < cnt) {
+      const int sl = slot0 + col;
+      arow = a.a_map ? a.a_map[sl] / a.a_div : sl;
+      my_orow = a.o_map ? a.o_map[sl] : sl;
+    }
+    // step s of group pair h covers codes 128h + 64(s/2) + 32(G%2) + 16(G/2)
+    // + 8(s%2) + 0..7 of the k-slice in lane group G (see swap_pairs)
+    const int ao = arow >= 0 ? (int)((int64_t)arow * a.act_ld * 2) +
+                                   (ks * GPW * 64 + 32 * (G & 1) + 16 * (G >> 1)) * 2
+                             : kMaskedOffset;
+    float ps[GPW];
+#pragma unroll
+    for (int h = 0; h < GP; ++h) {
+      ps[2 * h] = 0.f;
+      ps[2 * h + 1] = 0.f;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const u32x4 v = bload16(act_r, ao + (128 * h + 64 * (st >> 1) + 8 * (st & 1)) * 2, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ps[2 * h + (st >> 1)] = A::dot2(v[i], A::kOne2, ps[2 * h + (st >> 1)]);
+        xa[h][st] = pair_order(v);
+      }
+    }
+    // 64-wide group sums of routed row c, in every lane of column c
+#pragma unroll
+    for (int g = 0; g < GPW; ++g) {
+      ps[g] += __shfl_xor(ps[g], 16);
+      ps[g] += __shfl_xor(ps[g], 32);
+    }
+    // bias-MFMA A operand: lane (c, G) holds the sum of group 4b + G of row c
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float v = 0.f;
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        if (4 * b + g < GPW && G == g) v = ps[4 * b + g];
+      xb[b] = v;
+    }
+  };
+
+  // window position of group g of the slice: the window starts at the dword
+  // holding value sidx0, which is its half `sb_h` (odd rows of an odd number
+  // of scale values start mid-dword)
+  const int sb_h = ((tile * 16 + col) * GPR + sidx0) & 1;
+  auto sb_index = [&](int g) { return ((ks * GPW + g) >> gsh) - sidx0 + sb_h; };
+  // nibble-expansion constants in registers (one v_and_or_b32 per dword)
+  const uint32_t nib_mask = sgpr_const(0x000F000Fu);
+  const uint32_t magic = vgpr_const(A::kMagic2);
+  auto scale_f = [&](const SB &v, int g) { return A::to_f32(sb_at(v, sb_index(g))); };
+
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) issue(d, d < nu);
+
+  // one unit: ring slot d holds unit i of the block's range
+  auto step = [&](int d, int i) {
+    if (m_ci[d] != cur_ci) {
+      cur_ci = m_ci[d];
+      load_act(m_e[d], m_ci[d]);
+    }
+    // ---- partial products of this wavefront's k-slice
+    f32x4 o[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) o[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int h = 0; h < GP; ++h) {
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        const u32x4 w = swap_pairs(wq[d][m][h]);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          f32x4 acc = A::mfma16(xa[h][2 * q], nibble_pairs_v(w[2 * q], nib_mask, magic),
+                                f32x4{0.f, 0.f, 0.f, 0.f});
+          acc = A::mfma16(xa[h][2 * q + 1], nibble_pairs_v(w[2 * q + 1], nib_mask, magic), acc);
+          const float s = scale_f(sv[d][m], 2 * h + q);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) o[m][v] = fmaf(s, acc[v], o[m][v]);
+        }
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int gg = 4 * b + G;
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        float bp = 0.f;
+        if (gg < GPW) {
+          const float s = A::to_f32(sb_at(sv[d][m], sb_index(gg)));
+          const float bb = A::to_f32(sb_at(bv[d][m], sb_index(gg)));
+          bp = fmaf(-A::kMagic, s, bb);
+        }
+        o[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xb[b], bp, o[m], 0, 0, 0);
+      }
+    }
+    const int r0 = m_r0[d];
+    // refill this ring slot DEPTH units ahead before the reduction
+    issue(d, i + DEPTH < nu);
+
+    // ---- reduce the KS partial tiles in LDS (double-buffered: one barrier
+    // per unit) and finish the outputs; each thread finishes at most one
+    // (tile, routed row, weight row) output per pass, summing the KS partials
+    // in k-slice order
+    const int buf = i & 1;
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) s_red[buf][wv][m][v][lane] = o[m][v];
+    if (!DUAL && wv == 0 && G == 0) s_orow[buf][col] = my_orow;
+    __syncthreads();
+    for (int item = tid; item < NT * 256; item += 64 * NW) {
+      const int t = item >> 8, tok = (item >> 4) & 15, c = item & 15;
+      const int row = r0 + 16 * t + c;
+      if (tok < cur_cnt && row < R) {
+        const int pl = c + 16 * (tok >> 2), pv = tok & 3;
+        float sum[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          float p[kMaxNW];
+#pragma unroll
+          for (int k2 = 0; k2 < kMaxNW; ++k2)
+            p[k2] = s_red[buf][min(t * KS + k2, kMaxNW - 1)][m][pv][pl];
+          float acc = p[0];
+#pragma unroll
+          for (int k2 = 1; k2 < kMaxNW; ++k2) acc += k2 < KS ? p[k2] : 0.f;
+          sum[m] = acc;
+        }
+        uint16_t r;
+        int64_t orow;
+        if constexpr (DUAL) {
+          // reference rounding points: gate and up outputs are act tensors,
+          // silu(gate) * up is rounded once more
+          const float gv = round_act<DT>(sum[0]);
+          const float uv = round_act<DT>(sum[NM - 1]);
+          r = A::from_f32(gv / (1.0f + __expf(-gv)) * uv);
+          orow = cur_slot0 + tok;
+        } else {
+          r = A::from_f32(sum[0]);
+          orow = s_orow[buf][tok];
+        }
+        a.out[orow * a.out_ld + row] = r;
+      }
+    }
+  };
+
+  // Full passes over the ring, then the remainder: the loop body has no exit
+  // in the middle, so at every compute the ring holds DEPTH - 1 younger units
+  // of loads and the wait counts say so.
+  const int nfull = nu / DEPTH;
+  for (int it = 0; it < nfull; ++it) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) step(d, it * DEPTH + d);
+  }
+  const int rem = nu - nfull * DEPTH;
+#pragma unroll
+  for (int d = 0; d < DEPTH - 1; ++d)
+    if (d < rem) step(d, nfull * DEPTH + d);
+}
+
+struct GemvShape {
+  int gpw, ks, nt;
+};
+
+// Groups per wavefront k-slice (GPW) and k-slices per tile (KS): the block
+// is KS x NT <= 8 wavefronts, preferably exactly 8 (KS dividing 8).
+bool gemv_shape(int K, int R, GemvShape &s) {
+  if (K <= 0 || K % 64) return false;
+  const int g = K / 64;
+  static const int cand[] = {4, 6, 8, 2};  // even: 16-byte loads cover group pairs
+  s.gpw = 0;
+  for (int pass = 0; pass < 2 && !s.gpw; ++pass)
+    for (int c : cand)
+      if (g % c == 0 && g / c <= kMaxNW && (pass == 1 || kMaxNW % (g / c) == 0)) {
+        s.gpw = c;
+        break;
+      }
+  if (!s.gpw) return false;
+  s.ks = g / s.gpw;
+  s.nt = std::max(1, std::min(kMaxNW / s.ks, (R + 15) / 16));
+  return true;
+}
+
+template <int DT, bool DUAL, int GPW>
+hipError_t launch_cfg(const GroupedArgs &a, const GemvShape &s, hipStream_t st) {
+  // as many blocks as the register budget keeps resident on every CU
+  const int nw = s.ks * s.nt;
+  const int blocks = std::max(1, 4 * kWavesPerSimd / nw) * cu_count();
+  hipLaunchKernelGGL((gemv_kernel<DT, DUAL, GPW>), dim3(blocks), dim3(64 * s.ks * s.nt), 0, st, a,
+                     s.ks, s.nt);
   return hipGetLastError();
 }
 
-template <int DT>
-hipError_t launch_t(bool dual, const GroupedArgs &a, hipStream_t st) {
-  const int gpr = a.K / a.gs;
-  const int sb_mode = (gpr % 2 == 0 && gpr <= 32) ? SB_ROW : SB_PER_GROUP;
-  // gate/up: one 16-row tile of both matrices per wavefront; down: two tiles
-  return dual ? launch_nt<DT, true, 1>(a, sb_mode, st) : launch_nt<DT, false, 2>(a, sb_mode, st);
+template <int DT, bool DUAL>
+hipError_t launch_t(const GroupedArgs &a, const GemvShape &s, hipStream_t st) {
+  switch (s.gpw) {
+    case 8: return launch_cfg<DT, DUAL, 8>(a, s, st);
+    case 6: return launch_cfg<DT, DUAL, 6>(a, s, st);
+    case 4: return launch_cfg<DT, DUAL, 4>(a, s, st);
+    default: return launch_cfg<DT, DUAL, 2>(a, s, st);
+  }
 }
 
 }  // namespace
 
+bool gemv_supports(int K) {
+  GemvShape s;
+  return gemv_shape(K, 16, s);
+}
+
 hipError_t launch_gemv(int dtype, bool dual, const GroupedArgs &a, hipStream_t st) {
-  return dtype == DT_BF16 ? launch_t<DT_BF16>(dual, a, st) : launch_t<DT_F16>(dual, a, st);
+  GemvShape s;
+  if (!gemv_shape(a.K, a.R, s)) return hipErrorInvalidValue;
+  if (dtype == DT_BF16)
+    return dual ? launch_t<DT_BF16, true>(a, s, st) : launch_t<DT_BF16, false>(a, s, st);
+  return dual ? launch_t<DT_F16, true>(a, s, st) : launch_t<DT_F16, false>(a, s, st);
 }
 
 }  // namespace nvm

@@ -46,6 +46,9 @@ hipError_t launch_dispatch(const int32_t *ids, int64_t n, int64_t E, int32_t *of
                            int32_t *sorted, hipStream_t st);
 
 // Grouped products.  dual = fused gate/up with SwiGLU epilogue.
+// Decode products need the reduction dimension in at most 8 slices of 1, 2,
+// 4 or 8 whole 64-wide groups.
+bool gemv_supports(int K);
 hipError_t launch_gemv(int dtype, bool dual, const GroupedArgs &a, hipStream_t st);
 constexpr int kGemmBM = 128;   // prefill tile rows (routed pairs)
 constexpr int kGemmBN = 128;   // prefill tile columns per weight matrix
