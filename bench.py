@@ -122,7 +122,7 @@ class Stages:
         self.down = torch.empty((N, H), dtype=bf, device=dev)
         self.y = torch.empty((T, H), dtype=bf, device=dev)
         size = ctypes.c_size_t()
-        self.L.check(self.lib.nvm_route_workspace_size(T, H, E, ctypes.byref(size)))
+        self.L.check(self.lib.nvm_route_dispatch_workspace_size(T, H, E, k, ctypes.byref(size)))
         self.rws = torch.empty(max(size.value, 1), dtype=torch.uint8, device=dev)
 
     def run(self, x, events=None):
@@ -131,38 +131,37 @@ class Stages:
         T, H, I, E, k = self.T, self.H, self.I, self.E, self.k
         gs = m.w_gate.group_size
         r, g, u, d = m.w_router, m.w_gate, m.w_up, m.w_down
-        ev = events or [None] * 6
+        ev = events or [None] * 5
 
         def rec(i):
             if ev[i] is not None:
                 ev[i].record()
 
         rec(0)
-        L.check(lib.nvm_moe_route(x.data_ptr(), T, H, r.weight.data_ptr(), r.scales.data_ptr(),
-                                  r.biases.data_ptr(), E, gs, 4, k, 1, 1, None,
-                                  self.ids.data_ptr(), self.scores.data_ptr(),
-                                  self.rws.data_ptr(), self.rws.numel(), st))
+        L.check(lib.nvm_moe_route_dispatch(
+            x.data_ptr(), T, H, r.weight.data_ptr(), r.scales.data_ptr(), r.biases.data_ptr(), E,
+            gs, 4, k, 1, 1, None, self.ids.data_ptr(), self.scores.data_ptr(),
+            self.offsets.data_ptr(), self.sorted.data_ptr(), self.rws.data_ptr(), self.rws.numel(),
+            st))
         rec(1)
-        L.check(lib.nvm_moe_dispatch(self.ids.data_ptr(), T * k, E, self.offsets.data_ptr(),
-                                     self.sorted.data_ptr(), st))
-        rec(2)
         L.check(lib.nvm_moe_expert_gateup(
             x.data_ptr(), T, H, I, E, k, gs, 4, 1, g.weight.data_ptr(), g.scales.data_ptr(),
             g.biases.data_ptr(), u.weight.data_ptr(), u.scales.data_ptr(), u.biases.data_ptr(),
             self.offsets.data_ptr(), self.sorted.data_ptr(), self.h.data_ptr(), 0, st))
-        rec(3)
+        rec(2)
         L.check(lib.nvm_moe_expert_down(
             self.h.data_ptr(), T * k, H, I, E, gs, 4, 1, d.weight.data_ptr(),
             d.scales.data_ptr(), d.biases.data_ptr(), self.offsets.data_ptr(),
             self.sorted.data_ptr(), self.down.data_ptr(), 0, st))
-        rec(4)
+        rec(3)
         L.check(lib.nvm_moe_combine(self.down.data_ptr(), self.scores.data_ptr(), T, k, H, 1,
                                     self.y.data_ptr(), st))
-        rec(5)
+        rec(4)
         return self.y
 
 
-STAGE_NAMES = ["route", "dispatch", "gateup", "down", "combine"]
+# route = routing and dispatch (nvm_moe_route_dispatch)
+STAGE_NAMES = ["route", "gateup", "down", "combine"]
 
 
 def eager_stage_pass(layers, xs, steps, warmup, dev):
@@ -174,7 +173,7 @@ def eager_stage_pass(layers, xs, steps, warmup, dev):
     for i in range(warmup):
         stages[i % len(layers)].run(xs[i % len(xs)])
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(steps)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
     touched = []
     ids_snap = []
     for i in range(steps):
@@ -187,7 +186,7 @@ def eager_stage_pass(layers, xs, steps, warmup, dev):
     for i in range(steps):
         for j, n in enumerate(STAGE_NAMES):
             dur[n] += evs[i][j].elapsed_time(evs[i][j + 1]) * 1e3
-        total += evs[i][0].elapsed_time(evs[i][5]) * 1e3
+        total += evs[i][0].elapsed_time(evs[i][4]) * 1e3
     for i in range(steps):
         touched.append(int(torch.unique(ids_snap[i]).numel()))
     return {n: v / steps for n, v in dur.items()}, total / steps, touched, ids_snap
@@ -347,7 +346,10 @@ KERNEL_KEYS = (
     ("prefill_gateup", "gemm_kernel<1, true"),
     ("prefill_down", "gemm_kernel<1, false"),
     ("route_partial", "route_mfma_kernel<1"),
+    ("route_finalize_dispatch", "route_finalize_dispatch_kernel<1"),
     ("route_finalize", "route_finalize_kernel<1"),
+    ("dispatch_count", "dispatch_count_kernel"),
+    ("dispatch_scatter", "dispatch_scatter_kernel"),
     ("dispatch", "dispatch_kernel"),
     ("combine", "combine_kernel<1"),
 )

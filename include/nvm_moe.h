@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define NVM_ABI_VERSION 1
+#define NVM_ABI_VERSION 2
 
 enum nvm_dtype { NVM_DTYPE_F16 = 0, NVM_DTYPE_BF16 = 1 };
 
@@ -94,10 +94,27 @@ int nvm_moe_route(const void *x, int64_t T, int64_t H, const uint32_t *wr, const
  *   the histogram); sorted_pairs [n] int32 (pair indices, expert-major).
  * Pairs whose id lies outside [0,E) are left out: they fall in no expert's
  * range, offsets[E] counts only the valid pairs, and sorted_pairs[offsets[E]..n)
- * is not written.  1 <= E <= 512.  Needs no workspace.
+ * is not written.  1 <= E <= 512.  Workspace: nvm_dispatch_workspace_size
+ * (zero bytes, and workspace may be NULL, up to 4096 pairs).
  */
+int nvm_dispatch_workspace_size(int64_t n, int64_t E, size_t *bytes);
 int nvm_moe_dispatch(const int32_t *ids, int64_t n, int64_t E, int32_t *expert_offsets,
-                     int32_t *sorted_pairs, nvm_stream_t stream);
+                     int32_t *sorted_pairs, void *workspace, size_t workspace_bytes,
+                     nvm_stream_t stream);
+
+/*
+ * Routing followed by dispatch, as nvm_moe_forward runs them: the outputs of
+ * nvm_moe_route (probs may be NULL) and of nvm_moe_dispatch over the T*k ids.
+ * Decode batches (T <= 64) finalise and sort in a single launch.
+ * Replaces `route_topk` plus the `argsort` pair (layers/moe.py:37-49, 16-17).
+ * Workspace: nvm_route_dispatch_workspace_size.
+ */
+int nvm_route_dispatch_workspace_size(int64_t T, int64_t H, int64_t E, int top_k, size_t *bytes);
+int nvm_moe_route_dispatch(const void *x, int64_t T, int64_t H, const uint32_t *wr,
+                           const void *sr, const void *br, int64_t E, int group_size, int bits,
+                           int top_k, int norm_topk_prob, int dtype, void *probs, int32_t *ids,
+                           void *scores, int32_t *expert_offsets, int32_t *sorted_pairs,
+                           void *workspace, size_t workspace_bytes, nvm_stream_t stream);
 
 /*
  * Grouped expert linear: out[r] = x[r] . dequant(W[ids[r]])^T rounded to act,

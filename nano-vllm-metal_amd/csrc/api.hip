@@ -100,7 +100,8 @@ struct MoeWs {
   double *partial;
   int32_t *ids;
   uint16_t *scores;
-  int32_t *offsets, *sorted;
+  int32_t *offsets, *sorted, *counts;
+  unsigned *done;
   uint16_t *h, *down;
   size_t bytes;
 };
@@ -114,10 +115,48 @@ MoeWs carve_moe(void *base, int64_t T, int64_t H, int64_t I, int64_t E, int k) {
   w.scores = c.take<uint16_t>(N);
   w.offsets = c.take<int32_t>(E + 1);
   w.sorted = c.take<int32_t>(N);
+  w.counts = c.take<int32_t>((size_t)nvm::dispatch_workspace_bytes(N, E) / sizeof(int32_t));
+  w.done = c.take<unsigned>(1);
   w.h = c.take<uint16_t>((size_t)N * I);
   w.down = c.take<uint16_t>((size_t)N * H);
   w.bytes = (c.off + 255) & ~(size_t)255;
   return w;
+}
+
+// Routing then dispatch: one single-block launch finalises and sorts decode
+// batches; larger batches finalise per token and sort over blocks.
+int run_route_dispatch(int dtype, const void *x, int64_t T, int64_t H, const uint32_t *wr,
+                       const void *sr, const void *br, int64_t E, int gs, int k, int norm,
+                       void *probs, int32_t *ids, void *scores, int32_t *offsets, int32_t *sorted,
+                       double *partial, int32_t *counts, unsigned *done, hipStream_t st) {
+  const int splits = nvm::route_splits(T, H, E);
+  const bool fused = nvm::route_fused_dispatch(T, k);
+  NVM_TRY_HIP(nvm::launch_route_partial(dtype, x, T, H, wr, sr, br, E, gs, false, partial, nullptr,
+                                        fused ? done : nullptr, st));
+  if (fused) {
+    NVM_TRY_HIP(nvm::launch_route_finalize_dispatch(dtype, partial, splits, T, E, k, norm, probs,
+                                                    ids, scores, offsets, sorted, done, st));
+  } else {
+    NVM_TRY_HIP(nvm::launch_route_finalize(dtype, partial, splits, T, E, k, norm, probs, ids,
+                                           scores, st));
+    NVM_TRY_HIP(nvm::launch_dispatch(ids, T * k, E, offsets, sorted, counts, st));
+  }
+  return NVM_OK;
+}
+
+int check_route(const void *x, int64_t T, int64_t H, const uint32_t *wr, const void *sr,
+                const void *br, int64_t E, int group_size, int bits, int top_k, int dtype,
+                const int32_t *ids, const void *scores) {
+  if (int r = check_quant(group_size, bits, dtype)) return r;
+  NVM_REQUIRE(x && wr && sr && br && ids && scores, "route: null pointer");
+  NVM_REQUIRE(T >= 0 && H > 0 && E > 0, "route: bad shape");
+  NVM_REQUIRE(H % group_size == 0, "route: H=%lld not divisible by group_size %d",
+              (long long)H, group_size);
+  NVM_SUPPORTED(E <= kMaxExperts, "route: at most %lld experts", (long long)kMaxExperts);
+  NVM_REQUIRE(top_k >= 1 && top_k <= E, "route: top_k=%d outside [1, E=%lld]", top_k,
+              (long long)E);
+  NVM_SUPPORTED(top_k <= kMaxTopK, "route: top_k at most %d", kMaxTopK);
+  return NVM_OK;
 }
 
 int run_products(int dtype, bool decode, bool dual, nvm::GroupedArgs &g, int64_t pairs,
@@ -155,7 +194,7 @@ int nvm_quantized_matmul(const void *scales, const void *biases, int group_size,
               (long long)N, group_size);
   if (M == 0) return NVM_OK;
   NVM_TRY_HIP(nvm::launch_route_partial(dtype, a, M, N, b, scales, biases, K, group_size, true,
-                                        nullptr, out, (hipStream_t)stream));
+                                        nullptr, out, nullptr, (hipStream_t)stream));
   return NVM_OK;
 }
 
@@ -170,15 +209,8 @@ int nvm_moe_route(const void *x, int64_t T, int64_t H, const uint32_t *wr, const
                   const void *br, int64_t E, int group_size, int bits, int top_k,
                   int norm_topk_prob, int dtype, void *probs, int32_t *ids, void *scores,
                   void *workspace, size_t workspace_bytes, nvm_stream_t stream) {
-  if (int r = check_quant(group_size, bits, dtype)) return r;
-  NVM_REQUIRE(x && wr && sr && br && ids && scores, "route: null pointer");
-  NVM_REQUIRE(T >= 0 && H > 0 && E > 0, "route: bad shape");
-  NVM_REQUIRE(H % group_size == 0, "route: H=%lld not divisible by group_size %d",
-              (long long)H, group_size);
-  NVM_SUPPORTED(E <= kMaxExperts, "route: at most %lld experts", (long long)kMaxExperts);
-  NVM_REQUIRE(top_k >= 1 && top_k <= E, "route: top_k=%d outside [1, E=%lld]", top_k,
-              (long long)E);
-  NVM_SUPPORTED(top_k <= kMaxTopK, "route: top_k at most %d", kMaxTopK);
+  if (int r = check_route(x, T, H, wr, sr, br, E, group_size, bits, top_k, dtype, ids, scores))
+    return r;
   if (T == 0) return NVM_OK;
   size_t need = 0;
   nvm_route_workspace_size(T, H, E, &need);
@@ -187,20 +219,66 @@ int nvm_moe_route(const void *x, int64_t T, int64_t H, const uint32_t *wr, const
   const int splits = nvm::route_splits(T, H, E);
   hipStream_t st = (hipStream_t)stream;
   NVM_TRY_HIP(nvm::launch_route_partial(dtype, x, T, H, wr, sr, br, E, group_size, false,
-                                        (double *)workspace, nullptr, st));
+                                        (double *)workspace, nullptr, nullptr, st));
   NVM_TRY_HIP(nvm::launch_route_finalize(dtype, (const double *)workspace, splits, T, E, top_k,
                                          norm_topk_prob, probs, ids, scores, st));
   return NVM_OK;
 }
 
+int nvm_dispatch_workspace_size(int64_t n, int64_t E, size_t *bytes) {
+  NVM_REQUIRE(bytes, "dispatch_workspace_size: null output");
+  NVM_REQUIRE(n >= 0 && E > 0, "dispatch_workspace_size: bad shape");
+  *bytes = (size_t)nvm::dispatch_workspace_bytes(n, E);
+  return NVM_OK;
+}
+
 int nvm_moe_dispatch(const int32_t *ids, int64_t n, int64_t E, int32_t *expert_offsets,
-                     int32_t *sorted_pairs, nvm_stream_t stream) {
+                     int32_t *sorted_pairs, void *workspace, size_t workspace_bytes,
+                     nvm_stream_t stream) {
   NVM_REQUIRE(expert_offsets && (n == 0 || (ids && sorted_pairs)), "dispatch: null pointer");
   NVM_REQUIRE(n >= 0 && E > 0, "dispatch: bad shape");
   NVM_SUPPORTED(E <= kMaxExperts, "dispatch: at most %lld experts", (long long)kMaxExperts);
   NVM_SUPPORTED(n < (1ll << 31), "dispatch: too many pairs");
-  NVM_TRY_HIP(nvm::launch_dispatch(ids, n, E, expert_offsets, sorted_pairs, (hipStream_t)stream));
+  const size_t need = (size_t)nvm::dispatch_workspace_bytes(n, E);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(NVM_ERR_WORKSPACE, "dispatch: workspace of %zu bytes needed", need);
+  NVM_TRY_HIP(nvm::launch_dispatch(ids, n, E, expert_offsets, sorted_pairs, workspace,
+                                   (hipStream_t)stream));
   return NVM_OK;
+}
+
+int nvm_route_dispatch_workspace_size(int64_t T, int64_t H, int64_t E, int top_k, size_t *bytes) {
+  NVM_REQUIRE(bytes, "route_dispatch_workspace_size: null output");
+  NVM_REQUIRE(T >= 0 && H > 0 && E > 0 && top_k > 0, "route_dispatch_workspace_size: bad shape");
+  Carve c(nullptr);
+  c.take<double>((size_t)nvm::route_splits(T, H, E) * T * E);
+  c.take<int32_t>((size_t)nvm::dispatch_workspace_bytes(T * top_k, E) / sizeof(int32_t));
+  c.take<unsigned>(1);
+  *bytes = (c.off + 255) & ~(size_t)255;
+  return NVM_OK;
+}
+
+int nvm_moe_route_dispatch(const void *x, int64_t T, int64_t H, const uint32_t *wr,
+                           const void *sr, const void *br, int64_t E, int group_size, int bits,
+                           int top_k, int norm_topk_prob, int dtype, void *probs, int32_t *ids,
+                           void *scores, int32_t *expert_offsets, int32_t *sorted_pairs,
+                           void *workspace, size_t workspace_bytes, nvm_stream_t stream) {
+  if (int r = check_route(x, T, H, wr, sr, br, E, group_size, bits, top_k, dtype, ids, scores))
+    return r;
+  NVM_REQUIRE(expert_offsets && sorted_pairs, "route_dispatch: null pointer");
+  if (T == 0) return NVM_OK;
+  size_t need = 0;
+  nvm_route_dispatch_workspace_size(T, H, E, top_k, &need);
+  if (!workspace || workspace_bytes < need)
+    return fail(NVM_ERR_WORKSPACE, "route_dispatch: workspace of %zu bytes needed", need);
+  Carve c(workspace);
+  double *partial = c.take<double>((size_t)nvm::route_splits(T, H, E) * T * E);
+  int32_t *counts =
+      c.take<int32_t>((size_t)nvm::dispatch_workspace_bytes(T * top_k, E) / sizeof(int32_t));
+  unsigned *done = c.take<unsigned>(1);
+  return run_route_dispatch(dtype, x, T, H, wr, sr, br, E, group_size, top_k, norm_topk_prob,
+                            probs, ids, scores, expert_offsets, sorted_pairs, partial, counts, done,
+                            (hipStream_t)stream);
 }
 
 int nvm_grouped_linear_workspace_size(int64_t n, int64_t D, int64_t O, int64_t E, size_t *bytes) {
@@ -211,6 +289,7 @@ int nvm_grouped_linear_workspace_size(int64_t n, int64_t D, int64_t O, int64_t E
   Carve c(nullptr);
   c.take<int32_t>(E + 1);
   c.take<int32_t>(n);
+  c.take<int32_t>((size_t)nvm::dispatch_workspace_bytes(n, E) / sizeof(int32_t));
   *bytes = (c.off + 255) & ~(size_t)255;
   return NVM_OK;
 }
@@ -237,8 +316,9 @@ int nvm_grouped_expert_linear(const void *x, int64_t n, int64_t D, const uint32_
   Carve c(workspace);
   int32_t *offsets = c.take<int32_t>(E + 1);
   int32_t *sorted = c.take<int32_t>(n);
+  int32_t *counts = c.take<int32_t>((size_t)nvm::dispatch_workspace_bytes(n, E) / sizeof(int32_t));
   hipStream_t st = (hipStream_t)stream;
-  NVM_TRY_HIP(nvm::launch_dispatch(ids, n, E, offsets, sorted, st));
+  NVM_TRY_HIP(nvm::launch_dispatch(ids, n, E, offsets, sorted, counts, st));
   nvm::GroupedArgs g{};
   g.act = (const uint16_t *)x;
   g.act_ld = D;
@@ -363,12 +443,10 @@ int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, i
   const int64_t N = T * top_k;
   hipStream_t st = (hipStream_t)stream;
 
-  const int splits = nvm::route_splits(T, H, E);
-  NVM_TRY_HIP(nvm::launch_route_partial(dtype, x, T, H, wr, sr, br, E, group_size, false,
-                                        ws.partial, nullptr, st));
-  NVM_TRY_HIP(nvm::launch_route_finalize(dtype, ws.partial, splits, T, E, top_k, norm_topk_prob,
-                                         nullptr, ids, scores, st));
-  NVM_TRY_HIP(nvm::launch_dispatch(ids, N, E, ws.offsets, ws.sorted, st));
+  if (int r = run_route_dispatch(dtype, x, T, H, wr, sr, br, E, group_size, top_k, norm_topk_prob,
+                                 nullptr, ids, scores, ws.offsets, ws.sorted, ws.partial,
+                                 ws.counts, ws.done, st))
+    return r;
   if (int r = nvm_moe_expert_gateup(x, T, H, I, E, top_k, group_size, bits, dtype, wg, sg, bg,
                                     wu, su, bu, ws.offsets, ws.sorted, ws.h, regime, stream))
     return r;

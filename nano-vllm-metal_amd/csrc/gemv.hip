@@ -58,7 +58,7 @@ constexpr int kMaxNW = 8;   // wavefronts per block
 #define NVM_GEMV_WAVES_PER_SIMD 2
 #endif
 #ifndef NVM_GEMV_RING
-#define NVM_GEMV_RING 72
+#define NVM_GEMV_RING 48
 #endif
 constexpr int kWavesPerSimd = NVM_GEMV_WAVES_PER_SIMD;
 

@@ -32,18 +32,34 @@ struct GroupedArgs {
 // Router.  Partial float64 logits over hidden splits, then per-token finalise.
 // With final_act the logits are rounded and stored as act [T, E] directly.
 int route_splits(int64_t T, int64_t H, int64_t E);
+// `done` (may be NULL) is a counter the partial launch zeroes for the fused
+// finalise-and-dispatch launch that follows it.
 hipError_t launch_route_partial(int dtype, const void *x, int64_t T, int64_t H, const uint32_t *wr,
                                 const void *sr, const void *br, int64_t E, int gs, bool final_act,
-                                double *partial, void *final_out, hipStream_t st);
+                                double *partial, void *final_out, unsigned *done, hipStream_t st);
 hipError_t launch_route_finalize(int dtype, const double *partial, int splits, int64_t T,
                                  int64_t E, int k, int norm, void *probs, int32_t *ids,
                                  void *scores, hipStream_t st);
 
 constexpr int kMaxExperts = 512;
 
-// Dispatch: stable counting sort of ids into expert order.
+// Decode batches (T <= kFusedRouteTokens): finalise the tokens and sort the
+// pairs into expert order in one launch (its last block sorts; `done` is the
+// block counter zeroed by launch_route_partial).
+constexpr int64_t kFusedRouteTokens = 64;
+bool route_fused_dispatch(int64_t T, int k);
+hipError_t launch_route_finalize_dispatch(int dtype, const double *partial, int splits, int64_t T,
+                                          int64_t E, int k, int norm, void *probs, int32_t *ids,
+                                          void *scores, int32_t *offsets, int32_t *sorted,
+                                          unsigned *done, hipStream_t st);
+
+// Dispatch: stable counting sort of ids into expert order.  Up to
+// kSortChunk pairs sort in one block; more take per-block histograms in a
+// workspace of dispatch_workspace_bytes().
+constexpr int64_t kSortChunk = 4096;
+int64_t dispatch_workspace_bytes(int64_t n, int64_t E);
 hipError_t launch_dispatch(const int32_t *ids, int64_t n, int64_t E, int32_t *offsets,
-                           int32_t *sorted, hipStream_t st);
+                           int32_t *sorted, void *workspace, hipStream_t st);
 
 // Grouped products.  dual = fused gate/up with SwiGLU epilogue.
 // Decode products need the reduction dimension in at most 8 slices of 1, 2,

@@ -13,6 +13,7 @@
 // and with them the top-k ids, do not depend on summation order.
 #include "common.h"
 #include "internal.h"
+#include "sort.h"
 
 namespace nvm {
 
@@ -35,11 +36,13 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(
     const uint16_t *__restrict__ x, int T, int H, const uint32_t *__restrict__ wr,
     const uint16_t *__restrict__ sr, const uint16_t *__restrict__ br, int E, int gs, int KR,
     int n_tt, int n_eb, int splits, double *__restrict__ part,
-    uint16_t *__restrict__ fin) {
+    uint16_t *__restrict__ fin, unsigned *__restrict__ done) {
   using A = Act<DT>;
   constexpr int NC = 8;  // 32-wide chunks per batch; all loads of a batch are in flight together
   const int lane = threadIdx.x & 63;
   const int item = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  // the finalising launch that follows counts its blocks from zero
+  if (done && blockIdx.x == 0 && threadIdx.x == 0) *done = 0u;
   if (item >= n_tt * n_eb * splits) return;
   const int tt = item % n_tt;
   const int eb = (item / n_tt) % n_eb;
@@ -131,50 +134,65 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(
       if (fin)
         fin[(int64_t)tok * E + e] = act_from_f64<DT>(acc[b][i]);
       else
-        part[((int64_t)z * T + tok) * E + e] = acc[b][i];
+        part[((int64_t)tok * E + e) * splits + z] = acc[b][i];
     }
   }
 }
 
 constexpr int kMaxExpertSlots = 8;  // experts per lane: E <= 512
+constexpr int kMaxSplits = 16;      // hidden splits of the partial logits
 
-// One wavefront per token: sum the split partials, round the logits, softmax
-// in float64, select top-k by (prob desc, index asc), renormalise.
-template <int DT>
-__global__ __launch_bounds__(256) void route_finalize_kernel(
-    const double *__restrict__ part, int splits, int T, int E, int k, int norm,
-    uint16_t *__restrict__ probs, int32_t *__restrict__ ids, uint16_t *__restrict__ scores) {
+// Token t, one wavefront: sum the split partials (in split order), round the
+// logits, softmax in float64, select top-k by (prob desc, index asc),
+// renormalise.  Lane i < k returns expert id and score of slot i.  Each lane
+// holds experts lane + 64 j for j < NS (NS * 64 >= E).
+template <int DT, int NS>
+__device__ __forceinline__ void finalize_token(const double *__restrict__ part, int splits, int t,
+                                               int E, int k, int norm, uint16_t *__restrict__ probs,
+                                               int &my_id, uint16_t &my_score) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (t >= T) return;
   constexpr int P = Act<DT>::kPrec, EMIN = Act<DT>::kEmin;
-
-  double lg[kMaxExpertSlots];
+  // all partials of a logit are contiguous: issue every load of a slot
+  // before summing (loads past `splits` read zeros)
+  const rsrc_t pr = make_rsrc(part + (int64_t)t * E * splits, (uint32_t)(E * splits * 8));
+  double lg[NS];
   double mloc = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < kMaxExpertSlots; ++j) {
+  for (int j = 0; j < NS; ++j) lg[j] = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
     const int e = lane + 64 * j;
-    lg[j] = -INFINITY;
-    if (e < E) {
-      double s = 0.0;
-      for (int z = 0; z < splits; ++z) s += part[((int64_t)z * T + t) * E + e];
-      lg[j] = round_f64_to(s, P, EMIN);
-      mloc = fmax(mloc, lg[j]);
+    const int off = e < E ? e * splits * 8 : kMaskedOffset;
+    u32x4 v[kMaxSplits / 2];
+#pragma unroll
+    for (int z2 = 0; z2 < kMaxSplits / 2; ++z2)
+      v[z2] = bload16(pr, 2 * z2 < splits ? off + 16 * z2 : kMaskedOffset, 0);
+    // partials past `splits` read as +0.0 and leave the sum unchanged
+    double sum = 0.0;
+#pragma unroll
+    for (int z2 = 0; z2 < kMaxSplits / 2; ++z2) {
+      sum += __builtin_bit_cast(double, u32x2{v[z2].x, v[z2].y});
+      sum += __builtin_bit_cast(double, u32x2{v[z2].z, v[z2].w});
     }
+#pragma unroll
+    for (int jj = 0; jj < NS; ++jj)
+      if (jj == j && e < E) lg[jj] = round_f64_to(sum, P, EMIN);
   }
+#pragma unroll
+  for (int j = 0; j < NS; ++j) mloc = fmax(mloc, lg[j]);
   const double m = wave_reduce_f64(mloc, [](double a, double b) { return fmax(a, b); });
-  double p[kMaxExpertSlots];
+  double p[NS];
   double sloc = 0.0;
 #pragma unroll
-  for (int j = 0; j < kMaxExpertSlots; ++j) {
+  for (int j = 0; j < NS; ++j) {
     const int e = lane + 64 * j;
-    p[j] = (e < E) ? exp(lg[j] - m) : 0.0;
+    p[j] = e < E ? exp(lg[j] - m) : 0.0;
     sloc += p[j];
   }
   const double sum = wave_reduce_f64(sloc, [](double a, double b) { return a + b; });
-  uint32_t key[kMaxExpertSlots];
+  uint32_t key[NS];
 #pragma unroll
-  for (int j = 0; j < kMaxExpertSlots; ++j) {
+  for (int j = 0; j < NS; ++j) {
     const int e = lane + 64 * j;
     key[j] = 0;
     if (e < E) {
@@ -185,35 +203,80 @@ __global__ __launch_bounds__(256) void route_finalize_kernel(
       key[j] = ((uint32_t)pb << 16) | (uint32_t)(0xFFFF - e);
     }
   }
-  int my_id = 0;
+  int id = 0;
   double my_p = 0.0, psum = 0.0;
   for (int i = 0; i < k; ++i) {
     uint32_t best = 0;
 #pragma unroll
-    for (int j = 0; j < kMaxExpertSlots; ++j) best = max(best, key[j]);
+    for (int j = 0; j < NS; ++j) best = max(best, key[j]);
     best = wave_max_u32(best);
     const int e = 0xFFFF - (int)(best & 0xFFFFu);
     const double pv = (double)Act<DT>::to_f32(best >> 16);
     psum += pv;  // at most k act values: exact in float64
     if (lane == i) {
-      my_id = e;
+      id = e;
       my_p = pv;
     }
     if ((e & 63) == lane) {
 #pragma unroll
-      for (int j = 0; j < kMaxExpertSlots; ++j)
+      for (int j = 0; j < NS; ++j)
         if (j == (e >> 6)) key[j] = 0;
     }
   }
+  double sc = my_p;
+  if (norm) sc = my_p / round_f64_to(psum, P, EMIN);
+  my_id = id;
+  my_score = act_from_f64<DT>(sc);
+}
+
+// One wavefront per token.
+template <int DT, int NS>
+__global__ __launch_bounds__(256) void route_finalize_kernel(
+    const double *__restrict__ part, int splits, int T, int E, int k, int norm,
+    uint16_t *__restrict__ probs, int32_t *__restrict__ ids, uint16_t *__restrict__ scores) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= T) return;
+  int id;
+  uint16_t sc;
+  finalize_token<DT, NS>(part, splits, t, E, k, norm, probs, id, sc);
   if (lane < k) {
-    double sc = my_p;
-    if (norm) {
-      const double denom = round_f64_to(psum, P, EMIN);
-      sc = my_p / denom;
-    }
-    ids[(int64_t)t * k + lane] = my_id;
-    scores[(int64_t)t * k + lane] = act_from_f64<DT>(sc);
+    ids[(int64_t)t * k + lane] = id;
+    scores[(int64_t)t * k + lane] = sc;
   }
+}
+
+// Small batches: one wavefront per token, four per block (one per SIMD);
+// the last block to finish (a counter in the workspace, zeroed by the
+// partial-logit launch that precedes this one) sorts the T*k ids into expert
+// order (sort.h), so finalising and dispatch are one launch.
+template <int DT, int NS>
+__global__ __launch_bounds__(256) void route_finalize_dispatch_kernel(
+    const double *__restrict__ part, int splits, int T, int E, int k, int norm, int nbits,
+    uint16_t *__restrict__ probs, int32_t *__restrict__ ids, uint16_t *__restrict__ scores,
+    int32_t *__restrict__ offsets, int32_t *__restrict__ sorted, unsigned *__restrict__ done) {
+  extern __shared__ int lds[];
+  __shared__ int s_last;
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t < T) {
+    int id;
+    uint16_t sc;
+    finalize_token<DT, NS>(part, splits, t, E, k, norm, probs, id, sc);
+    if (lane < k) {
+      ids[(int64_t)t * k + lane] = id;
+      scores[(int64_t)t * k + lane] = sc;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();  // this block's ids are visible before it is counted
+    s_last = atomicAdd(done, 1u) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();  // every block's ids are visible to the sort
+  block_sort([&](int p) { return ids[p]; }, T * k, E, nbits, lds, offsets, sorted);
 }
 
 struct RoutePlan {
@@ -229,9 +292,10 @@ RoutePlan route_plan(int64_t T, int64_t H, int64_t E) {
   p.n_tt = (int)n_tt;
   p.n_eb = (int)((E + 16 * p.eb - 1) / (16 * p.eb));
   p.splits = 1;
-  // hidden slices of at least 256 columns keep the finalise pass short
+  // hidden slices of at least 64 columns, at most kMaxSplits of them; about
+  // 2048 wavefronts share the work
   const int64_t chunks = H / 32;
-  while (p.splits * 2 <= chunks / 8 && chunks % (p.splits * 2) == 0 &&
+  while (p.splits * 2 <= kMaxSplits && p.splits * 2 <= chunks / 2 && chunks % (p.splits * 2) == 0 &&
          n_tt * p.n_eb * p.splits * 2 <= 2048)
     p.splits *= 2;
   return p;
@@ -240,7 +304,7 @@ RoutePlan route_plan(int64_t T, int64_t H, int64_t E) {
 template <int DT, int EB>
 hipError_t launch_mfma_t(const void *x, int64_t T, int64_t H, const uint32_t *wr, const void *sr,
                          const void *br, int64_t E, int gs, const RoutePlan &p, double *partial,
-                         void *fin, hipStream_t st) {
+                         void *fin, unsigned *done, hipStream_t st) {
   const int64_t items = (int64_t)p.n_tt * p.n_eb * p.splits;
   dim3 grid((unsigned)((items + 3) / 4));
   // 8-byte scale loads need 4 groups (group 64) or 2 groups (group 128) of
@@ -252,21 +316,21 @@ hipError_t launch_mfma_t(const void *x, int64_t T, int64_t H, const uint32_t *wr
     hipLaunchKernelGGL((route_mfma_kernel<DT, EB, true>), grid, dim3(256), 0, st,
                        (const uint16_t *)x, (int)T, (int)H, wr, (const uint16_t *)sr,
                        (const uint16_t *)br, (int)E, gs, (int)(H / p.splits), p.n_tt, p.n_eb,
-                       p.splits, partial, (uint16_t *)fin);
+                       p.splits, partial, (uint16_t *)fin, done);
   else
     hipLaunchKernelGGL((route_mfma_kernel<DT, EB, false>), grid, dim3(256), 0, st,
                        (const uint16_t *)x, (int)T, (int)H, wr, (const uint16_t *)sr,
                        (const uint16_t *)br, (int)E, gs, (int)(H / p.splits), p.n_tt, p.n_eb,
-                       p.splits, partial, (uint16_t *)fin);
+                       p.splits, partial, (uint16_t *)fin, done);
   return hipGetLastError();
 }
 
 template <int DT>
 hipError_t launch_route_t(const void *x, int64_t T, int64_t H, const uint32_t *wr, const void *sr,
                           const void *br, int64_t E, int gs, const RoutePlan &p, double *partial,
-                          void *fin, hipStream_t st) {
-  return p.eb == 4 ? launch_mfma_t<DT, 4>(x, T, H, wr, sr, br, E, gs, p, partial, fin, st)
-                   : launch_mfma_t<DT, 1>(x, T, H, wr, sr, br, E, gs, p, partial, fin, st);
+                          void *fin, unsigned *done, hipStream_t st) {
+  return p.eb == 4 ? launch_mfma_t<DT, 4>(x, T, H, wr, sr, br, E, gs, p, partial, fin, done, st)
+                   : launch_mfma_t<DT, 1>(x, T, H, wr, sr, br, E, gs, p, partial, fin, done, st);
 }
 
 }  // namespace
@@ -276,24 +340,84 @@ int route_splits(int64_t T, int64_t H, int64_t E) { return route_plan(T, H, E).s
 hipError_t launch_route_partial(int dtype, const void *x, int64_t T, int64_t H,
                                 const uint32_t *wr, const void *sr, const void *br, int64_t E,
                                 int gs, bool final_act, double *partial, void *fin,
-                                hipStream_t st) {
+                                unsigned *done, hipStream_t st) {
   RoutePlan p = route_plan(T, H, E);
   if (final_act) p.splits = 1;
   return dtype == DT_BF16
-             ? launch_route_t<DT_BF16>(x, T, H, wr, sr, br, E, gs, p, partial, fin, st)
-             : launch_route_t<DT_F16>(x, T, H, wr, sr, br, E, gs, p, partial, fin, st);
+             ? launch_route_t<DT_BF16>(x, T, H, wr, sr, br, E, gs, p, partial, fin, done, st)
+             : launch_route_t<DT_F16>(x, T, H, wr, sr, br, E, gs, p, partial, fin, done, st);
+}
+
+bool route_fused_dispatch(int64_t T, int k) { return T <= kFusedRouteTokens && T * k <= kSortChunk; }
+
+namespace {
+
+template <int DT, int NS>
+void launch_fin_dispatch(const double *partial, int splits, int64_t T, int64_t E, int k, int norm,
+                         int nbits, void *probs, int32_t *ids, void *scores, int32_t *offsets,
+                         int32_t *sorted, unsigned *done, hipStream_t st) {
+  const size_t lds = sizeof(int) * (size_t)(5 * E);  // block_sort: (4 wavefronts + 1) * E
+  hipLaunchKernelGGL((route_finalize_dispatch_kernel<DT, NS>), dim3((unsigned)((T + 3) / 4)),
+                     dim3(256), lds, st, partial, splits, (int)T, (int)E, k, norm, nbits,
+                     (uint16_t *)probs, ids, (uint16_t *)scores, offsets, sorted, done);
+}
+
+template <int DT, int NS>
+void launch_fin(const double *partial, int splits, int64_t T, int64_t E, int k, int norm,
+                void *probs, int32_t *ids, void *scores, hipStream_t st) {
+  hipLaunchKernelGGL((route_finalize_kernel<DT, NS>), dim3((unsigned)((T + 3) / 4)), dim3(256), 0,
+                     st, partial, splits, (int)T, (int)E, k, norm, (uint16_t *)probs, ids,
+                     (uint16_t *)scores);
+}
+
+// Slots of 64 experts per lane: the smallest of 1, 2, 4, 8 covering E.
+template <int DT, template <int, int> class F, class... Args>
+void by_slots(int64_t E, Args... args) {
+  if (E <= 64)
+    F<DT, 1>::run(args...);
+  else if (E <= 128)
+    F<DT, 2>::run(args...);
+  else if (E <= 256)
+    F<DT, 4>::run(args...);
+  else
+    F<DT, 8>::run(args...);
+}
+
+template <int DT, int NS>
+struct FinDispatch {
+  template <class... Args>
+  static void run(Args... args) { launch_fin_dispatch<DT, NS>(args...); }
+};
+template <int DT, int NS>
+struct Fin {
+  template <class... Args>
+  static void run(Args... args) { launch_fin<DT, NS>(args...); }
+};
+
+}  // namespace
+
+hipError_t launch_route_finalize_dispatch(int dtype, const double *partial, int splits, int64_t T,
+                                          int64_t E, int k, int norm, void *probs, int32_t *ids,
+                                          void *scores, int32_t *offsets, int32_t *sorted,
+                                          unsigned *done, hipStream_t st) {
+  int nbits = 0;
+  while ((1ll << nbits) < E) ++nbits;
+  if (dtype == DT_BF16)
+    by_slots<DT_BF16, FinDispatch>(E, partial, splits, T, E, k, norm, nbits, probs, ids, scores,
+                                   offsets, sorted, done, st);
+  else
+    by_slots<DT_F16, FinDispatch>(E, partial, splits, T, E, k, norm, nbits, probs, ids, scores,
+                                  offsets, sorted, done, st);
+  return hipGetLastError();
 }
 
 hipError_t launch_route_finalize(int dtype, const double *partial, int splits, int64_t T,
                                  int64_t E, int k, int norm, void *probs, int32_t *ids,
                                  void *scores, hipStream_t st) {
-  dim3 grid((unsigned)((T + 3) / 4));
   if (dtype == DT_BF16)
-    hipLaunchKernelGGL((route_finalize_kernel<DT_BF16>), grid, dim3(256), 0, st, partial, splits,
-                       (int)T, (int)E, k, norm, (uint16_t *)probs, ids, (uint16_t *)scores);
+    by_slots<DT_BF16, Fin>(E, partial, splits, T, E, k, norm, probs, ids, scores, st);
   else
-    hipLaunchKernelGGL((route_finalize_kernel<DT_F16>), grid, dim3(256), 0, st, partial, splits,
-                       (int)T, (int)E, k, norm, (uint16_t *)probs, ids, (uint16_t *)scores);
+    by_slots<DT_F16, Fin>(E, partial, splits, T, E, k, norm, probs, ids, scores, st);
   return hipGetLastError();
 }
 

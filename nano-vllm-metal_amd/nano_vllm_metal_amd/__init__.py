@@ -8,7 +8,7 @@ GPU (libnvm_moe.so); nothing falls back to the CPU.
 """
 
 from .linear import QuantizedWeights, dequantize, quantize, quantized_linear, quantized_matmul
-from .moe import Moe, grouped_expert_linear, moe_dispatch, route_topk
+from .moe import Moe, grouped_expert_linear, moe_dispatch, route_and_dispatch, route_topk
 
 __all__ = [
     "QuantizedWeights",
@@ -19,5 +19,6 @@ __all__ = [
     "route_topk",
     "grouped_expert_linear",
     "moe_dispatch",
+    "route_and_dispatch",
     "Moe",
 ]

@@ -23,6 +23,8 @@ NVM_ERR_HIP = -4
 
 REGIME_AUTO, REGIME_DECODE, REGIME_PREFILL = 0, 1, 2
 
+ABI_VERSION = 2  # NVM_ABI_VERSION of include/nvm_moe.h
+
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
 
 _P = ctypes.c_void_p
@@ -35,7 +37,11 @@ SIGNATURES = {
     "nvm_quantized_matmul": [_P, _P, _I, _I, _P, _P, _I, _P, _I64, _I64, _I64, _I, _P],
     "nvm_route_workspace_size": [_I64, _I64, _I64, ctypes.POINTER(_SZ)],
     "nvm_moe_route": [_P, _I64, _I64, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _P, _P, _P, _SZ, _P],
-    "nvm_moe_dispatch": [_P, _I64, _I64, _P, _P, _P],
+    "nvm_dispatch_workspace_size": [_I64, _I64, ctypes.POINTER(_SZ)],
+    "nvm_moe_dispatch": [_P, _I64, _I64, _P, _P, _P, _SZ, _P],
+    "nvm_route_dispatch_workspace_size": [_I64, _I64, _I64, _I, ctypes.POINTER(_SZ)],
+    "nvm_moe_route_dispatch": [_P, _I64, _I64, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _P, _P,
+                               _P, _P, _P, _SZ, _P],
     "nvm_grouped_linear_workspace_size": [_I64, _I64, _I64, _I64, ctypes.POINTER(_SZ)],
     "nvm_grouped_expert_linear": [_P, _I64, _I64, _P, _P, _P, _I64, _I64, _I, _I, _P, _I, _P, _I, _P, _SZ, _P],
     "nvm_moe_workspace_size": [_I64, _I64, _I64, _I64, _I, ctypes.POINTER(_SZ)],
@@ -74,7 +80,7 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = _I
         fn.argtypes = args
-    if lib.nvm_abi_version() != 1:
+    if lib.nvm_abi_version() != ABI_VERSION:
         raise RuntimeError(f"unexpected ABI version {lib.nvm_abi_version()}")
     _lib = lib
     return lib

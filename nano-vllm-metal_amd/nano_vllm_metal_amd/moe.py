@@ -93,9 +93,43 @@ def moe_dispatch(expert_ids: torch.Tensor, num_experts: int):
     n = flat.numel()
     offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
     sorted_pairs = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    size = ctypes.c_size_t()
+    _lib.check(lib.nvm_dispatch_workspace_size(n, num_experts, ctypes.byref(size)))
+    ws = _workspace(size.value, dev)
     _lib.check(lib.nvm_moe_dispatch(flat.data_ptr(), n, num_experts, offsets.data_ptr(),
-                                    sorted_pairs.data_ptr(), _lib.stream_of(dev)))
+                                    sorted_pairs.data_ptr(), ws.data_ptr(), ws.numel(),
+                                    _lib.stream_of(dev)))
     return offsets, sorted_pairs[:n]
+
+
+def route_and_dispatch(x: torch.Tensor, w_router: QuantizedWeights, top_k: int,
+                       norm_topk_prob: bool = False):
+    """Routing then dispatch, the first stage of ``Moe`` (moe.py:37-49, 16-17).
+
+    Returns ``(ids [T, k] int32, scores [T, k], offsets [E+1] int32,
+    sorted_pairs [T*k] int32)`` for ``x`` of ``T`` tokens, as
+    ``route_topk`` followed by ``moe_dispatch`` of the flat ids.
+    """
+    lib = _lib.load()
+    dev = _lib.require_device(x, w_router.weight, w_router.scales, w_router.biases)
+    H = x.shape[-1]
+    x2 = x.reshape(-1, H).contiguous()
+    T = x2.shape[0]
+    E = w_router.weight.shape[0]
+    ids = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    scores = torch.empty((T, top_k), dtype=x.dtype, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    sorted_pairs = torch.empty(max(T * top_k, 1), dtype=torch.int32, device=dev)
+    size = ctypes.c_size_t()
+    _lib.check(lib.nvm_route_dispatch_workspace_size(T, H, E, top_k, ctypes.byref(size)))
+    ws = _workspace(size.value, dev)
+    _lib.check(lib.nvm_moe_route_dispatch(
+        x2.data_ptr(), T, H, _i32(w_router.weight).data_ptr(),
+        w_router.scales.contiguous().data_ptr(), w_router.biases.contiguous().data_ptr(), E,
+        w_router.group_size, w_router.bits, top_k, int(bool(norm_topk_prob)),
+        _lib.dtype_code(x.dtype), None, ids.data_ptr(), scores.data_ptr(), offsets.data_ptr(),
+        sorted_pairs.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(dev)))
+    return ids, scores, offsets, sorted_pairs[:T * top_k]
 
 
 def grouped_expert_linear(x: torch.Tensor, w_experts: QuantizedWeights,

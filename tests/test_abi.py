@@ -40,7 +40,7 @@ def test_library_exports_every_header_function():
 
 def test_abi_version():
     L, lib = _lib()
-    assert lib.nvm_abi_version() == 1
+    assert lib.nvm_abi_version() == L.ABI_VERSION == 2
 
 
 def _err(lib) -> str:
@@ -106,8 +106,20 @@ def test_quantized_matmul_validation():
 
 def test_dispatch_and_route_validation():
     L, lib = _lib()
-    assert lib.nvm_moe_dispatch(1, 10, 0, 1, 1, None) == L.NVM_ERR_INVALID
-    assert lib.nvm_moe_dispatch(1, 10, 4096, 1, 1, None) == L.NVM_ERR_UNSUPPORTED
+    assert lib.nvm_moe_dispatch(1, 10, 0, 1, 1, None, 0, None) == L.NVM_ERR_INVALID
+    assert lib.nvm_moe_dispatch(1, 10, 4096, 1, 1, None, 0, None) == L.NVM_ERR_UNSUPPORTED
+    # more than 4096 pairs sort over blocks and need the histogram workspace
+    size = ctypes.c_size_t()
+    assert lib.nvm_dispatch_workspace_size(4096, 128, ctypes.byref(size)) == 0 and size.value == 0
+    assert lib.nvm_dispatch_workspace_size(32768, 128, ctypes.byref(size)) == 0
+    assert size.value == 4 * 8 * 128
+    assert lib.nvm_moe_dispatch(1, 32768, 128, 1, 1, None, 0, None) == L.NVM_ERR_WORKSPACE
+    r = lib.nvm_moe_route_dispatch(1, 4, 2048, 1, 1, 1, 128, 64, 4, 8, 1, 1, None, 1, 1, 1, 1,
+                                   None, 0, None)
+    assert r == L.NVM_ERR_WORKSPACE
+    r = lib.nvm_moe_route_dispatch(1, 4, 2048, 1, 1, 1, 128, 64, 4, 8, 1, 1, None, 1, 1, None, 1,
+                                   1, 1 << 30, None)
+    assert r == L.NVM_ERR_INVALID
     r = lib.nvm_moe_route(1, 4, 2048, 1, 1, 1, 128, 64, 4, 9, 0, 1, None, 1, 1, 1, 0, None)
     assert r == L.NVM_ERR_WORKSPACE
     r = lib.nvm_moe_route(1, 4, 2048, 1, 1, 1, 128, 64, 4, 129, 0, 1, None, 1, 1, 1, 1 << 30, None)

@@ -53,6 +53,24 @@ def test_route_bit_exact(T, H, E, k, act, gs, norm):
     assert np.array_equal(to_np(scores), sc_ref), "scores differ"
 
 
+@pytest.mark.parametrize("T", [1, 5, 32, 64, 65, 700])
+def test_route_and_dispatch_matches_oracle(T):
+    """One call: routing plus the stable sort (single launch for T <= 64)."""
+    from nano_vllm_metal_amd import route_and_dispatch
+
+    H, E, k, act, gs = 2048, 128, 8, "bfloat16", 64
+    x, router = _route_case(3000 + T, T, H, E, k, act, gs, True)
+    _, _, ids_ref, sc_ref = O.route_topk(x, *router, gs, k, True, act)
+    off_ref, srt_ref = O.dispatch(ids_ref, E)
+    ids, scores, off, srt = route_and_dispatch(to_act(x, act, DEV), qweights(router, act, gs, DEV),
+                                               k, True)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy(), ids_ref)
+    assert np.array_equal(to_np(scores), sc_ref)
+    assert np.array_equal(off.cpu().numpy(), off_ref)
+    assert np.array_equal(srt.cpu().numpy(), srt_ref)
+
+
 def test_route_ties_pick_lower_index():
     """All-zero router weights: every prob is 1/E, ids must be 0..k-1."""
     from nano_vllm_metal_amd import QuantizedWeights, route_topk
