@@ -68,9 +68,14 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(
     so[b] = e_ok[b] ? e * GPR * 2 : kMaskedOffset;
   }
 
-  f64x4 acc[EB];
+  // CH independent accumulator chains per expert tile shorten the dependent
+  // MFMA chain (four chains in all); they are added once at the end
+  constexpr int CH = 4 / EB;
+  f64x4 acc[EB][CH];
 #pragma unroll
-  for (int b = 0; b < EB; ++b) acc[b] = f64x4{0.0, 0.0, 0.0, 0.0};
+  for (int b = 0; b < EB; ++b)
+#pragma unroll
+    for (int h = 0; h < CH; ++h) acc[b][h] = f64x4{0.0, 0.0, 0.0, 0.0};
 
   for (int kb = 0; kb < KR; kb += 32 * NC) {
     const int kbs = __builtin_amdgcn_readfirstlane(kb);
@@ -80,12 +85,15 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(
     uint32_t qv[EB][NC];
     // packed scales/biases: the 16-bit value of group i is half (i & 1) of dword i >> 1
     u32x2 sv[EB], bv[EB];
+    // chunks past the split's range read through masked offsets
 #pragma unroll
-    for (int c = 0; c < NC; ++c) xv[c] = bload16(xr, xo + 64 * c, 2 * kbs);
+    for (int c = 0; c < NC; ++c)
+      xv[c] = bload16(xr, kbs + 32 * c < KR ? xo + 64 * c : kMaskedOffset, 2 * kbs);
 #pragma unroll
     for (int b = 0; b < EB; ++b) {
 #pragma unroll
-      for (int c = 0; c < NC; ++c) qv[b][c] = bload4(wrr, wo[b] + 16 * c, kbs / 2);
+      for (int c = 0; c < NC; ++c)
+        qv[b][c] = bload4(wrr, kbs + 32 * c < KR ? wo[b] + 16 * c : kMaskedOffset, kbs / 2);
       if constexpr (SB_VEC) {
         sv[b] = bload8(srr, so[b], 2 * g0);
         bv[b] = bload8(brr, so[b], 2 * g0);
@@ -118,7 +126,7 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
           const double w = fma((double)((qv[b][c] >> (4 * m)) & 0xFu), s, bb);
-          acc[b] = __builtin_amdgcn_mfma_f64_16x16x4f64(xd[m], w, acc[b], 0, 0, 0);
+          acc[b][m % CH] = __builtin_amdgcn_mfma_f64_16x16x4f64(xd[m], w, acc[b][m % CH], 0, 0, 0);
         }
       }
     }
@@ -128,13 +136,15 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(
     const int e = (eb * EB + b) * 16 + col;
     if (!e_ok[b]) continue;
 #pragma unroll
+    for (int h = 1; h < CH; ++h) acc[b][0] += acc[b][h];
+#pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tok = tt * 16 + G + 4 * i;
       if (tok >= T) continue;
       if (fin)
-        fin[(int64_t)tok * E + e] = act_from_f64<DT>(acc[b][i]);
+        fin[(int64_t)tok * E + e] = act_from_f64<DT>(acc[b][0][i]);
       else
-        part[((int64_t)tok * E + e) * splits + z] = acc[b][i];
+        part[((int64_t)tok * E + e) * splits + z] = acc[b][0][i];
     }
   }
 }
