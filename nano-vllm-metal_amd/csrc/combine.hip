@@ -19,6 +19,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict
                                                       int64_t T, int k, int64_t H,
                                                       uint16_t *__restrict__ y) {
   using A = Act<DT>;
+  hoist_args(down, scores, T, k, H, y);
   const int64_t chunks = H / 8;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= T * chunks) return;

@@ -171,6 +171,19 @@ __device__ __forceinline__ u32x4 nibble_pairs(uint32_t w) {
   return o;
 }
 
+// Kernel arguments are read from the kernarg segment by scalar loads that the
+// compiler places at their first use, often inside branches and each behind its
+// own wait.  Naming them all in one empty asm statement at kernel entry issues
+// the loads together: one memory round trip instead of one per use.
+template <class T>
+__device__ __forceinline__ void hoist_arg(const T &v) {
+  asm volatile("" ::"s"(v));
+}
+template <class... T>
+__device__ __forceinline__ void hoist_args(const T &...v) {
+  (hoist_arg(v), ...);
+}
+
 __device__ __forceinline__ u32x4 ldg16(const void *p) { return *(const u32x4 *)p; }
 __device__ __forceinline__ u32x2 ldg8(const void *p) { return *(const u32x2 *)p; }
 

@@ -149,6 +149,8 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
   __shared__ int s_orow[2][kChunk];  // output rows of the unit's routed rows
   __shared__ float s_red[2][kMaxNW][NM][4][64];
 
+  hoist_args(a.act, a.act_ld, a.act_rows, a.a_map, a.a_div, a.offsets, a.w0, a.s0, a.b0, a.w1,
+             a.s1, a.b1, a.R, a.K, a.gs, a.E, a.out, a.o_map, a.out_ld, KS, NT);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int NW = blockDim.x >> 6;
   const int col = lane & 15, G = lane >> 4;
@@ -373,21 +375,19 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
       for (int v = 0; v < 4; ++v) s_red[buf][wv][m][v][lane] = o[m][v];
     if (!DUAL && wv == 0 && G == 0) s_orow[buf][col] = my_orow;
     __syncthreads();
-    for (int item = tid; item < NT * 256; item += 64 * NW) {
-      const int t = item >> 8, tok = (item >> 4) & 15, c = item & 15;
+    // items (tile, routed row < cur_cnt, weight row): the unit's outputs only
+    const int nitem = NT * cur_cnt * 16;
+    for (int item = tid; item < nitem; item += 64 * NW) {
+      const int c = item & 15, rest = item >> 4;
+      const int t = rest / cur_cnt, tok = rest - t * cur_cnt;
       const int row = r0 + 16 * t + c;
-      if (tok < cur_cnt && row < R) {
+      if (row < R) {
         const int pl = c + 16 * (tok >> 2), pv = tok & 3;
         float sum[NM];
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
-          float p[kMaxNW];
-#pragma unroll
-          for (int k2 = 0; k2 < kMaxNW; ++k2)
-            p[k2] = s_red[buf][min(t * KS + k2, kMaxNW - 1)][m][pv][pl];
-          float acc = p[0];
-#pragma unroll
-          for (int k2 = 1; k2 < kMaxNW; ++k2) acc += k2 < KS ? p[k2] : 0.f;
+          float acc = s_red[buf][t * KS][m][pv][pl];
+          for (int k2 = 1; k2 < KS; ++k2) acc += s_red[buf][t * KS + k2][m][pv][pl];
           sum[m] = acc;
         }
         uint16_t r;

@@ -39,6 +39,7 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(
     uint16_t *__restrict__ fin, unsigned *__restrict__ done) {
   using A = Act<DT>;
   constexpr int NC = 8;  // 32-wide chunks per batch; all loads of a batch are in flight together
+  hoist_args(x, T, H, wr, sr, br, E, gs, KR, n_tt, n_eb, splits, part, fin, done);
   const int lane = threadIdx.x & 63;
   const int item = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   // the finalising launch that follows counts its blocks from zero
@@ -265,6 +266,7 @@ __global__ __launch_bounds__(256) void route_finalize_dispatch_kernel(
     const double *__restrict__ part, int splits, int T, int E, int k, int norm, int nbits,
     uint16_t *__restrict__ probs, int32_t *__restrict__ ids, uint16_t *__restrict__ scores,
     int32_t *__restrict__ offsets, int32_t *__restrict__ sorted, unsigned *__restrict__ done) {
+  hoist_args(part, splits, T, E, k, norm, nbits, probs, ids, scores, offsets, sorted, done);
   extern __shared__ int lds[];
   __shared__ int s_last;
   const int lane = threadIdx.x & 63;
