@@ -70,6 +70,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
   __shared__ int s_orow[BM];
   __shared__ int s_tiles[kMaxExperts + 1];
 
+  hoist_args(a.act, a.act_ld, a.act_rows, a.a_map, a.a_div, a.offsets, a.w0, a.s0, a.b0, a.w1,
+             a.s1, a.b1, a.R, a.K, a.gs, a.E, a.out, a.o_map, a.out_ld, n_tiles);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int l32 = lane & 31, h = lane >> 5;
 
@@ -160,30 +162,39 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
     srow[s] = grow < R ? grow * GPR * 2 : kMaskedOffset;
   }
 
-  u32x4 ga[4], gb[2];
-  uint32_t gsc[2], gbi[2];
-  auto load_stage = [&](int k0) {
+  const int nk = a.K / BK;
+  // Global loads of one k-step, issued two k-steps ahead into one of two
+  // register sets.  Every issue makes the same loads; k-steps past the end
+  // read through masked offsets (zeros, no traffic), so the wait counts are
+  // the same on every path.
+  struct Stage {
+    u32x4 a[4], b[2];
+    uint32_t s[2], z[2];
+  };
+  auto issue = [&](Stage &g, int ks) {
+    const bool ok = ks < nk;
+    const int k0 = ok ? ks * BK : 0;
     const int sa = __builtin_amdgcn_readfirstlane(k0 * 2);
     const int sb = __builtin_amdgcn_readfirstlane(k0 >> 1);
     const int sg = __builtin_amdgcn_readfirstlane((k0 / a.gs) * 2);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) ga[c] = bload16(ra, a_voff[c], sa);
-    gb[0] = bload16(rw0, b_voff[0], sb);
-    gb[1] = bload16(rw1, b_voff[1], sb);
-    gsc[0] = bload2(rs0, srow[0], sg);
-    gbi[0] = bload2(rb0, srow[0], sg);
-    gsc[1] = bload2(rs1, srow[1], sg);
-    gbi[1] = bload2(rb1, srow[1], sg);
+    for (int c = 0; c < 4; ++c) g.a[c] = bload16(ra, ok ? a_voff[c] : kMaskedOffset, sa);
+    g.b[0] = bload16(rw0, ok ? b_voff[0] : kMaskedOffset, sb);
+    g.b[1] = bload16(rw1, ok ? b_voff[1] : kMaskedOffset, sb);
+    g.s[0] = bload2(rs0, ok ? srow[0] : kMaskedOffset, sg);
+    g.z[0] = bload2(rb0, ok ? srow[0] : kMaskedOffset, sg);
+    g.s[1] = bload2(rs1, ok ? srow[1] : kMaskedOffset, sg);
+    g.z[1] = bload2(rb1, ok ? srow[1] : kMaskedOffset, sg);
   };
-  auto store_stage = [&](int buf) {
+  auto store = [&](const Stage &g, int buf) {
     uint8_t *As = smem + buf * STAGE;
     uint8_t *Bs = As + A_STAGE;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      *(u32x4 *)(As + ((tid >> 3) + 32 * c) * A_PITCH + 16 * (tid & 7)) = ga[c];
+      *(u32x4 *)(As + ((tid >> 3) + 32 * c) * A_PITCH + 16 * (tid & 7)) = g.a[c];
 #pragma unroll
     for (int c = 0; c < 2; ++c)
-      *(u32x4 *)(Bs + ((tid >> 1) + 128 * c) * B_PITCH + 16 * (tid & 1)) = gb[c];
+      *(u32x4 *)(Bs + ((tid >> 1) + 128 * c) * B_PITCH + 16 * (tid & 1)) = g.b[c];
   };
 
   f32x16 acc[2][4];
@@ -194,45 +205,79 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[s][i][r] = 0.f;
 
-  const int nk = a.K / BK;
-  load_stage(0);
-  store_stage(0);
-  float sc[2] = {A::to_f32(gsc[0]), A::to_f32(gsc[1])};
-  float bi[2] = {A::to_f32(gbi[0]), A::to_f32(gbi[1])};
-  __syncthreads();
-
-  for (int ks = 0; ks < nk; ++ks) {
-    const bool more = ks + 1 < nk;
-    if (more) load_stage((ks + 1) * BK);
-    const uint8_t *As = smem + (ks & 1) * STAGE;
+  float sc[2], bi[2];
+  auto take_sb = [&](const Stage &g) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      sc[s] = A::to_f32(g.s[s]);
+      bi[s] = A::to_f32(g.z[s]);
+    }
+  };
+  // Software-pipelined over the four 16-wide chunks: the A reads and the
+  // dequantisation of chunk c + 1 are issued ahead of chunk c's MFMAs.
+  auto compute = [&](int buf) {
+    const uint8_t *As = smem + buf * STAGE;
     const uint8_t *Bs = As + A_STAGE;
     u32x4 bw[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) bw[s] = *(const u32x4 *)(Bs + lrow[s] * B_PITCH + 16 * h);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      u32x4 af[4];
+    auto load_a = [&](int c, u32x4 (&af)[4]) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         af[i] = *(const u32x4 *)(As + (32 * i + l32) * A_PITCH + 16 * (4 * h + c));
-      u32x4 bf[2];
+    };
+    auto deq = [&](int c, u32x4 (&bf)[2]) {
 #pragma unroll
       for (int s = 0; s < 2; ++s) bf[s] = dequant8<DT>(bw[s][c], sc[s], bi[s]);
+    };
+    u32x4 af[4], bf[2];
+    load_a(0, af);
+    deq(0, bf);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      u32x4 afn[4], bfn[2];
+      if (c < 3) {
+        load_a(c + 1, afn);
+        deq(c + 1, bfn);
+      }
 #pragma unroll
       for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[s][i] = A::mfma32(af[i], bf[s], acc[s][i]);
-    }
-    if (more) {
-      store_stage((ks + 1) & 1);
+      if (c < 3) {
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        sc[s] = A::to_f32(gsc[s]);
-        bi[s] = A::to_f32(gbi[s]);
+        for (int i = 0; i < 4; ++i) af[i] = afn[i];
+        bf[0] = bfn[0];
+        bf[1] = bfn[1];
       }
     }
+  };
+
+  // k-step ks computes LDS buffer ks & 1 while the loads of ks + 2 are in
+  // flight in the register set that held ks; then ks + 1 (issued a k-step
+  // earlier) is stored into the other buffer.  Two k-steps per loop trip keep
+  // the register sets static.
+  Stage g0, g1;
+  issue(g0, 0);
+  issue(g1, 1);
+  store(g0, 0);
+  take_sb(g0);
+  __syncthreads();
+  auto step = [&](int ks, Stage &gi, Stage &gs) {
+    issue(gi, ks + 2);
+    compute(ks & 1);
+    if (ks + 1 < nk) {
+      store(gs, (ks + 1) & 1);
+      take_sb(gs);
+    }
     __syncthreads();
+  };
+  int ks = 0;
+  for (; ks + 1 < nk; ks += 2) {
+    step(ks, g0, g1);
+    step(ks + 1, g1, g0);
   }
+  if (ks < nk) step(ks, g0, g1);
 
   // C fragment of v_mfma_f32_32x32x16: lane l, register 4*q+j holds row
   // 8*q + 4*(l/32) + j, column l%32
