@@ -25,13 +25,28 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict
   if (idx >= T * chunks) return;
   const int64_t t = idx / chunks, c = idx - t * chunks;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < k; ++j) {
-    const float s = A::to_f32(scores[t * k + j]);
-    const u32x4 v = ldg16(down + ((t * k + j) * H + 8 * c));
+  // eight pairs per batch, all their loads in flight together
+  for (int j0 = 0; j0 < k; j0 += 8) {
+    u32x4 v[8];
+    uint32_t sv[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc[2 * i] += round_act<DT>(A::lo(v[i]) * s);
-      acc[2 * i + 1] += round_act<DT>(A::hi(v[i]) * s);
+    for (int jj = 0; jj < 8; ++jj) {
+      v[jj] = u32x4{0u, 0u, 0u, 0u};
+      sv[jj] = 0u;
+      if (j0 + jj < k) {  // uniform
+        v[jj] = ldg16(down + ((t * k + j0 + jj) * H + 8 * c));
+        sv[jj] = scores[t * k + j0 + jj];
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      if (j0 + jj >= k) break;
+      const float s = A::to_f32(sv[jj]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += round_act<DT>(A::lo(v[jj][i]) * s);
+        acc[2 * i + 1] += round_act<DT>(A::hi(v[jj][i]) * s);
+      }
     }
   }
   u32x4 o;

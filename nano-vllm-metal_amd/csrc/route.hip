@@ -170,24 +170,33 @@ __device__ __forceinline__ void finalize_token(const double *__restrict__ part, 
   double mloc = -INFINITY;
 #pragma unroll
   for (int j = 0; j < NS; ++j) lg[j] = -INFINITY;
+  // slots are read two at a time, all loads of a pair of slots in flight
+  // together (partials past `splits` read as +0.0 and leave the sums unchanged)
+  constexpr int SB = NS < 2 ? NS : 2;
 #pragma unroll
-  for (int j = 0; j < NS; ++j) {
-    const int e = lane + 64 * j;
-    const int off = e < E ? e * splits * 8 : kMaskedOffset;
-    u32x4 v[kMaxSplits / 2];
+  for (int j0 = 0; j0 < NS; j0 += SB) {
+    u32x4 v[SB][kMaxSplits / 2];
 #pragma unroll
-    for (int z2 = 0; z2 < kMaxSplits / 2; ++z2)
-      v[z2] = bload16(pr, 2 * z2 < splits ? off + 16 * z2 : kMaskedOffset, 0);
-    // partials past `splits` read as +0.0 and leave the sum unchanged
-    double sum = 0.0;
+    for (int jb = 0; jb < SB; ++jb) {
+      const int e = lane + 64 * (j0 + jb);
+      const int off = e < E ? e * splits * 8 : kMaskedOffset;
 #pragma unroll
-    for (int z2 = 0; z2 < kMaxSplits / 2; ++z2) {
-      sum += __builtin_bit_cast(double, u32x2{v[z2].x, v[z2].y});
-      sum += __builtin_bit_cast(double, u32x2{v[z2].z, v[z2].w});
+      for (int z2 = 0; z2 < kMaxSplits / 2; ++z2)
+        v[jb][z2] = bload16(pr, 2 * z2 < splits ? off + 16 * z2 : kMaskedOffset, 0);
     }
 #pragma unroll
-    for (int jj = 0; jj < NS; ++jj)
-      if (jj == j && e < E) lg[jj] = round_f64_to(sum, P, EMIN);
+    for (int jb = 0; jb < SB; ++jb) {
+      const int e = lane + 64 * (j0 + jb);
+      double sum = 0.0;
+#pragma unroll
+      for (int z2 = 0; z2 < kMaxSplits / 2; ++z2) {
+        sum += __builtin_bit_cast(double, u32x2{v[jb][z2].x, v[jb][z2].y});
+        sum += __builtin_bit_cast(double, u32x2{v[jb][z2].z, v[jb][z2].w});
+      }
+#pragma unroll
+      for (int jj = 0; jj < NS; ++jj)
+        if (jj == j0 + jb && e < E) lg[jj] = round_f64_to(sum, P, EMIN);
+    }
   }
 #pragma unroll
   for (int j = 0; j < NS; ++j) mloc = fmax(mloc, lg[j]);
@@ -288,7 +297,11 @@ __global__ __launch_bounds__(256) void route_finalize_dispatch_kernel(
   __syncthreads();
   if (!s_last) return;
   __threadfence();  // every block's ids are visible to the sort
-  block_sort([&](int p) { return ids[p]; }, T * k, E, nbits, lds, offsets, sorted);
+  // one read of the ids into LDS serves both passes of the sort
+  int *ids_lds = lds + 5 * E;
+  for (int p = threadIdx.x; p < T * k; p += blockDim.x) ids_lds[p] = ids[p];
+  __syncthreads();
+  block_sort([&](int p) { return ids_lds[p]; }, T * k, E, nbits, lds, offsets, sorted);
 }
 
 struct RoutePlan {
@@ -368,7 +381,8 @@ template <int DT, int NS>
 void launch_fin_dispatch(const double *partial, int splits, int64_t T, int64_t E, int k, int norm,
                          int nbits, void *probs, int32_t *ids, void *scores, int32_t *offsets,
                          int32_t *sorted, unsigned *done, hipStream_t st) {
-  const size_t lds = sizeof(int) * (size_t)(5 * E);  // block_sort: (4 wavefronts + 1) * E
+  // block_sort: (4 wavefronts + 1) * E, then the T*k ids
+  const size_t lds = sizeof(int) * (size_t)(5 * E + T * k);
   hipLaunchKernelGGL((route_finalize_dispatch_kernel<DT, NS>), dim3((unsigned)((T + 3) / 4)),
                      dim3(256), lds, st, partial, splits, (int)T, (int)E, k, norm, nbits,
                      (uint16_t *)probs, ids, (uint16_t *)scores, offsets, sorted, done);
