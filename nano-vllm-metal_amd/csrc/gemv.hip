@@ -259,7 +259,9 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
   float xb[NB];
   int cur_ci = -1, cur_slot0 = 0, cur_cnt = 0, my_orow = 0;
   const rsrc_t act_r = make_rsrc(a.act, (uint32_t)(a.act_rows * a.act_ld * 2));
-  auto load_act = [&](int e, int ci) {
+  // requests the chunk's activations into xa in load order (act_finish puts
+  // them in MFMA order once they are needed)
+  auto act_issue = [&](int e, int ci) {
     const int slot0 =
         __builtin_amdgcn_readfirstlane(s_off[e]) +
         (ci - __builtin_amdgcn_readfirstlane(s_cb[e])) * kChunk;
@@ -277,6 +279,14 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
     const int ao = arow >= 0 ? (int)((int64_t)arow * a.act_ld * 2) +
                                    (ks * GPW * 64 + 32 * (G & 1) + 16 * (G >> 1)) * 2
                              : kMaskedOffset;
+#pragma unroll
+    for (int h = 0; h < GP; ++h)
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+        xa[h][st] = bload16(act_r, ao + (128 * h + 64 * (st >> 1) + 8 * (st & 1)) * 2, 0);
+  };
+  // group sums (bias operand) and MFMA order of the requested activations
+  auto act_finish = [&]() {
     float ps[GPW];
 #pragma unroll
     for (int h = 0; h < GP; ++h) {
@@ -284,7 +294,7 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
       ps[2 * h + 1] = 0.f;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        const u32x4 v = bload16(act_r, ao + (128 * h + 64 * (st >> 1) + 8 * (st & 1)) * 2, 0);
+        const u32x4 v = xa[h][st];
 #pragma unroll
         for (int i = 0; i < 4; ++i) ps[2 * h + (st >> 1)] = A::dot2(v[i], A::kOne2, ps[2 * h + (st >> 1)]);
         xa[h][st] = pair_order(v);
@@ -317,14 +327,25 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
   const uint32_t magic = vgpr_const(A::kMagic2);
   auto scale_f = [&](const SB &v, int g) { return A::to_f32(sb_at(v, sb_index(g))); };
 
+  // The first chunk's activations are requested before the ring fill: loads
+  // return in order, so they are in registers while the ring still streams.
+  // The wider slices leave no registers for them beside the filling ring and
+  // load them at the first unit instead.
+  constexpr bool kActFirst = GPW <= 4 || (!DUAL && GPW == 6);
+  if (kActFirst) {
+    cur_ci = it_ci;
+    act_issue(it_e, it_ci);
+  }
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) issue(d, d < nu);
+  if (kActFirst) act_finish();
 
   // one unit: ring slot d holds unit i of the block's range
   auto step = [&](int d, int i) {
     if (m_ci[d] != cur_ci) {
       cur_ci = m_ci[d];
-      load_act(m_e[d], m_ci[d]);
+      act_issue(m_e[d], m_ci[d]);
+      act_finish();
     }
     // ---- partial products of this wavefront's k-slice
     f32x4 o[NM];
