@@ -109,6 +109,14 @@ __device__ __forceinline__ uint32_t sb_at(const u32x4 &v, int idx) {
   const uint32_t d = w == 0 ? v.x : w == 1 ? v.y : w == 2 ? v.z : v.w;
   return (idx & 1) ? (d >> 16) : (d & 0xFFFFu);
 }
+// The same as a select tree on the index bits: with aligned windows the
+// equality chain above becomes a dynamic vector extract, which a per-lane
+// index puts in scratch memory.
+__device__ __forceinline__ uint32_t sb_at_tree(const u32x2 &v, int idx) { return sb_at(v, idx); }
+__device__ __forceinline__ uint32_t sb_at_tree(const u32x4 &v, int idx) {
+  const uint32_t d = (idx & 4) ? ((idx & 2) ? v.w : v.z) : ((idx & 2) ? v.y : v.x);
+  return (idx & 1) ? (d >> 16) : (d & 0xFFFFu);
+}
 
 // Words (w0, w1, w2, w3) of a 16-byte load in lane group G hold codes
 // 32G + 8j.. of a 128-code group pair.  Exchanging the lower half-wave's
@@ -136,7 +144,10 @@ struct GemvCfg {
   static constexpr int NB = (GPW + 3) / 4;  // bias MFMAs (four groups each)
 };
 
-template <int DT, bool DUAL, int GPW>
+// SBA: group size 64 with an even number of groups per row, so every lane's
+// scale window starts on a dword (sb_h = 0) and the group of a scale value is
+// known at compile time.
+template <int DT, bool DUAL, int GPW, bool SBA>
 __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
     const GroupedArgs a, int KS, int NT) {
   using A = Act<DT>;
@@ -320,8 +331,8 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
   // window position of group g of the slice: the window starts at the dword
   // holding value sidx0, which is its half `sb_h` (odd rows of an odd number
   // of scale values start mid-dword)
-  const int sb_h = ((tile * 16 + col) * GPR + sidx0) & 1;
-  auto sb_index = [&](int g) { return ((ks * GPW + g) >> gsh) - sidx0 + sb_h; };
+  const int sb_h = SBA ? 0 : ((tile * 16 + col) * GPR + sidx0) & 1;
+  auto sb_index = [&](int g) { return SBA ? g : ((ks * GPW + g) >> gsh) - sidx0 + sb_h; };
   // nibble-expansion constants in registers (one v_and_or_b32 per dword)
   const uint32_t nib_mask = sgpr_const(0x000F000Fu);
   const uint32_t magic = vgpr_const(A::kMagic2);
@@ -347,23 +358,65 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
       act_issue(m_e[d], m_ci[d]);
       act_finish();
     }
-    // ---- partial products of this wavefront's k-slice
+    // ---- partial products of this wavefront's k-slice.  Narrow slices: all
+    // codes are expanded into operands of their own, then the MFMAs issue as
+    // independent chains (two per group), then the group scales apply in
+    // group order (expanding into one reused operand serialises expansion,
+    // MFMA and the next expansion).  Wider slices keep the per-pair order,
+    // which needs fewer registers.  Both sum in the same order.
     f32x4 o[NM];
 #pragma unroll
     for (int m = 0; m < NM; ++m) o[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (GPW <= 4) {
+      constexpr int HB = GP, h0 = 0;
+      u32x4 bop[HB][NM][4];
+      f32x4 acc[HB][NM][2];
 #pragma unroll
-    for (int h = 0; h < GP; ++h) {
+      for (int hh = 0; hh < HB; ++hh)
 #pragma unroll
-      for (int m = 0; m < NM; ++m) {
-        const u32x4 w = swap_pairs(wq[d][m][h]);
+        for (int m = 0; m < NM; ++m)
+          if (h0 + hh < GP) {
+            const u32x4 w = swap_pairs(wq[d][m][h0 + hh]);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          f32x4 acc = A::mfma16(xa[h][2 * q], nibble_pairs_v(w[2 * q], nib_mask, magic),
-                                f32x4{0.f, 0.f, 0.f, 0.f});
-          acc = A::mfma16(xa[h][2 * q + 1], nibble_pairs_v(w[2 * q + 1], nib_mask, magic), acc);
-          const float s = scale_f(sv[d][m], 2 * h + q);
+            for (int j = 0; j < 4; ++j) bop[hh][m][j] = nibble_pairs_v(w[j], nib_mask, magic);
+          }
 #pragma unroll
-          for (int v = 0; v < 4; ++v) o[m][v] = fmaf(s, acc[v], o[m][v]);
+      for (int step2 = 0; step2 < 2; ++step2)
+#pragma unroll
+        for (int hh = 0; hh < HB; ++hh)
+#pragma unroll
+          for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+              if (h0 + hh < GP)
+                acc[hh][m][q] = A::mfma16(xa[h0 + hh][2 * q + step2], bop[hh][m][2 * q + step2],
+                                          step2 ? acc[hh][m][q] : f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+      for (int hh = 0; hh < HB; ++hh)
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+            if (h0 + hh < GP) {
+              const float s = scale_f(sv[d][m], 2 * (h0 + hh) + q);
+#pragma unroll
+              for (int v = 0; v < 4; ++v) o[m][v] = fmaf(s, acc[hh][m][q][v], o[m][v]);
+            }
+    } else {
+#pragma unroll
+      for (int h = 0; h < GP; ++h) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          const u32x4 w = swap_pairs(wq[d][m][h]);
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            f32x4 acc = A::mfma16(xa[h][2 * q], nibble_pairs_v(w[2 * q], nib_mask, magic),
+                                  f32x4{0.f, 0.f, 0.f, 0.f});
+            acc = A::mfma16(xa[h][2 * q + 1], nibble_pairs_v(w[2 * q + 1], nib_mask, magic), acc);
+            const float s = scale_f(sv[d][m], 2 * h + q);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) o[m][v] = fmaf(s, acc[v], o[m][v]);
+          }
         }
       }
     }
@@ -374,8 +427,9 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
       for (int m = 0; m < NM; ++m) {
         float bp = 0.f;
         if (gg < GPW) {
-          const float s = A::to_f32(sb_at(sv[d][m], sb_index(gg)));
-          const float bb = A::to_f32(sb_at(bv[d][m], sb_index(gg)));
+          const int si = sb_index(gg);
+          const float s = A::to_f32(SBA ? sb_at_tree(sv[d][m], si) : sb_at(sv[d][m], si));
+          const float bb = A::to_f32(SBA ? sb_at_tree(bv[d][m], si) : sb_at(bv[d][m], si));
           bp = fmaf(-A::kMagic, s, bb);
         }
         o[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xb[b], bp, o[m], 0, 0, 0);
@@ -466,23 +520,27 @@ bool gemv_shape(int K, int R, GemvShape &s) {
   return true;
 }
 
-template <int DT, bool DUAL, int GPW>
+template <int DT, bool DUAL, int GPW, bool SBA>
 hipError_t launch_cfg(const GroupedArgs &a, const GemvShape &s, hipStream_t st) {
   // as many blocks as the register budget keeps resident on every CU
   const int nw = s.ks * s.nt;
   const int blocks = std::max(1, 4 * kWavesPerSimd / nw) * cu_count();
-  hipLaunchKernelGGL((gemv_kernel<DT, DUAL, GPW>), dim3(blocks), dim3(64 * s.ks * s.nt), 0, st, a,
-                     s.ks, s.nt);
+  hipLaunchKernelGGL((gemv_kernel<DT, DUAL, GPW, SBA>), dim3(blocks), dim3(64 * s.ks * s.nt), 0, st,
+                     a, s.ks, s.nt);
   return hipGetLastError();
 }
 
 template <int DT, bool DUAL>
 hipError_t launch_t(const GroupedArgs &a, const GemvShape &s, hipStream_t st) {
+  // aligned scale windows for the common slice widths
+  const bool sba = a.gs == 64 && (a.K / 64) % 2 == 0;
   switch (s.gpw) {
-    case 8: return launch_cfg<DT, DUAL, 8>(a, s, st);
-    case 6: return launch_cfg<DT, DUAL, 6>(a, s, st);
-    case 4: return launch_cfg<DT, DUAL, 4>(a, s, st);
-    default: return launch_cfg<DT, DUAL, 2>(a, s, st);
+    case 8: return launch_cfg<DT, DUAL, 8, false>(a, s, st);
+    case 6:
+      return sba ? launch_cfg<DT, DUAL, 6, true>(a, s, st) : launch_cfg<DT, DUAL, 6, false>(a, s, st);
+    case 4:
+      return sba ? launch_cfg<DT, DUAL, 4, true>(a, s, st) : launch_cfg<DT, DUAL, 4, false>(a, s, st);
+    default: return launch_cfg<DT, DUAL, 2, false>(a, s, st);
   }
 }
 
