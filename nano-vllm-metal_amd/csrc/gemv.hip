@@ -461,8 +461,17 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
         float sum[NM];
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
-          float acc = s_red[buf][t * KS][m][pv][pl];
-          for (int k2 = 1; k2 < KS; ++k2) acc += s_red[buf][t * KS + k2][m][pv][pl];
+          // four partials per LDS round trip (reads past KS land on other
+          // entries of s_red and are not added), summed in k-slice order
+          float acc = 0.f;
+          for (int k0 = 0; k0 < KS; k0 += 4) {
+            float part[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) part[j] = s_red[buf][min(t * KS + k0 + j, NW - 1)][m][pv][pl];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (k0 + j < KS) acc = (k0 + j == 0) ? part[0] : acc + part[j];
+          }
           sum[m] = acc;
         }
         uint16_t r;
@@ -472,7 +481,7 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
           // silu(gate) * up is rounded once more
           const float gv = round_act<DT>(sum[0]);
           const float uv = round_act<DT>(sum[NM - 1]);
-          r = A::from_f32(gv / (1.0f + __expf(-gv)) * uv);
+          r = A::from_f32(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * uv);
           orow = cur_slot0 + tok;
         } else {
           r = A::from_f32(sum[0]);
