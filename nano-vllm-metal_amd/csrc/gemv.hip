@@ -169,15 +169,23 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
   const int gsh = a.gs == 128 ? 1 : 0;
 
   if (wv == 0) {
+    // every offset in flight at once (one round trip, not one per 64
+    // experts), then the chunk counts from LDS
+    constexpr int kOffRegs = kMaxExperts / 64 + 1;
+    const rsrc_t off_r = make_rsrc(a.offsets, (uint32_t)(E + 1) * 4);
+    int ov[kOffRegs];
+#pragma unroll
+    for (int j = 0; j < kOffRegs; ++j)
+      if (64 * j <= E) ov[j] = (int)bload4(off_r, (64 * j + lane) * 4, 0);
+#pragma unroll
+    for (int j = 0; j < kOffRegs; ++j)
+      if (64 * j <= E && 64 * j + lane <= E) s_off[64 * j + lane] = ov[j];
+    __builtin_amdgcn_wave_barrier();
     int carry = 0;
     for (int e0 = 0; e0 < E; e0 += 64) {
       const int e = e0 + lane;
       int n = 0;
-      if (e < E) {
-        const int o0 = a.offsets[e];
-        s_off[e] = o0;
-        n = (a.offsets[e + 1] - o0 + kChunk - 1) / kChunk;
-      }
+      if (e < E) n = (s_off[e + 1] - s_off[e] + kChunk - 1) / kChunk;
       int inc = n;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
@@ -187,18 +195,23 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
       if (e < E) s_cb[e] = carry + inc - n;
       carry += __shfl(inc, 63);
     }
-    if (lane == 0) {
-      s_off[E] = a.offsets[E];
-      s_cb[E] = carry;
-    }
+    if (lane == 0) s_cb[E] = carry;
   }
   __syncthreads();
 
   const int rows_unit = 16 * NT;
   const int RT = (R + rows_unit - 1) / rows_unit;
   const int U = s_cb[E] * RT;
-  const int u0 = (int)((int64_t)blockIdx.x * U / gridDim.x);
-  const int u1 = (int)((int64_t)(blockIdx.x + 1) * U / gridDim.x);
+  // the block's share in 32-bit arithmetic where it fits (64-bit division is
+  // a long software sequence)
+  int u0, u1;
+  if ((int64_t)U * gridDim.x < (1ll << 31)) {
+    u0 = (int)((unsigned)(blockIdx.x * U) / gridDim.x);
+    u1 = (int)((unsigned)((blockIdx.x + 1) * U) / gridDim.x);
+  } else {
+    u0 = (int)((int64_t)blockIdx.x * U / gridDim.x);
+    u1 = (int)((int64_t)(blockIdx.x + 1) * U / gridDim.x);
+  }
   const int nu = u1 - u0;
   if (nu <= 0) return;  // uniform over the block, before any further barrier
 
@@ -207,19 +220,15 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
   // ---- unit iterator (uniform): chunk it_ci of expert it_e, row tile it_rt
   int it_ci = u0 / RT;
   int it_rt = u0 - it_ci * RT;
-  int it_e;
-  {
-    // largest expert whose first chunk is <= it_ci (an empty expert shares its
-    // first chunk with the next one, so the search lands on a non-empty one)
-    int lo = 0, hi = E - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (__builtin_amdgcn_readfirstlane(s_cb[mid]) <= it_ci)
-        lo = mid;
-      else
-        hi = mid - 1;
+  int it_e = E - 1;
+  // the non-empty expert holding chunk it_ci, found by all lanes at once
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    const uint64_t m = __ballot(e < E && s_cb[e] <= it_ci && it_ci < s_cb[e + 1]);
+    if (m) {
+      it_e = e0 + (int)__builtin_ctzll(m);
+      break;
     }
-    it_e = lo;
   }
   auto advance = [&]() {
     if (++it_rt == RT) {
