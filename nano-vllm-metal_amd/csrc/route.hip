@@ -191,7 +191,9 @@ __device__ __forceinline__ void finalize_token(const double *__restrict__ part, 
 #pragma unroll
       for (int z2 = 0; z2 < kMaxSplits / 2; ++z2) {
         sum += __builtin_bit_cast(double, u32x2{v[jb][z2].x, v[jb][z2].y});
-        sum += __builtin_bit_cast(double, u32x2{v[jb][z2].z, v[jb][z2].w});
+        // an odd split count leaves the last pair's second value to the next
+        // expert's row
+        if (2 * z2 + 1 < splits) sum += __builtin_bit_cast(double, u32x2{v[jb][z2].z, v[jb][z2].w});
       }
 #pragma unroll
       for (int jj = 0; jj < NS; ++jj)
@@ -317,10 +319,12 @@ RoutePlan route_plan(int64_t T, int64_t H, int64_t E) {
   p.n_tt = (int)n_tt;
   p.n_eb = (int)((E + 16 * p.eb - 1) / (16 * p.eb));
   p.splits = 1;
-  // hidden slices of at least 64 columns, at most kMaxSplits of them; about
-  // 2048 wavefronts share the work
-  const int64_t chunks = H / 32;
-  while (p.splits * 2 <= kMaxSplits && p.splits * 2 <= chunks / 2 && chunks % (p.splits * 2) == 0 &&
+  // hidden slices of whole 128-column blocks (so every slice, and every
+  // 256-column batch inside it, starts on a quantisation group of 64 or 128:
+  // the partial kernel takes a chunk's group from its offset in the batch), at
+  // most kMaxSplits of them; about 2048 wavefronts share the work
+  const int64_t blocks128 = H / 128;
+  while (p.splits * 2 <= kMaxSplits && H % 128 == 0 && blocks128 % (p.splits * 2) == 0 &&
          n_tt * p.n_eb * p.splits * 2 <= 2048)
     p.splits *= 2;
   return p;

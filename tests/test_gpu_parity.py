@@ -38,6 +38,10 @@ def _route_case(seed, T, H, E, k, act, gs, norm, x_std=1.0, router_std=0.02):
     (64, 2048, 128, 8, "bfloat16", 64),
     (600, 2048, 128, 8, "bfloat16", 64),   # large-T router tiling
     (32, 4096, 128, 8, "bfloat16", 64),    # 235B-A22B shape
+    (24, 384, 16, 4, "bfloat16", 64),      # hidden sizes that are not whole
+    (24, 384, 16, 4, "float16", 128),      # 128-column blocks: one hidden split
+    (24, 640, 16, 4, "float16", 64),
+    (300, 1152, 64, 6, "bfloat16", 128),   # nine 128-column blocks
 ])
 @pytest.mark.parametrize("norm", [False, True])
 def test_route_bit_exact(T, H, E, k, act, gs, norm):
@@ -238,6 +242,31 @@ def test_moe_reference_test_shape(regime):
 def test_moe_30b_decode(T):
     x, w = _moe_case(100 + T, T, 2048, 128, 768, "bfloat16")
     _check_moe(x, w, 8, True, "bfloat16", 64, "auto")
+
+
+def test_moe_235b_decode():
+    """H4096 I1536: gate/up through the eight-group slice GEMV (KS 8), down
+    through six-group slices in four k-slices."""
+    x, w = _moe_case(300, 32, 4096, 128, 1536, "bfloat16")
+    _check_moe(x, w, 8, True, "bfloat16", 64, "decode")
+
+
+def test_moe_30b_decode_group128():
+    """Group size 128: the decode GEMV's general scale windows (two groups per
+    128-code pair)."""
+    x, w = _moe_case(400, 32, 2048, 128, 768, "bfloat16", gs=128)
+    _check_moe(x, w, 8, False, "bfloat16", 128, "decode")
+
+
+@pytest.mark.parametrize("H,I,act,gs", [(384, 256, "bfloat16", 64), (384, 256, "float16", 128),
+                                         (640, 320, "float16", 64)])
+def test_moe_odd_slice_widths(H, I, act, gs):
+    """H384: six-group gate/up slices in one k-slice; with group 128 every
+    other row's scale window starts mid-dword (three values per row).  H640:
+    two-group slices in five k-slices (five wavefronts per block), and the
+    down product (five groups per row, no GEMV slicing) on the GEMM."""
+    x, w = _moe_case(500 + H + gs, 24, H, 16, I, act, gs=gs)
+    _check_moe(x, w, 4, True, act, gs, "decode")
 
 
 def test_moe_30b_prefill_sampled_rows():
