@@ -269,6 +269,48 @@ def test_moe_odd_slice_widths(H, I, act, gs):
     _check_moe(x, w, 4, True, act, gs, "decode")
 
 
+def _skewed_case(seed, T, H, E, I, act, s=1.1, gs=64):
+    """Zipf(s) expert popularity: one 64-wide activation group held at 1.0 and
+    log-popularity offsets in those router columns."""
+    x, w = O.make_inputs(seed, T, H, E, I, act, gs)
+    x = np.array(x)
+    x[:, :64] = 1.0
+    rng = np.random.default_rng(seed + 1)
+    wr = O.round_act(rng.standard_normal((E, H)) * 0.02, act)
+    p = np.arange(1, E + 1, dtype=np.float64) ** -s
+    wr[:, :64] = O.round_act(np.log(p / p.sum())[:, None] / 64.0, act)
+    w["router"] = O.quantize(wr, gs, 4, act)
+    return x, w
+
+
+@pytest.mark.parametrize("T,E,k,regime", [(16, 512, 8, "decode"), (20, 1, 1, "decode"),
+                                          (20, 1, 1, "prefill"), (40, 64, 6, "auto")])
+def test_moe_expert_count_extremes(T, E, k, regime):
+    """The most experts the kernels take (512), a single expert, and a top-k
+    that is not a power of two."""
+    x, w = _moe_case(600 + E + k, T, 256, E, 128, "bfloat16")
+    _check_moe(x, w, k, True, "bfloat16", 64, regime)
+
+
+@pytest.mark.parametrize("T,regime", [(300, "decode"), (5, "prefill")])
+def test_moe_forced_regimes(T, regime):
+    """The decode GEMV on a prefill-sized batch (many chunks per expert and
+    units per block), the prefill GEMM on a handful of tokens."""
+    x, w = _moe_case(700 + T, T, 256, 16, 128, "bfloat16")
+    _check_moe(x, w, 4, False, "bfloat16", 64, regime)
+
+
+@pytest.mark.parametrize("regime", ["decode", "prefill"])
+def test_moe_skewed_routing(regime):
+    """Zipf(1.1) popularity: the favourite expert takes many 128-row tiles,
+    rare experts one row or none."""
+    x, w = _skewed_case(800, 512, 256, 16, 128, "bfloat16")
+    _, _, ids, _ = O.route_topk(x, *w["router"], 64, 4, True, "bfloat16")
+    counts = np.bincount(ids.reshape(-1), minlength=16)
+    assert counts.max() >= 3 * counts.mean(), counts  # the case is skewed
+    _check_moe(x, w, 4, True, "bfloat16", 64, regime)
+
+
 def test_moe_30b_prefill_sampled_rows():
     """T=512 through the prefill GEMM, every row checked; T=4096 rows sampled."""
     x, w = _moe_case(200, 512, 2048, 128, 768, "bfloat16")
