@@ -315,3 +315,32 @@ def test_moe_30b_prefill_sampled_rows():
     """T=512 through the prefill GEMM, every row checked; T=4096 rows sampled."""
     x, w = _moe_case(200, 512, 2048, 128, 768, "bfloat16")
     _check_moe(x, w, 8, True, "bfloat16", 64, "prefill")
+
+
+@pytest.mark.parametrize("T", [32, 200])
+def test_moe_graph_replay_matches_eager(T):
+    """The fused forward captured in a HIP graph (as the benchmark times it)
+    gives the eager result on every replay, with eager calls sharing the
+    workspace in between.  T=32 takes the fused route-and-dispatch launch whose
+    counters the router launch zeroes; T=200 the per-block dispatch."""
+    x, w = _moe_case(900 + T, T, 2048, 128, 768, "bfloat16")
+    moe = make_moe(w, "bfloat16", 64, 8, True, DEV)
+    xt = to_act(x, "bfloat16", DEV)
+    y_eager = moe(xt).clone()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        moe(xt)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y_graph = moe(xt)
+    for r in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_graph, y_eager), f"replay {r} differs from the eager result"
+        y_again = moe(xt)
+        torch.cuda.synchronize()
+        assert torch.equal(y_again, y_eager), f"eager call after replay {r} differs"
