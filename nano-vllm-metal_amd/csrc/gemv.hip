@@ -157,8 +157,13 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
 
   __shared__ int s_off[kMaxExperts + 1];  // slot offsets of the experts
   __shared__ int s_cb[kMaxExperts + 1];   // first chunk index of each expert
-  __shared__ int s_orow[2][kChunk];  // output rows of the unit's routed rows
-  __shared__ float s_red[2][kMaxNW][NM][4][64];
+  // Units per barrier: for the single product with an even ring the
+  // reduction and the epilogue run once per two units (the epilogue items
+  // then spread over more wavefronts), over four buffers of partials.  (The
+  // gate/up product measured slower that way.)
+  constexpr int UPB = !DUAL && DEPTH % 2 == 0 ? 2 : 1, NBUF = 2 * UPB;
+  __shared__ int s_orow[NBUF][kChunk];  // output rows of the unit's routed rows
+  __shared__ float s_red[NBUF][kMaxNW][NM][4][64];
 
   hoist_args(a.act, a.act_ld, a.act_rows, a.a_map, a.a_div, a.offsets, a.w0, a.s0, a.b0, a.w1,
              a.s1, a.b1, a.R, a.K, a.gs, a.E, a.out, a.o_map, a.out_ld, KS, NT);
@@ -360,6 +365,57 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
   for (int d = 0; d < DEPTH; ++d) issue(d, d < nu);
   if (kActFirst) act_finish();
 
+  // epilogue metadata of the units since the last barrier
+  int ep_r0[UPB], ep_cnt[UPB], ep_slot0[UPB], ep_buf[UPB];
+  // outputs of the last nun units: items (unit, tile, routed row < cnt,
+  // weight row), one per thread and pass
+  auto epilogue = [&](int nun) {
+    const int n0 = NT * ep_cnt[0] * 16;
+    const int ntot = n0 + (nun > 1 ? NT * ep_cnt[UPB - 1] * 16 : 0);
+    for (int item0 = tid; item0 < ntot; item0 += 64 * NW) {
+      const bool second = UPB > 1 && item0 >= n0;
+      const int item = second ? item0 - n0 : item0;
+      const int cnt = second ? ep_cnt[UPB - 1] : ep_cnt[0];
+      const int ub = second ? ep_buf[UPB - 1] : ep_buf[0];
+      const int c = item & 15, rest = item >> 4;
+      const int t = rest / cnt, tok = rest - t * cnt;
+      const int row = (second ? ep_r0[UPB - 1] : ep_r0[0]) + 16 * t + c;
+      if (row < R) {
+        const int pl = c + 16 * (tok >> 2), pv = tok & 3;
+        float sum[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          // four partials per LDS round trip (reads past KS land on other
+          // entries of s_red and are not added), summed in k-slice order
+          float acc = 0.f;
+          for (int k0 = 0; k0 < KS; k0 += 4) {
+            float part[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) part[j] = s_red[ub][min(t * KS + k0 + j, NW - 1)][m][pv][pl];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (k0 + j < KS) acc = (k0 + j == 0) ? part[0] : acc + part[j];
+          }
+          sum[m] = acc;
+        }
+        uint16_t r;
+        int64_t orow;
+        if constexpr (DUAL) {
+          // reference rounding points: gate and up outputs are act tensors,
+          // silu(gate) * up is rounded once more
+          const float gv = round_act<DT>(sum[0]);
+          const float uv = round_act<DT>(sum[NM - 1]);
+          r = A::from_f32(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * uv);
+          orow = (second ? ep_slot0[UPB - 1] : ep_slot0[0]) + tok;
+        } else {
+          r = A::from_f32(sum[0]);
+          orow = s_orow[ub][tok];
+        }
+        a.out[orow * a.out_ld + row] = r;
+      }
+    }
+  };
+
   // one unit: ring slot d holds unit i of the block's range
   auto step = [&](int d, int i) {
     if (m_ci[d] != cur_ci) {
@@ -448,56 +504,22 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
     // refill this ring slot DEPTH units ahead before the reduction
     issue(d, i + DEPTH < nu);
 
-    // ---- reduce the KS partial tiles in LDS (double-buffered: one barrier
-    // per unit) and finish the outputs; each thread finishes at most one
-    // (tile, routed row, weight row) output per pass, summing the KS partials
-    // in k-slice order
-    const int buf = i & 1;
+    // ---- partial tiles of the unit into LDS; every UPB units one barrier,
+    // then the KS partials of each output are summed in k-slice order
+    const int buf = i % NBUF;
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
       for (int v = 0; v < 4; ++v) s_red[buf][wv][m][v][lane] = o[m][v];
     if (!DUAL && wv == 0 && G == 0) s_orow[buf][col] = my_orow;
-    __syncthreads();
-    // items (tile, routed row < cur_cnt, weight row): the unit's outputs only
-    const int nitem = NT * cur_cnt * 16;
-    for (int item = tid; item < nitem; item += 64 * NW) {
-      const int c = item & 15, rest = item >> 4;
-      const int t = rest / cur_cnt, tok = rest - t * cur_cnt;
-      const int row = r0 + 16 * t + c;
-      if (row < R) {
-        const int pl = c + 16 * (tok >> 2), pv = tok & 3;
-        float sum[NM];
-#pragma unroll
-        for (int m = 0; m < NM; ++m) {
-          // four partials per LDS round trip (reads past KS land on other
-          // entries of s_red and are not added), summed in k-slice order
-          float acc = 0.f;
-          for (int k0 = 0; k0 < KS; k0 += 4) {
-            float part[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) part[j] = s_red[buf][min(t * KS + k0 + j, NW - 1)][m][pv][pl];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              if (k0 + j < KS) acc = (k0 + j == 0) ? part[0] : acc + part[j];
-          }
-          sum[m] = acc;
-        }
-        uint16_t r;
-        int64_t orow;
-        if constexpr (DUAL) {
-          // reference rounding points: gate and up outputs are act tensors,
-          // silu(gate) * up is rounded once more
-          const float gv = round_act<DT>(sum[0]);
-          const float uv = round_act<DT>(sum[NM - 1]);
-          r = A::from_f32(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * uv);
-          orow = cur_slot0 + tok;
-        } else {
-          r = A::from_f32(sum[0]);
-          orow = s_orow[buf][tok];
-        }
-        a.out[orow * a.out_ld + row] = r;
-      }
+    const int u = d % UPB;
+    ep_r0[u] = r0;
+    ep_cnt[u] = cur_cnt;
+    ep_slot0[u] = cur_slot0;
+    ep_buf[u] = buf;
+    if (u == UPB - 1) {
+      __syncthreads();
+      epilogue(UPB);
     }
   };
 
@@ -513,6 +535,11 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
 #pragma unroll
   for (int d = 0; d < DEPTH - 1; ++d)
     if (d < rem) step(d, nfull * DEPTH + d);
+  // a last unit still waiting for its barrier (uniform)
+  if (UPB > 1 && (nu % UPB) != 0) {
+    __syncthreads();
+    epilogue(1);
+  }
 }
 
 struct GemvShape {
