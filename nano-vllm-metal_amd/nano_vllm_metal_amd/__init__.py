@@ -9,6 +9,7 @@ GPU (libnvm_moe.so); nothing falls back to the CPU.
 
 from .linear import QuantizedWeights, dequantize, quantize, quantized_linear, quantized_matmul
 from .moe import Moe, grouped_expert_linear, moe_dispatch, route_and_dispatch, route_topk
+from .loader import load_moe_block, load_moe_blocks, read_config, sparse_layers
 
 __all__ = [
     "QuantizedWeights",
@@ -21,4 +22,8 @@ __all__ = [
     "moe_dispatch",
     "route_and_dispatch",
     "Moe",
+    "load_moe_block",
+    "load_moe_blocks",
+    "read_config",
+    "sparse_layers",
 ]
