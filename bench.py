@@ -11,8 +11,10 @@ them.  The decode value is timed over HIP-graph replays of the layer calls;
 per-kernel durations come from HIP events around each stage in an eager pass.
 
 Also reported: decode batches 1/8/64, prefill of 4096 tokens with uniform and
-Zipf(1.1) routing (MFMA roofline), and the CPU baseline (the C restatement of
-the reference algorithm in oracle/, timed on a bounded sample).
+Zipf(1.1) routing (MFMA roofline), the dense W4A16 projections of the same
+model through quantized_matmul (q/k/o and the lm head, 1/32/4096 rows), and
+the CPU baseline (the C restatement of the reference algorithm in oracle/,
+timed on a bounded sample).
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -293,6 +295,60 @@ def prefill_bench(layers, T, steps, warmup, dev, zipf):
     }
 
 
+# Dense W4A16 projections of the same model (quantized_linear): name, in, out.
+DENSE_SHAPES = (("q_proj", 2048, 4096), ("k_proj", 2048, 512), ("o_proj", 4096, 2048),
+                ("lm_head", 2048, 151936))
+
+
+def dense_bench(dev, rows=(1, 32, 4096), reps=20, n=10):
+    """Kernel time of quantized_matmul per call (HIP-graph replay of `reps`
+    calls, `n` replays) for the 30B-A3B dense projection shapes."""
+    import torch
+    from nano_vllm_metal_amd import quantized_matmul
+
+    gs = 64
+    out = {}
+    for name, N, K in DENSE_SHAPES:
+        g = torch.Generator(device=dev).manual_seed(N + K)
+        w = torch.randint(-2**31, 2**31 - 1, (K, N // 8), dtype=torch.int32, device=dev,
+                          generator=g)
+        sc = (torch.rand(K, N // gs, device=dev, generator=g) * 0.01).to(torch.bfloat16)
+        bi = (torch.rand(K, N // gs, device=dev, generator=g) * -0.04).to(torch.bfloat16)
+        wbytes = K * N // 2 + 2 * 2 * K * (N // gs)
+        res = {"in": N, "out": K, "weight_bytes": wbytes}
+        for M in rows:
+            if name == "lm_head" and M > 32:
+                continue
+            a = torch.randn(M, N, device=dev, generator=g).to(torch.bfloat16)
+            fn = lambda: quantized_matmul(sc, bi, gs, 4, a, w, True)  # noqa: E731
+            st = torch.cuda.Stream()
+            st.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(st):
+                for _ in range(3):
+                    fn()
+            torch.cuda.current_stream().wait_stream(st)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(reps):
+                    fn()
+            graph.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(n):
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (n * reps)
+            res[str(M)] = {"us": us, "weight_gbs": wbytes / us / 1e3,
+                           "tflops": 2.0 * M * N * K / us / 1e6}
+            del graph
+        out[name] = res
+        del w, sc, bi
+    return out
+
+
 def cpu_baseline(layer, T, seconds, dev):
     """The C restatement of the reference path (oracle/moe_ref.c) on host cores."""
     import numpy as np
@@ -450,6 +506,8 @@ def main():
                     help="also run a plain 256 MiB device copy (calibrates HBM byte counters)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="measure only the 4096-token prefill with uniform routing")
+    ap.add_argument("--dense-only", action="store_true",
+                    help="measure only the dense W4A16 projections (quantized_matmul)")
     ap.add_argument("--rocprof-summary", metavar="DIR",
                     help="summarise rocprofv3 CSV output under DIR and exit (no GPU)")
     ap.add_argument("--write-traffic", action="store_true",
@@ -478,6 +536,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.dense_only:
+        log("[bench] dense W4A16 projections")
+        print(json.dumps({"dense": dense_bench(dev)}), flush=True)
+        return
     if args.prefill_only:
         log("[bench] building 2 layers of 30B-A3B MoE weights")
         layers = make_layers(2, H, E, I, gs, dev)
@@ -555,6 +617,8 @@ def main():
                 f"{r['layer_tflops']:.0f} TFLOP/s, kernels {r['kernel_us']}")
             if zipf:
                 del lay
+        log("[bench] dense W4A16 projections")
+        out["dense"] = dense_bench(dev)
         u = out["prefill"]["uniform"]
         out["prefill_roofline"] = {
             "kernel": "gemm_kernel<bf16, gate/up+SwiGLU> (nvm_moe_expert_gateup, prefill)",

@@ -63,7 +63,12 @@ const char *nvm_last_error(void);
  * CPU loop :84-148), which `quantized_linear` uses for the router logits
  * (layers/linear.py:92-126, layers/moe.py:43).  Like the reference, only
  * transpose_b = 1 and bits = 4 are accepted; group_size may be 64 or 128.
- * The dot products accumulate in float64 and are rounded once to act.
+ * Router-sized products (K <= 512 outputs, M <= 64 rows) accumulate in
+ * float64 and are rounded once to act.  The rest (the projections of a dense
+ * layer, prefill batches) run on the expert-product kernels as one expert,
+ * accumulating in float32 as the reference's kernels do
+ * (quantized_matmul.metal:25-44, :100-110), when N is a multiple of 64 up to
+ * 8192 and K a multiple of 16; other shapes take the float64 path.
  * Needs no workspace.
  */
 int nvm_quantized_matmul(const void *scales, const void *biases, int group_size, int bits,

@@ -182,6 +182,15 @@ int nvm_abi_version(void) { return NVM_ABI_VERSION; }
 
 const char *nvm_last_error(void) { return g_err.c_str(); }
 
+// Router-sized products (at most 512 outputs over at most 64 rows) run on the
+// float64 router kernel, which rounds the exact sum once.  The rest (dense
+// projections, prefill batches) run on the expert products as one expert with
+// no offsets, accumulating in fp32 like the reference's kernel: exact float64
+// sums are bound by the f64 matrix cores (2048 -> 512 over 4096 rows: 171 us
+// against 48 us).
+constexpr int64_t kExactOutMax = 512;
+constexpr int64_t kExactRowsMax = 64;
+
 int nvm_quantized_matmul(const void *scales, const void *biases, int group_size, int bits,
                          const void *a, const uint32_t *b, int transpose_b, void *out, int64_t M,
                          int64_t N, int64_t K, int dtype, nvm_stream_t stream) {
@@ -193,6 +202,36 @@ int nvm_quantized_matmul(const void *scales, const void *biases, int group_size,
   NVM_REQUIRE(N % group_size == 0, "quantized_matmul: N=%lld not divisible by group_size %d",
               (long long)N, group_size);
   if (M == 0) return NVM_OK;
+  // (the product kernels address weights and activations through 32-bit
+  // buffer offsets)
+  if ((K > kExactOutMax || M > kExactRowsMax) && K % 16 == 0 && N % 64 == 0 && N <= kMaxProductK &&
+      K * (N / 2) <= 0x7FFF0000ll && M * N * 2 <= 0x7FFF0000ll) {
+    nvm::GroupedArgs g{};
+    g.act = (const uint16_t *)a;
+    g.act_ld = N;
+    g.act_rows = M;
+    g.a_map = nullptr;
+    g.a_div = 1;
+    g.offsets = nullptr;  // one expert over all M rows
+    g.w0 = b;
+    g.s0 = (const uint16_t *)scales;
+    g.b0 = (const uint16_t *)biases;
+    g.R = (int)K;
+    g.K = (int)N;
+    g.gs = group_size;
+    g.E = 1;
+    g.out = (uint16_t *)out;
+    g.o_map = nullptr;
+    g.out_ld = K;
+    // The GEMV streams the weights once per 16-row chunk; the GEMM once, but
+    // a block runs all N/64 k-steps in sequence, so a grid of fewer blocks
+    // than CUs leaves the GEMM latency-bound.  GEMV up to two chunks, and up
+    // to 32 chunks while the GEMM grid would not fill the chip.
+    const int64_t gemm_blocks = (M + nvm::kGemmBM - 1) / nvm::kGemmBM * ((K + 255) / 256);
+    const bool decode = nvm::gemv_supports((int)N) &&
+                        (M <= 32 || (M <= 512 && gemm_blocks < nvm::cu_count()));
+    return run_products(dtype, decode, false, g, M, (hipStream_t)stream);
+  }
   NVM_TRY_HIP(nvm::launch_route_partial(dtype, a, M, N, b, scales, biases, K, group_size, true,
                                         nullptr, out, nullptr, (hipStream_t)stream));
   return NVM_OK;

@@ -28,6 +28,7 @@ struct Act<DT_BF16> {
   // mantissa bits gives the exact value 128 + q (the bf16 ulp at 128 is 1).
   static constexpr uint32_t kMagic2 = 0x43004300u;
   static constexpr float kMagic = 128.0f;
+  static constexpr int kCodeShift = 0;  // mantissa bit of the code's lsb
   static constexpr uint32_t kOne2 = 0x3F803F80u;  // (1.0, 1.0)
   static constexpr int kPrec = 8;                 // significant bits
   static constexpr int kEmin = -126;              // exponent of the smallest normal
@@ -58,9 +59,13 @@ struct Act<DT_BF16> {
 
 template <>
 struct Act<DT_F16> {
-  // Two copies of fp16(1024.0): the fp16 ulp at 1024 is 1, so 1024 + q is exact.
-  static constexpr uint32_t kMagic2 = 0x64006400u;
-  static constexpr float kMagic = 1024.0f;
+  // Two copies of fp16(64.0) with the code in mantissa bits 4..7: the weight
+  // of bit 4 at 64 is 1, so the value is 64 + q exactly.  (Bits 0..3 would
+  // need M = 1024, and the M*s*sum(x) term that cancels afterwards would cost
+  // sixteen times more float32 precision.)
+  static constexpr uint32_t kMagic2 = 0x54005400u;
+  static constexpr float kMagic = 64.0f;
+  static constexpr int kCodeShift = 4;
   static constexpr uint32_t kOne2 = 0x3C003C00u;
   static constexpr int kPrec = 11;
   static constexpr int kEmin = -14;
@@ -134,17 +139,26 @@ __device__ __forceinline__ u32x4 pair_order(u32x4 d) {
 
 // Expand one packed word (codes q0..q7 at bits 4j) into four dwords of
 // 16-bit floats (M+q0, M+q4)(M+q1, M+q5)(M+q2, M+q6)(M+q3, M+q7), exactly,
-// where M is the dtype's magic constant (128 for bf16, 1024 for fp16).
-// With `mask` = 0x000F000F in an SGPR and `magic` (two copies of M) in a VGPR,
-// each dword is one v_and_or_b32 (after a shift for the upper three): gfx9
-// VOP3 encodings take no literal and read at most one SGPR, so with both
+// where M is the dtype's magic constant and SH its code shift (bf16: M = 128,
+// codes in mantissa bits 0..3; fp16: M = 64, bits 4..7).  With `mask` =
+// 0x000F000F << SH in an SGPR and `magic` (two copies of M) in a VGPR, each
+// dword is one v_and_or_b32 after at most one shift (three of the four):
+// gfx9 VOP3 encodings take no literal and read at most one SGPR, so with both
 // constants as literals the compiler would emit an AND and an OR.
+template <int S>
+__device__ __forceinline__ uint32_t shift_by(uint32_t w) {
+  if constexpr (S >= 0)
+    return w << S;
+  else
+    return w >> -S;
+}
+template <int SH>
 __device__ __forceinline__ u32x4 nibble_pairs_v(uint32_t w, uint32_t mask, uint32_t magic) {
   u32x4 o;
-  o.x = (w & mask) | magic;
-  o.y = ((w >> 4) & mask) | magic;
-  o.z = ((w >> 8) & mask) | magic;
-  o.w = ((w >> 12) & mask) | magic;
+  o.x = (shift_by<SH>(w) & mask) | magic;
+  o.y = (shift_by<SH - 4>(w) & mask) | magic;
+  o.z = (shift_by<SH - 8>(w) & mask) | magic;
+  o.w = (shift_by<SH - 12>(w) & mask) | magic;
   return o;
 }
 // The constants above as register values the compiler cannot fold back into
@@ -158,17 +172,6 @@ __device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
   uint32_t r;
   asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(v));
   return r;
-}
-
-template <int DT>
-__device__ __forceinline__ u32x4 nibble_pairs(uint32_t w) {
-  constexpr uint32_t m = Act<DT>::kMagic2;
-  u32x4 o;
-  o.x = (w & 0x000F000Fu) | m;
-  o.y = ((w >> 4) & 0x000F000Fu) | m;
-  o.z = ((w >> 8) & 0x000F000Fu) | m;
-  o.w = ((w >> 12) & 0x000F000Fu) | m;
-  return o;
 }
 
 // Kernel arguments are read from the kernarg segment by scalar loads that the

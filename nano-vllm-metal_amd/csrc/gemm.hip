@@ -77,11 +77,14 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
 
   // m-tile list: exclusive prefix over experts of ceil(count / BM), built by
   // wavefront 0 from the expert offsets (E <= kMaxExperts)
+  // expert slot offsets (none: one expert over all act_rows rows, the dense
+  // product)
+  auto offs = [&](int i) { return a.offsets ? a.offsets[i] : (i == 0 ? 0 : (int)a.act_rows); };
   if (wv == 0) {
     int carry = 0;
     for (int c0 = 0; c0 < a.E; c0 += 64) {
       const int e = c0 + lane;
-      const int tv = e < a.E ? (a.offsets[e + 1] - a.offsets[e] + BM - 1) / BM : 0;
+      const int tv = e < a.E ? (offs(e + 1) - offs(e) + BM - 1) / BM : 0;
       int inc = tv;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
@@ -116,8 +119,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
       hi = mid - 1;
   }
   const int e = lo;
-  const int m0 = a.offsets[e] + (mt - s_tiles[e]) * BM;
-  const int mcnt = min(BM, a.offsets[e + 1] - m0);
+  const int m0 = offs(e) + (mt - s_tiles[e]) * BM;
+  const int mcnt = min(BM, offs(e + 1) - m0);
   const int R = a.R, KW = a.K >> 3, GPR = a.K / a.gs;
   const int n0 = nt * (DUAL ? WROWS / 2 : WROWS);
 

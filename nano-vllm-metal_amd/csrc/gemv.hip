@@ -62,20 +62,6 @@ constexpr int kMaxNW = 8;   // wavefronts per block
 #endif
 constexpr int kWavesPerSimd = NVM_GEMV_WAVES_PER_SIMD;
 
-// Compute units of the current device (cached per device).
-int cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 // Scale or bias values of one weight row over the k-slice, read as an
 // aligned window: the 16-bit value for group g of the slice is half
 // sb_index(g) of the window (a few values on either side are read and unused).
@@ -176,12 +162,17 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
   if (wv == 0) {
     // every offset in flight at once (one round trip, not one per 64
     // experts), then the chunk counts from LDS
+    // (no offsets: one expert over all act_rows rows, the dense product)
     constexpr int kOffRegs = kMaxExperts / 64 + 1;
-    const rsrc_t off_r = make_rsrc(a.offsets, (uint32_t)(E + 1) * 4);
     int ov[kOffRegs];
+    if (a.offsets) {
+      const rsrc_t off_r = make_rsrc(a.offsets, (uint32_t)(E + 1) * 4);
 #pragma unroll
-    for (int j = 0; j < kOffRegs; ++j)
-      if (64 * j <= E) ov[j] = (int)bload4(off_r, (64 * j + lane) * 4, 0);
+      for (int j = 0; j < kOffRegs; ++j)
+        if (64 * j <= E) ov[j] = (int)bload4(off_r, (64 * j + lane) * 4, 0);
+    } else {
+      ov[0] = lane == 1 ? (int)a.act_rows : 0;
+    }
 #pragma unroll
     for (int j = 0; j < kOffRegs; ++j)
       if (64 * j <= E && 64 * j + lane <= E) s_off[64 * j + lane] = ov[j];
@@ -348,8 +339,9 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
   const int sb_h = SBA ? 0 : ((tile * 16 + col) * GPR + sidx0) & 1;
   auto sb_index = [&](int g) { return SBA ? g : ((ks * GPW + g) >> gsh) - sidx0 + sb_h; };
   // nibble-expansion constants in registers (one v_and_or_b32 per dword)
-  const uint32_t nib_mask = sgpr_const(0x000F000Fu);
+  const uint32_t nib_mask = sgpr_const(0x000F000Fu << A::kCodeShift);
   const uint32_t magic = vgpr_const(A::kMagic2);
+  auto expand = [&](uint32_t w) { return nibble_pairs_v<A::kCodeShift>(w, nib_mask, magic); };
   auto scale_f = [&](const SB &v, int g) { return A::to_f32(sb_at(v, sb_index(g))); };
 
   // The first chunk's activations are requested before the ring fill: loads
@@ -443,7 +435,7 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
           if (h0 + hh < GP) {
             const u32x4 w = swap_pairs(wq[d][m][h0 + hh]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) bop[hh][m][j] = nibble_pairs_v(w[j], nib_mask, magic);
+            for (int j = 0; j < 4; ++j) bop[hh][m][j] = expand(w[j]);
           }
 #pragma unroll
       for (int step2 = 0; step2 < 2; ++step2)
@@ -475,9 +467,9 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
           const u32x4 w = swap_pairs(wq[d][m][h]);
 #pragma unroll
           for (int q = 0; q < 2; ++q) {
-            f32x4 acc = A::mfma16(xa[h][2 * q], nibble_pairs_v(w[2 * q], nib_mask, magic),
+            f32x4 acc = A::mfma16(xa[h][2 * q], expand(w[2 * q]),
                                   f32x4{0.f, 0.f, 0.f, 0.f});
-            acc = A::mfma16(xa[h][2 * q + 1], nibble_pairs_v(w[2 * q + 1], nib_mask, magic), acc);
+            acc = A::mfma16(xa[h][2 * q + 1], expand(w[2 * q + 1]), acc);
             const float s = scale_f(sv[d][m], 2 * h + q);
 #pragma unroll
             for (int v = 0; v < 4; ++v) o[m][v] = fmaf(s, acc[v], o[m][v]);
@@ -590,6 +582,20 @@ hipError_t launch_t(const GroupedArgs &a, const GemvShape &s, hipStream_t st) {
 }
 
 }  // namespace
+
+// Compute units of the current device (cached per device).
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
 
 bool gemv_supports(int K) {
   GemvShape s;

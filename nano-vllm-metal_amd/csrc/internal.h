@@ -18,7 +18,7 @@ struct GroupedArgs {
   int64_t act_rows;  // rows of `act` (bounds of the activation buffer)
   const int32_t *a_map;
   int a_div;
-  const int32_t *offsets;  // [E+1] slot ranges per expert
+  const int32_t *offsets;  // [E+1] slot ranges per expert; NULL (E = 1): all act_rows rows
   const uint32_t *w0;
   const uint16_t *s0, *b0;
   const uint32_t *w1;
@@ -65,6 +65,7 @@ hipError_t launch_dispatch(const int32_t *ids, int64_t n, int64_t E, int32_t *of
 // Decode products need the reduction dimension in at most 8 slices of 1, 2,
 // 4 or 8 whole 64-wide groups.
 bool gemv_supports(int K);
+int cu_count();  // compute units of the current device
 hipError_t launch_gemv(int dtype, bool dual, const GroupedArgs &a, hipStream_t st);
 constexpr int kGemmBM = 128;   // prefill tile rows (routed pairs)
 constexpr int kGemmBN = 128;   // prefill tile columns per weight matrix

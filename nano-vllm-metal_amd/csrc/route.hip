@@ -31,6 +31,10 @@ typedef double f64x4 __attribute__((ext_vector_type(4)));
 // chunk exactly once, 8 consecutive bf16/fp16 values and one packed word per
 // lane.  The D fragment of the float64 MFMA is row-interleaved: element i of
 // lane (c, G) is token t0+G+4i of expert e0+c.
+//
+// With `fin` (logits rounded straight to the activation dtype, no partial
+// buffer) the block's four wavefronts take the four hidden splits of one tile
+// and add their float64 partials in LDS, in split order, before rounding.
 template <int DT, int EB, bool SB_VEC>
 __global__ __launch_bounds__(256) void route_mfma_kernel(
     const uint16_t *__restrict__ x, int T, int H, const uint32_t *__restrict__ wr,
@@ -40,14 +44,17 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(
   using A = Act<DT>;
   constexpr int NC = 8;  // 32-wide chunks per batch; all loads of a batch are in flight together
   hoist_args(x, T, H, wr, sr, br, E, gs, KR, n_tt, n_eb, splits, part, fin, done);
-  const int lane = threadIdx.x & 63;
-  const int item = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   // the finalising launch that follows counts its blocks from zero
   if (done && blockIdx.x == 0 && threadIdx.x == 0) *done = 0u;
-  if (item >= n_tt * n_eb * splits) return;
+  // in-block splits: one tile per block (uniform exit, the block meets at a
+  // barrier); else one (tile, split) item per wavefront
+  const bool in_block = fin && splits > 1;
+  const int item = in_block ? blockIdx.x : blockIdx.x * (blockDim.x >> 6) + wv;
+  if (item >= n_tt * n_eb * (in_block ? 1 : splits)) return;
   const int tt = item % n_tt;
   const int eb = (item / n_tt) % n_eb;
-  const int z = item / (n_tt * n_eb);
+  const int z = in_block ? wv : item / (n_tt * n_eb);
   const int col = lane & 15, G = lane >> 4;
   const int t = tt * 16 + col;
   const int k_begin = z * KR;
@@ -133,11 +140,31 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(
     }
   }
 #pragma unroll
+  for (int b = 0; b < EB; ++b)
+#pragma unroll
+    for (int h = 1; h < CH; ++h) acc[b][0] += acc[b][h];
+  if (in_block) {
+    // [split][tile b][element i][lane]
+    extern __shared__ double s_part[];
+#pragma unroll
+    for (int b = 0; b < EB; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_part[((wv * EB + b) * 4 + i) * 64 + lane] = acc[b][0][i];
+    __syncthreads();
+    if (wv != 0) return;
+#pragma unroll
+    for (int b = 0; b < EB; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        double sum = s_part[((0 * EB + b) * 4 + i) * 64 + lane];
+        for (int zz = 1; zz < splits; ++zz) sum += s_part[((zz * EB + b) * 4 + i) * 64 + lane];
+        acc[b][0][i] = sum;
+      }
+  }
+#pragma unroll
   for (int b = 0; b < EB; ++b) {
     const int e = (eb * EB + b) * 16 + col;
     if (!e_ok[b]) continue;
-#pragma unroll
-    for (int h = 1; h < CH; ++h) acc[b][0] += acc[b][h];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tok = tt * 16 + G + 4 * i;
@@ -306,6 +333,8 @@ __global__ __launch_bounds__(256) void route_finalize_dispatch_kernel(
   block_sort([&](int p) { return ids_lds[p]; }, T * k, E, nbits, lds, offsets, sorted);
 }
 
+constexpr int kFinSplits = 4;  // hidden splits of a rounded-logits block (its wavefronts)
+
 struct RoutePlan {
   int eb, n_tt, n_eb, splits;
 };
@@ -334,20 +363,22 @@ template <int DT, int EB>
 hipError_t launch_mfma_t(const void *x, int64_t T, int64_t H, const uint32_t *wr, const void *sr,
                          const void *br, int64_t E, int gs, const RoutePlan &p, double *partial,
                          void *fin, unsigned *done, hipStream_t st) {
+  const bool in_block = fin && p.splits > 1;
   const int64_t items = (int64_t)p.n_tt * p.n_eb * p.splits;
-  dim3 grid((unsigned)((items + 3) / 4));
+  dim3 grid((unsigned)(in_block ? (int64_t)p.n_tt * p.n_eb : (items + 3) / 4));
+  const size_t lds = in_block ? sizeof(double) * kFinSplits * EB * 4 * 64 : 0;
   // 8-byte scale loads need 4 groups (group 64) or 2 groups (group 128) of
   // whole dwords at every 256-column batch start
   const int64_t gpr = H / gs;
   const int sb_vec =
       (H / p.splits) % 256 == 0 && ((gs == 64 && gpr % 4 == 0) || (gs == 128 && gpr % 2 == 0));
   if (sb_vec)
-    hipLaunchKernelGGL((route_mfma_kernel<DT, EB, true>), grid, dim3(256), 0, st,
+    hipLaunchKernelGGL((route_mfma_kernel<DT, EB, true>), grid, dim3(256), lds, st,
                        (const uint16_t *)x, (int)T, (int)H, wr, (const uint16_t *)sr,
                        (const uint16_t *)br, (int)E, gs, (int)(H / p.splits), p.n_tt, p.n_eb,
                        p.splits, partial, (uint16_t *)fin, done);
   else
-    hipLaunchKernelGGL((route_mfma_kernel<DT, EB, false>), grid, dim3(256), 0, st,
+    hipLaunchKernelGGL((route_mfma_kernel<DT, EB, false>), grid, dim3(256), lds, st,
                        (const uint16_t *)x, (int)T, (int)H, wr, (const uint16_t *)sr,
                        (const uint16_t *)br, (int)E, gs, (int)(H / p.splits), p.n_tt, p.n_eb,
                        p.splits, partial, (uint16_t *)fin, done);
@@ -371,7 +402,9 @@ hipError_t launch_route_partial(int dtype, const void *x, int64_t T, int64_t H,
                                 int gs, bool final_act, double *partial, void *fin,
                                 unsigned *done, hipStream_t st) {
   RoutePlan p = route_plan(T, H, E);
-  if (final_act) p.splits = 1;
+  // rounded logits: the four wavefronts of a block split the hidden range
+  // when it is whole 128-column blocks per split
+  if (final_act) p.splits = H % (128 * kFinSplits) == 0 ? kFinSplits : 1;
   return dtype == DT_BF16
              ? launch_route_t<DT_BF16>(x, T, H, wr, sr, br, E, gs, p, partial, fin, done, st)
              : launch_route_t<DT_F16>(x, T, H, wr, sr, br, E, gs, p, partial, fin, done, st);

@@ -119,8 +119,10 @@ def quantized_matmul(scales: torch.Tensor, biases: torch.Tensor, group_size: int
 
     Mirrors linear.py:73-89 / ``_ext.quantized_matmul``: ``transpose_b`` must
     be True (quantized_matmul.cpp:56-58), ``a``, ``scales`` and ``biases`` share
-    the f16/bf16 dtype (:26-37).  Accumulates in float64, rounds once to
-    ``a.dtype``.
+    the f16/bf16 dtype (:26-37).  Router-sized products (up to 512 outputs
+    over up to 64 rows) accumulate in float64 and round once to ``a.dtype``;
+    the rest run on the expert GEMV or GEMM as a single expert, accumulating
+    in float32 like the reference's kernels (quantized_matmul.metal:25-44).
     """
     lib = _lib.load()
     if a.dtype != scales.dtype or scales.dtype != biases.dtype:

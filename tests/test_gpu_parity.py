@@ -105,8 +105,14 @@ def test_quantized_matmul_identity_known_answer():
         assert np.array_equal(to_np(out), ref)
 
 
-@pytest.mark.parametrize("M,N,K,act,gs", [(3, 128, 5, "float16", 128), (300, 512, 96, "bfloat16", 64),
-                                          (7, 2048, 128, "bfloat16", 64)])
+# Router-sized products (up to 512 outputs over up to 64 rows, or output
+# widths the products do not tile): float64 sums, one rounding -> bit-exact.
+# N a multiple of 512 splits the sums over a block's four wavefronts.
+@pytest.mark.parametrize("M,N,K,act,gs", [(3, 128, 5, "float16", 128), (300, 512, 100, "bfloat16", 64),
+                                          (7, 2048, 128, "bfloat16", 64),
+                                          (37, 1024, 200, "float16", 128),
+                                          (1, 4096, 512, "bfloat16", 64),
+                                          (20, 640, 48, "bfloat16", 64)])
 def test_quantized_matmul_matches_oracle(M, N, K, act, gs):
     from nano_vllm_metal_amd import quantized_matmul
 
@@ -117,6 +123,49 @@ def test_quantized_matmul_matches_oracle(M, N, K, act, gs):
     out = quantized_matmul(to_act(s, act, DEV), to_act(b, act, DEV), gs, 4, to_act(a, act, DEV),
                            to_words(wq, DEV), transpose_b=True)
     assert np.array_equal(to_np(out), O.quantized_matmul(a, wq, s, b, gs, act))
+
+
+# Dense projections (more than 512 outputs, or more than 64 rows) run on the
+# expert GEMV (N <= 4096; up to 32 rows, or up to 512 while the GEMM grid
+# would be smaller than the chip) or the GEMM, accumulating in float32 like
+# quantized_matmul.metal:25-44.  The
+# GEMV's sums equal the unrounded dequantised products; the GEMM rounds each
+# dequantised weight to the activation dtype before its MFMA, as MLX's qmm
+# does (the reference's NVM_QMATMUL_BACKEND=mlx path, layers/linear.py:109-117).
+# Both are held to the tolerance against the exactly rounded oracle (outputs
+# are of unit scale, so the mean error is taken relative to the largest
+# output), and most elements must equal the exactly rounded result of their
+# own numerics.
+@pytest.mark.parametrize("M,N,K,act,gs,path", [
+    (1, 2048, 4096, "bfloat16", 64, "gemv"),     # four-group slices, aligned scales
+    (7, 2048, 1024, "float16", 128, "gemv"),     # group 128
+    (16, 4096, 2048, "bfloat16", 128, "gemv"),   # eight-group slices, full chunk
+    (3, 1024, 528, "bfloat16", 64, "gemv"),      # output tile past the last row
+    (17, 2048, 768, "bfloat16", 64, "gemv"),     # two chunks, the second of one row
+    (300, 1024, 4096, "float16", 64, "gemv"),    # 19 chunks (GEMM grid of 48 blocks)
+    (5, 6144, 1024, "bfloat16", 128, "gemm"),    # N the GEMV does not slice
+    (600, 1024, 1024, "float16", 64, "gemm"),    # beyond 512 rows, ragged last tile
+    (700, 2048, 768, "bfloat16", 64, "gemm"),
+    (65, 2048, 512, "bfloat16", 64, "gemv"),     # narrow output beyond 64 rows
+    (300, 512, 96, "bfloat16", 64, "gemv"),
+    (4096, 2048, 128, "float16", 128, "gemm"),
+])
+def test_quantized_matmul_dense_products(M, N, K, act, gs, path):
+    from nano_vllm_metal_amd import quantized_matmul
+
+    rng = np.random.default_rng(M * 7 + N + K)
+    a = O.round_act(rng.standard_normal((M, N)), act)
+    w = O.round_act(rng.standard_normal((K, N)) * 0.02, act)
+    wq, s, b = O.quantize(w, gs, 4, act)
+    out = quantized_matmul(to_act(s, act, DEV), to_act(b, act, DEV), gs, 4, to_act(a, act, DEV),
+                           to_words(wq, DEV), transpose_b=True)
+    ref = O.quantized_matmul(a, wq, s, b, gs, act)
+    assert_moe_close(out, ref, act, f"quantized_matmul {M}x{N}x{K}", mae_rel=True)
+    if path == "gemm":
+        wd = O.round_act(O.dequantize(wq, s, b, gs), act)
+        ref = O.round_act(np.asarray(a, np.float64) @ wd.T, act)
+    same = np.mean(to_np(out) == ref)
+    assert same > 0.9, f"{path}: {same:.3f} of the outputs equal the rounded exact result"
 
 
 # ---------------------------------------------------------------- dispatch
