@@ -9,10 +9,11 @@
 #include "nvm_moe.h"
 
 namespace {
-
 thread_local std::string g_err;
+}  // namespace
 
-int fail(int code, const char *fmt, ...) {
+namespace nvm {
+int set_error(int code, const char *fmt, ...) {
   char buf[512];
   va_list ap;
   va_start(ap, fmt);
@@ -21,6 +22,11 @@ int fail(int code, const char *fmt, ...) {
   g_err = buf;
   return code;
 }
+}  // namespace nvm
+
+namespace {
+
+int (*const fail)(int, const char *, ...) = nvm::set_error;
 
 #define NVM_TRY_HIP(expr)                                                              \
   do {                                                                                 \

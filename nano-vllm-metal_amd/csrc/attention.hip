@@ -1,0 +1,566 @@
+// Paged attention over a paged KV cache (declared in include/nvm_attention.h).
+//
+// Restates the reference's op metal/src/paged_attention.cpp (CPU loop
+// :122-296, int8 decode loop :298-410, decode split-K kernel
+// paged_attention.metal:277-409): per query row, an online softmax in float32
+// over the key positions j < min(context_len, max_pages * page_size) whose
+// page id (block_table[b, j / page_size]) is not negative, causal rows seeing
+// j <= i + context_len - L, then the probability-weighted sum of the values.
+// Pages are [P, num_kv_heads, page_size, D] (cache/paged.py).
+//
+// Decode kernel (L = 1, f16/bf16 pages, D = 64 or 128).  A block owns one
+// (request, kv head, group of up to RP query heads, context split): the query
+// heads that share a kv head read each key and value row once (grouped-query
+// sharing; the reference reads them once per query head).  Its four
+// wavefronts take 64-position tiles of the split in turn.
+//   * Scores on the matrix cores, S^T = K . Q^T with v_mfma_f32_16x16x32 in
+//     the page dtype: the key rows are the A operand straight from memory
+//     (lane (c, G) loads 16 bytes: position c of a 16-row subtile, dims
+//     32k + 8G .. +7), and the float32 query is split into three page-dtype
+//     parts q = q1 + q2 + q3 (exact for bf16; for f16 to the f16 subnormal
+//     range), so every product is exact and the sums are float32 as in the
+//     reference.  C holds head c, positions 4G..4G+3 of each subtile.
+//   * Softmax in base 2 (scores pre-scaled by scale * log2 e): the tile's
+//     row maximum is two lane swaps, the row sums stay lane-partial.
+//   * P . V on the VALU: the tile's probabilities go to LDS; a group of D/8
+//     lanes (8 dims each, 16-byte value loads) covers a value row, and each
+//     of the 64/(D/8) groups takes D/8 consecutive positions of the tile.
+//   * The four wavefronts' (max, sum, output) partials meet in LDS; with more
+//     than one split per row they go to the workspace and a second launch
+//     combines them.
+// Other shapes (L > 1, f32 or int8 pages, other head dims) run one wavefront
+// per query row over the context, with the reference's formula per element.
+#include <math.h>
+
+#include <algorithm>
+
+#include "common.h"
+#include "internal.h"
+#include "nvm_attention.h"
+
+namespace nvm {
+
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kTile = 64;           // context positions per wavefront step
+constexpr int kTargetBlocks = 512;  // decode: split the context until about this many blocks
+constexpr int kMaxRowDim = 256;     // head dim of the row kernel (4 values per lane)
+
+struct PagedArgs {
+  const float *q;
+  const void *kp, *vp;
+  const float *ks, *vs;
+  const int32_t *bt, *lens;
+  float *out, *part_o, *part_ml;
+  int P, L, D, page_size, max_pages, Hkv, Hq, R, HG, S, span, causal;
+  float scale2;  // scale * log2(e): scores are kept in base 2
+};
+
+// Hand-over of LDS data between the lanes of one wavefront: its LDS
+// operations execute in program order, so only the compiler must not move
+// loads or stores across this point.
+__device__ __forceinline__ void wave_lds_sync() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// q = p0 + p1 + p2 in the page dtype, for four pairs of values.
+template <int DT>
+__device__ __forceinline__ void split3(const float (&x)[8], u32x4 &p0, u32x4 &p1, u32x4 &p2) {
+  using A = Act<DT>;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float a0 = x[2 * i], a1 = x[2 * i + 1];
+    const uint32_t h = A::pack2(a0, a1);
+    a0 -= A::lo(h);
+    a1 -= A::hi(h);
+    const uint32_t m = A::pack2(a0, a1);
+    a0 -= A::lo(m);
+    a1 -= A::hi(m);
+    p0[i] = h;
+    p1[i] = m;
+    p2[i] = A::pack2(a0, a1);
+  }
+}
+
+template <int DT, int DH, int RP>
+__global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
+  using A = Act<DT>;
+  constexpr int NC = DH / 32;        // 32-dim chunks of a score MFMA
+  constexpr int LPD = DH / 8;        // lanes per value row in P.V, 8 dims each
+  constexpr int PPG = LPD;           // positions per lane group per tile (64 / (64 / LPD))
+  __shared__ float s_p[4][kTile][RP];
+  __shared__ float s_alpha[4][RP];
+  __shared__ int s_row[4][kTile];
+  __shared__ float s_o[4][RP][DH];
+  __shared__ float s_m[4][RP], s_l[4][RP];
+
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int c16 = lane & 15, G = lane >> 4;
+  int blk = blockIdx.x;
+  const int s = blk % a.S;
+  blk /= a.S;
+  const int hg = blk % a.HG;
+  blk /= a.HG;
+  const int kvh = blk % a.Hkv;
+  const int b = blk / a.Hkv;
+  const int nh = min(RP, a.R - hg * RP);
+  const int64_t n0 = (int64_t)b * a.Hq + (int64_t)kvh * a.R + hg * RP;
+  const int ctx = min(a.lens[b], a.max_pages * a.page_size);
+  const int p0 = s * a.span;
+  const int p1 = min(p0 + a.span, ctx);
+
+  // B operand of the score MFMAs: query head c16, dims 32k + 8G .. +7
+  u32x4 qb[NC][3];
+  {
+    const bool ok = c16 < nh;
+    const float *qp = a.q + (n0 + (ok ? c16 : 0)) * DH;
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      const int d0 = 32 * k + 8 * G;
+      const f32x4 x0 = ok ? *(const f32x4 *)(qp + d0) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 x1 = ok ? *(const f32x4 *)(qp + d0 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+      split3<DT>(x, qb[k][0], qb[k][1], qb[k][2]);
+    }
+  }
+
+  const uint32_t kv_bytes = (uint32_t)((int64_t)a.P * a.Hkv * a.page_size * DH * 2);
+  const rsrc_t kr = make_rsrc(a.kp, kv_bytes), vr = make_rsrc(a.vp, kv_bytes);
+  const int64_t bt_row = (int64_t)b * a.max_pages;
+  const int dd = 8 * (lane % LPD), pgrp = lane / LPD;
+
+  float m_run = -INFINITY, l_run = 0.f;  // head c16; l_run is this lane's share
+  float o[RP][8];
+#pragma unroll
+  for (int r = 0; r < RP; ++r)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[r][j] = 0.f;
+
+  for (int t0 = p0 + kTile * wv; t0 < p1; t0 += 4 * kTile) {
+    // element offsets of the key/value rows of positions t0 + 16u + c16
+    int rowoff[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int pos = t0 + 16 * u + c16;
+      int pg = -1;
+      if (pos < p1) pg = a.bt[bt_row + pos / a.page_size];
+      rowoff[u] = (pg >= 0 && pg < a.P)
+                      ? ((pg * a.Hkv + kvh) * a.page_size + pos % a.page_size) * DH
+                      : -1;
+    }
+    u32x4 kop[4][NC];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int k = 0; k < NC; ++k)
+        kop[u][k] = bload16(kr, rowoff[u] >= 0 ? (rowoff[u] + 32 * k + 8 * G) * 2 : kMaskedOffset, 0);
+    uint32_t vmask[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      vmask[u] = (uint32_t)__builtin_amdgcn_ballot_w64(rowoff[u] >= 0) & 0xFFFFu;
+      if (G == 0) s_row[wv][16 * u + c16] = rowoff[u];
+    }
+
+    // S^T: lane (c16, G) holds head c16 at positions 16u + 4G + i
+    f32x4 acc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < NC; ++k)
+#pragma unroll
+        for (int part = 0; part < 3; ++part) acc[u] = A::mfma16(kop[u][k], qb[k][part], acc[u]);
+    }
+    float sc[4][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool valid = (vmask[u] >> (4 * G + i)) & 1u;
+        sc[u][i] = valid ? acc[u][i] * a.scale2 : -INFINITY;
+        tmax = fmaxf(tmax, sc[u][i]);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_new = fmaxf(m_run, tmax);
+    const bool any = m_new != -INFINITY;
+    const float alpha = any ? exp2f(m_run - m_new) : 1.f;
+    float psum = 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = any ? exp2f(sc[u][i] - m_new) : 0.f;
+        psum += p;
+        if (c16 < RP) s_p[wv][16 * u + 4 * G + i][c16] = p;
+      }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    if (G == 0 && c16 < RP) s_alpha[wv][c16] = alpha;
+    wave_lds_sync();
+
+    // P . V: lane group pgrp takes positions pgrp*PPG .. +PPG-1 of the tile
+#pragma unroll
+    for (int r = 0; r < RP; ++r) {
+      const float al = s_alpha[wv][r];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[r][j] *= al;
+    }
+#pragma unroll
+    for (int mm = 0; mm < PPG; ++mm) {
+      const int tp = pgrp * PPG + mm;
+      const int ro = s_row[wv][tp];
+      const u32x4 v = bload16(vr, ro >= 0 ? (ro + dd) * 2 : kMaskedOffset, 0);
+      const float vf[8] = {A::lo(v[0]), A::hi(v[0]), A::lo(v[1]), A::hi(v[1]),
+                           A::lo(v[2]), A::hi(v[2]), A::lo(v[3]), A::hi(v[3])};
+#pragma unroll
+      for (int r = 0; r < RP; ++r) {
+        const float pr = s_p[wv][tp][r];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[r][j] = fmaf(pr, vf[j], o[r][j]);
+      }
+    }
+    wave_lds_sync();
+  }
+
+  // sum the lane groups' outputs and the lane shares of the row sums
+#pragma unroll
+  for (int x = LPD; x < 64; x <<= 1)
+#pragma unroll
+    for (int r = 0; r < RP; ++r)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[r][j] += __shfl_xor(o[r][j], x);
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
+  if (lane < LPD) {
+#pragma unroll
+    for (int r = 0; r < RP; ++r)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s_o[wv][r][dd + j] = o[r][j];
+  }
+  if (G == 0 && c16 < RP) {
+    s_m[wv][c16] = m_run;
+    s_l[wv][c16] = l_run;
+  }
+  __syncthreads();
+
+  for (int e = threadIdx.x; e < RP * DH; e += 256) {
+    const int r = e / DH, d = e % DH;
+    if (r >= nh) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_m[w][r]);
+    float Ls = 0.f, Os = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float mw = s_m[w][r];
+      if (mw != -INFINITY) {
+        const float f = exp2f(mw - M);
+        Ls += f * s_l[w][r];
+        Os += f * s_o[w][r][d];
+      }
+    }
+    const int64_t n = n0 + r;
+    if (a.S == 1) {
+      a.out[n * DH + d] = Ls > 0.f ? Os / Ls : 0.f;
+    } else {
+      a.part_o[(n * a.S + s) * DH + d] = Os;
+      if (d == 0) {
+        a.part_ml[(n * a.S + s) * 2] = M;
+        a.part_ml[(n * a.S + s) * 2 + 1] = Ls;
+      }
+    }
+  }
+}
+
+// Splits of a row: out = sum_s 2^(M_s - M) O_s / sum_s 2^(M_s - M) L_s.
+__global__ __launch_bounds__(256) void paged_combine_kernel(const float *__restrict__ part_o,
+                                                            const float *__restrict__ part_ml,
+                                                            int S, int D, int64_t total,
+                                                            float *__restrict__ out) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= total) return;
+  const int64_t n = e / D;
+  const int d = (int)(e - n * D);
+  const float *ml = part_ml + n * S * 2;
+  float M = -INFINITY;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * s]);
+  float Ls = 0.f, Os = 0.f;
+  for (int s = 0; s < S; ++s) {
+    const float ms = ml[2 * s];
+    if (ms != -INFINITY) {
+      const float f = exp2f(ms - M);
+      Ls += f * ml[2 * s + 1];
+      Os += f * part_o[(n * S + s) * D + d];
+    }
+  }
+  out[e] = Ls > 0.f ? Os / Ls : 0.f;
+}
+
+template <int KVT>
+__device__ __forceinline__ float kv_at(const void *base, int64_t i) {
+  if constexpr (KVT == NVM_KV_F32) return ((const float *)base)[i];
+  if constexpr (KVT == NVM_KV_I8) return (float)((const int8_t *)base)[i];
+  if constexpr (KVT == NVM_KV_BF16) return Act<DT_BF16>::to_f32(((const uint16_t *)base)[i]);
+  return Act<DT_F16>::to_f32(((const uint16_t *)base)[i]);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int x = 32; x > 0; x >>= 1) v += __shfl_xor(v, x);
+  return v;  // the same in every lane: each step adds the same two operands
+}
+
+// One wavefront per query row (n, i): lanes hold dims lane + 64k; positions
+// in order, the score reduced across the wavefront, online softmax.
+template <int KVT>
+__global__ __launch_bounds__(256) void paged_rows_kernel(PagedArgs a, int64_t rows) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t n = row / a.L;
+  const int i = (int)(row - n * a.L);
+  const int b = (int)(n / a.Hq);
+  const int kvh = (int)(n % a.Hq) / a.R;
+  const int ctx_len = a.lens[b];
+  const int ctx = min(ctx_len, a.max_pages * a.page_size);
+  const int last = a.causal ? min(ctx, i + ctx_len - a.L + 1) : ctx;
+  constexpr int KD = kMaxRowDim / 64;
+  float qv[KD], ov[KD];
+#pragma unroll
+  for (int k = 0; k < KD; ++k) {
+    const int d = lane + 64 * k;
+    qv[k] = d < a.D ? a.q[row * a.D + d] : 0.f;
+    ov[k] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  for (int j = 0; j < last; ++j) {
+    const int pg = a.bt[(int64_t)b * a.max_pages + j / a.page_size];
+    if (pg < 0 || pg >= a.P) continue;
+    const int64_t slot = ((int64_t)pg * a.Hkv + kvh) * a.page_size + j % a.page_size;
+    const float ksc = KVT == NVM_KV_I8 ? a.ks[slot] : 1.f;
+    const float vsc = KVT == NVM_KV_I8 ? a.vs[slot] : 1.f;
+    float dot = 0.f;
+#pragma unroll
+    for (int k = 0; k < KD; ++k) {
+      const int d = lane + 64 * k;
+      if (d < a.D) {
+        const float kx = kv_at<KVT>(a.kp, slot * a.D + d);
+        dot += qv[k] * (KVT == NVM_KV_I8 ? kx * ksc : kx);
+      }
+    }
+    const float sc = wave_sum(dot) * a.scale2;
+    const float m_new = fmaxf(m, sc);
+    const float alpha = exp2f(m - m_new);
+    const float p = exp2f(sc - m_new);
+    l = l * alpha + p;
+#pragma unroll
+    for (int k = 0; k < KD; ++k) {
+      const int d = lane + 64 * k;
+      if (d < a.D) {
+        const float vx = kv_at<KVT>(a.vp, slot * a.D + d);
+        ov[k] = ov[k] * alpha + p * (KVT == NVM_KV_I8 ? vx * vsc : vx);
+      }
+    }
+    m = m_new;
+  }
+#pragma unroll
+  for (int k = 0; k < KD; ++k) {
+    const int d = lane + 64 * k;
+    if (d < a.D) a.out[row * a.D + d] = l > 0.f ? ov[k] / l : 0.f;
+  }
+}
+
+struct AttnPlan {
+  bool decode;  // the split-context decode kernel
+  int RP, HG, S, span;
+};
+
+AttnPlan attn_plan(int64_t N, int64_t L, int64_t D, int64_t max_pages, int64_t page_size,
+                   int kv_dtype, int Hkv, int Hq) {
+  AttnPlan p{false, 0, 1, 1, 0};
+  p.decode = L == 1 && (kv_dtype == NVM_KV_F16 || kv_dtype == NVM_KV_BF16) && (D == 64 || D == 128);
+  if (!p.decode) return p;
+  const int R = Hq / Hkv;
+  p.RP = R <= 8 ? 8 : 16;
+  p.HG = (R + p.RP - 1) / p.RP;
+  const int64_t tiles = (max_pages * page_size + kTile - 1) / kTile;
+  const int64_t base = N / Hq * Hkv * p.HG;
+  const int64_t s0 = std::max<int64_t>(1, (kTargetBlocks + base - 1) / base);
+  int64_t tps = std::max<int64_t>(1, (tiles + s0 - 1) / s0);
+  if (tps >= 4) tps = (tps + 3) / 4 * 4;  // whole rounds of the four wavefronts
+  p.S = (int)std::max<int64_t>(1, (tiles + tps - 1) / tps);
+  p.span = (int)(tps * kTile);
+  return p;
+}
+
+size_t attn_workspace(const AttnPlan &p, int64_t N, int64_t D) {
+  if (!p.decode || p.S == 1) return 0;
+  const size_t o = ((size_t)N * p.S * D * sizeof(float) + 255) & ~(size_t)255;
+  return o + (((size_t)N * p.S * 2 * sizeof(float) + 255) & ~(size_t)255);
+}
+
+template <int DT>
+void launch_decode(const PagedArgs &a, int RP, int D, unsigned grid, hipStream_t st) {
+  if (D == 128) {
+    if (RP == 8)
+      hipLaunchKernelGGL((paged_decode_kernel<DT, 128, 8>), dim3(grid), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((paged_decode_kernel<DT, 128, 16>), dim3(grid), dim3(256), 0, st, a);
+  } else {
+    if (RP == 8)
+      hipLaunchKernelGGL((paged_decode_kernel<DT, 64, 8>), dim3(grid), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((paged_decode_kernel<DT, 64, 16>), dim3(grid), dim3(256), 0, st, a);
+  }
+}
+
+#define ATTN_REQUIRE(cond, ...)                                              \
+  do {                                                                       \
+    if (!(cond)) return set_error(NVM_ERR_INVALID, __VA_ARGS__);             \
+  } while (0)
+#define ATTN_SUPPORTED(cond, ...)                                            \
+  do {                                                                       \
+    if (!(cond)) return set_error(NVM_ERR_UNSUPPORTED, __VA_ARGS__);         \
+  } while (0)
+
+int check_attention(int64_t N, int64_t L, int64_t D, int64_t max_pages, int64_t page_size,
+                    int kv_dtype, int num_kv_heads, int num_heads) {
+  ATTN_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
+               "paged_attention: num_heads must be divisible by num_kv_heads");
+  ATTN_REQUIRE(N >= 0 && N % num_heads == 0,
+               "paged_attention: q.shape[0] must be divisible by num_heads");
+  ATTN_REQUIRE(L >= 1 && D >= 1 && page_size >= 1 && max_pages >= 0,
+               "paged_attention: bad shape L=%lld D=%lld page_size=%lld max_pages=%lld",
+               (long long)L, (long long)D, (long long)page_size, (long long)max_pages);
+  ATTN_REQUIRE(kv_dtype >= NVM_KV_F16 && kv_dtype <= NVM_KV_I8, "paged_attention: bad kv dtype %d",
+               kv_dtype);
+  ATTN_SUPPORTED(D <= kMaxRowDim, "paged_attention: head dimension at most %d", kMaxRowDim);
+  ATTN_SUPPORTED(max_pages * page_size <= 0x7FFFFFFFll, "paged_attention: context capacity too large");
+  return NVM_OK;
+}
+
+}  // namespace
+
+}  // namespace nvm
+
+extern "C" {
+
+int nvm_paged_attention_workspace_size(int64_t N, int64_t L, int64_t D, int64_t max_pages,
+                                       int64_t page_size, int kv_dtype, int num_kv_heads,
+                                       int num_heads, size_t *bytes) {
+  using namespace nvm;
+  if (int r = check_attention(N, L, D, max_pages, page_size, kv_dtype, num_kv_heads, num_heads))
+    return r;
+  if (!bytes) return set_error(NVM_ERR_INVALID, "paged_attention: null bytes");
+  *bytes = attn_workspace(attn_plan(N, L, D, max_pages, page_size, kv_dtype, num_kv_heads,
+                                    num_heads),
+                          N, D);
+  return NVM_OK;
+}
+
+int nvm_paged_attention(const float *q, int64_t N, int64_t L, int64_t D, const void *key_pages,
+                        const void *value_pages, int64_t P, int64_t page_size, int kv_dtype,
+                        const float *key_scales, const float *value_scales,
+                        const int32_t *block_table, int64_t B, int64_t max_pages,
+                        const int32_t *context_lens, float scale, int is_causal,
+                        int num_kv_heads, int num_heads, float *out, void *workspace,
+                        size_t workspace_bytes, nvm_stream_t stream) {
+  using namespace nvm;
+  if (int r = check_attention(N, L, D, max_pages, page_size, kv_dtype, num_kv_heads, num_heads))
+    return r;
+  ATTN_REQUIRE(B >= 0 && N / num_heads == B,
+               "paged_attention: q batch size must match block_table batch size");
+  ATTN_REQUIRE(P >= 0 && P <= 0x7FFFFFFFll, "paged_attention: bad page count %lld", (long long)P);
+  const int elt = kv_dtype == NVM_KV_F32 ? 4 : kv_dtype == NVM_KV_I8 ? 1 : 2;
+  // (the kernels address pages through 32-bit buffer offsets, and a masked
+  // lane reads at kMaskedOffset, which must lie beyond every page tensor)
+  ATTN_SUPPORTED(P * num_kv_heads * page_size * D * elt <= 0x7FFF0000ll,
+                 "paged_attention: page tensors of %lld bytes; at most 2 GiB each",
+                 (long long)(P * num_kv_heads * page_size * D * elt));
+  if (N == 0) return NVM_OK;
+  ATTN_REQUIRE(q && out && block_table && context_lens, "paged_attention: null pointer");
+  ATTN_REQUIRE(P == 0 || (key_pages && value_pages), "paged_attention: null page pointer");
+  ATTN_REQUIRE(kv_dtype != NVM_KV_I8 || P == 0 || (key_scales && value_scales),
+               "paged_attention_int8: key_scales and value_scales are required");
+
+  const AttnPlan plan = attn_plan(N, L, D, max_pages, page_size, kv_dtype, num_kv_heads,
+                                  num_heads);
+  const size_t need = attn_workspace(plan, N, D);
+  if (need && (!workspace || workspace_bytes < need))
+    return set_error(NVM_ERR_WORKSPACE, "paged_attention: workspace of %zu bytes needed", need);
+
+  PagedArgs a{};
+  a.q = q;
+  a.kp = key_pages;
+  a.vp = value_pages;
+  a.ks = key_scales;
+  a.vs = value_scales;
+  a.bt = block_table;
+  a.lens = context_lens;
+  a.out = out;
+  a.P = (int)P;
+  a.L = (int)L;
+  a.D = (int)D;
+  a.page_size = (int)page_size;
+  a.max_pages = (int)max_pages;
+  a.Hkv = num_kv_heads;
+  a.Hq = num_heads;
+  a.R = num_heads / num_kv_heads;
+  a.HG = plan.HG;
+  a.S = plan.S;
+  a.span = plan.span;
+  a.causal = is_causal ? 1 : 0;
+  a.scale2 = scale * kLog2e;
+  hipStream_t st = (hipStream_t)stream;
+
+  if (plan.decode) {
+    if (plan.S > 1) {
+      a.part_o = (float *)workspace;
+      a.part_ml = (float *)((char *)workspace + (((size_t)N * plan.S * D * sizeof(float) + 255) &
+                                                 ~(size_t)255));
+    }
+    const unsigned grid = (unsigned)(B * num_kv_heads * plan.HG * plan.S);
+    if (grid == 0) return NVM_OK;
+    if (kv_dtype == NVM_KV_BF16)
+      launch_decode<DT_BF16>(a, plan.RP, (int)D, grid, st);
+    else
+      launch_decode<DT_F16>(a, plan.RP, (int)D, grid, st);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(NVM_ERR_HIP, "paged_attention: %s", hipGetErrorString(e));
+    if (plan.S > 1) {
+      const int64_t total = N * D;
+      hipLaunchKernelGGL(paged_combine_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
+                         0, st, a.part_o, a.part_ml, plan.S, (int)D, total, out);
+      e = hipGetLastError();
+      if (e != hipSuccess)
+        return set_error(NVM_ERR_HIP, "paged_attention combine: %s", hipGetErrorString(e));
+    }
+    return NVM_OK;
+  }
+
+  const int64_t rows = N * L;
+  const unsigned grid = (unsigned)((rows + 3) / 4);
+  switch (kv_dtype) {
+    case NVM_KV_F32:
+      hipLaunchKernelGGL((paged_rows_kernel<NVM_KV_F32>), dim3(grid), dim3(256), 0, st, a, rows);
+      break;
+    case NVM_KV_I8:
+      hipLaunchKernelGGL((paged_rows_kernel<NVM_KV_I8>), dim3(grid), dim3(256), 0, st, a, rows);
+      break;
+    case NVM_KV_BF16:
+      hipLaunchKernelGGL((paged_rows_kernel<NVM_KV_BF16>), dim3(grid), dim3(256), 0, st, a, rows);
+      break;
+    default:
+      hipLaunchKernelGGL((paged_rows_kernel<NVM_KV_F16>), dim3(grid), dim3(256), 0, st, a, rows);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(NVM_ERR_HIP, "paged_attention: %s", hipGetErrorString(e));
+  return NVM_OK;
+}
+
+}  // extern "C"

@@ -21,8 +21,8 @@
 //   the memory pipe never drains between units.
 //
 // Exact inner products on the matrix cores.  A 4-bit code q becomes the exact
-// 16-bit float M+q (M = 128 for bf16, 1024 for fp16) by OR-ing it into a
-// constant; v_mfma_f32_16x16x32 accumulates x.(M+q) over one 64-wide group,
+// 16-bit float M+q (M = 128 for bf16, code in mantissa bits 0-3; M = 64 for
+// fp16, bits 4-7) by OR-ing it into a constant; v_mfma_f32_16x16x32 accumulates x.(M+q) over one 64-wide group,
 // and the group is folded as
 //   sum_i x_i w_i = s * sum_i x_i (M + q_i) + (b - M s) * sum_i x_i,
 // the reference's w = q*s + b (metal/src/quantized_matmul.cpp:135) without

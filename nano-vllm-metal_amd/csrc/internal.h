@@ -7,6 +7,10 @@
 
 namespace nvm {
 
+// Records the message that nvm_last_error() returns on this thread; returns
+// `code` (a negative NVM_ERR_* status).
+int set_error(int code, const char *fmt, ...);
+
 // Arguments of the grouped expert products (decode GEMV and prefill GEMM).
 //   Sorted slot n (expert-major, see dispatch) reads activation row
 //   a_map ? a_map[n] / a_div : n  and writes output row  o_map ? o_map[n] : n.

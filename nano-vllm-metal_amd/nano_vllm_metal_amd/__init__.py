@@ -3,13 +3,15 @@
 Public names mirror the reference's package root for this path
 (``src/nano_vllm_metal/__init__.py:6,8``): ``QuantizedWeights``,
 ``quantized_matmul``, ``quantized_linear``, ``route_topk``,
-``grouped_expert_linear`` and ``Moe``.  All compute runs in HIP kernels on the
-GPU (libnvm_moe.so); nothing falls back to the CPU.
+``grouped_expert_linear`` and ``Moe``, plus ``paged_attention``
+(``layers/attention.py:154``).  All compute runs in HIP kernels on the GPU
+(libnvm_moe.so); nothing falls back to the CPU.
 """
 
 from .linear import QuantizedWeights, dequantize, quantize, quantized_linear, quantized_matmul
 from .moe import Moe, grouped_expert_linear, moe_dispatch, route_and_dispatch, route_topk
 from .loader import load_moe_block, load_moe_blocks, read_config, sparse_layers
+from .attention import paged_attention
 
 __all__ = [
     "QuantizedWeights",
@@ -26,4 +28,5 @@ __all__ = [
     "load_moe_blocks",
     "read_config",
     "sparse_layers",
+    "paged_attention",
 ]

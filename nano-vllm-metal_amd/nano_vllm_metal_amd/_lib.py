@@ -26,6 +26,8 @@ REGIME_AUTO, REGIME_DECODE, REGIME_PREFILL = 0, 1, 2
 ABI_VERSION = 2  # NVM_ABI_VERSION of include/nvm_moe.h
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
+# nvm_kv_dtype of include/nvm_attention.h
+KV_DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2, torch.int8: 3}
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -49,6 +51,10 @@ SIGNATURES = {
                               _P, _P, _P, _I, _P],
     "nvm_moe_expert_down": [_P, _I64, _I64, _I64, _I64, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P],
     "nvm_moe_combine": [_P, _P, _I64, _I, _I64, _I, _P, _P],
+    "nvm_paged_attention_workspace_size": [_I64, _I64, _I64, _I64, _I64, _I, _I, _I,
+                                           ctypes.POINTER(_SZ)],
+    "nvm_paged_attention": [_P, _I64, _I64, _I64, _P, _P, _I64, _I64, _I, _P, _P, _P, _I64, _I64,
+                            _P, ctypes.c_float, _I, _I, _I, _P, _P, _SZ, _P],
     "nvm_moe_forward": [_P, _I64, _I64, _I64, _I64, _I, _I, _I, _I, _I,
                         _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                         _P, _P, _P, _I, _P, _SZ, _P],

@@ -1,0 +1,80 @@
+"""Paged attention over a paged KV cache on the GPU (libnvm_moe.so).
+
+Mirrors ``paged_attention`` of the reference (``layers/attention.py:154-230``)
+and the ops it calls, ``metal.paged_attention`` and
+``metal.paged_attention_int8_decode`` (``metal/bindings.cpp:50-80``): the same
+arguments, masks and output (float32, ``[B, num_heads, L, D]``).  Tensors are
+torch tensors on one GPU; there is no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+
+def paged_attention(query: torch.Tensor, key_pages: torch.Tensor, value_pages: torch.Tensor,
+                    block_table: torch.Tensor, context_lens: torch.Tensor, page_size: int,
+                    key_scales: torch.Tensor | None = None,
+                    value_scales: torch.Tensor | None = None, scale: float | None = None,
+                    mask: str | None = None) -> torch.Tensor:
+    """``softmax(query . paged_key^T * scale) . paged_value``.
+
+    ``query [B, num_heads, L, D]``; ``key_pages``/``value_pages``
+    ``[P, num_kv_heads, page_size, D]`` (float32, float16, bfloat16, or int8
+    with ``key_scales``/``value_scales [P, num_kv_heads, page_size, 1]``);
+    ``block_table [B, max_pages]`` physical page ids (negative: no page);
+    ``context_lens [B]``.  ``mask`` is None or ``"causal"`` (query row i of L
+    sees key positions j <= i + context_len - L).  Returns float32
+    ``[B, num_heads, L, D]``.
+    """
+    if isinstance(mask, torch.Tensor):
+        raise NotImplementedError("Paged attention only supports mask=None or causal")
+    if mask is not None and mask != "causal":
+        raise NotImplementedError(f"unsupported mask {mask!r}")
+    lib = _lib.load()
+    B, Hq, L, D = query.shape
+    P, Hkv, ps, Dk = key_pages.shape
+    if ps != page_size:
+        raise ValueError(f"paged_attention: page tensors hold {ps} slots, page_size={page_size}")
+    if Dk != D:
+        raise ValueError("paged_attention: q and page tensors must have the same head dimension")
+    if key_pages.shape != value_pages.shape or key_pages.dtype != value_pages.dtype:
+        raise ValueError("paged_attention: key_pages and value_pages must match in shape and dtype")
+    if key_pages.dtype not in _lib.KV_DTYPE_CODES:
+        raise ValueError(f"paged_attention: unsupported page dtype {key_pages.dtype}")
+    if Hq % Hkv != 0:
+        raise ValueError("paged_attention: num_heads must be divisible by num_kv_heads")
+    if block_table.dim() != 2 or context_lens.dim() != 1 or block_table.shape[0] != B \
+            or context_lens.shape[0] != B:
+        raise ValueError("paged_attention: block_table [B, max_pages] and context_lens [B] "
+                         "must match the query batch")
+    dev = _lib.require_device(query, key_pages, value_pages, block_table, context_lens,
+                              key_scales, value_scales)
+    factor = scale if scale is not None else 1.0 / (D ** 0.5)
+    q = query.to(torch.float32).reshape(B * Hq, L, D).contiguous()
+    kp = key_pages.contiguous()
+    vp = value_pages.contiguous()
+    bt = block_table.to(torch.int32).contiguous()
+    lens = context_lens.to(torch.int32).contiguous()
+    ks = vs = None
+    if key_pages.dtype == torch.int8:
+        if key_scales is None or value_scales is None:
+            raise ValueError("paged_attention: int8 pages need key_scales and value_scales")
+        ks = key_scales.to(torch.float32).reshape(P, Hkv, ps).contiguous()
+        vs = value_scales.to(torch.float32).reshape(P, Hkv, ps).contiguous()
+    out = torch.empty((B * Hq, L, D), dtype=torch.float32, device=dev)
+    kv = _lib.KV_DTYPE_CODES[key_pages.dtype]
+    size = ctypes.c_size_t(0)
+    _lib.check(lib.nvm_paged_attention_workspace_size(B * Hq, L, D, bt.shape[1], page_size, kv,
+                                                      Hkv, Hq, ctypes.byref(size)))
+    ws = torch.empty(max(size.value, 1), dtype=torch.uint8, device=dev)
+    _lib.check(lib.nvm_paged_attention(
+        q.data_ptr(), B * Hq, L, D, kp.data_ptr(), vp.data_ptr(), P, page_size, kv,
+        _lib.ptr(ks), _lib.ptr(vs), bt.data_ptr(), B, bt.shape[1], lens.data_ptr(),
+        float(factor), int(mask == "causal"), Hkv, Hq, out.data_ptr(), ws.data_ptr(),
+        size.value, _lib.stream_of(dev)))
+    return out.reshape(B, Hq, L, D)

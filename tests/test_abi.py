@@ -1,6 +1,6 @@
 """The C ABI and the host-side mirror, without a GPU.
 
-* libnvm_moe.so loads and exports every function declared in include/nvm_moe.h;
+* libnvm_moe.so loads and exports every function declared in include/*.h;
 * argument validation returns the documented status codes and messages
   before any device work (so it can be exercised on a CPU-only host);
 * the Python mirror rejects CPU tensors and maps status codes to exceptions;
@@ -18,7 +18,7 @@ import pytest
 import torch
 
 ROOT = Path(__file__).resolve().parent.parent
-HEADER = ROOT / "include" / "nvm_moe.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 def _lib():
@@ -28,8 +28,10 @@ def _lib():
 
 
 def test_library_exports_every_header_function():
-    names = set(re.findall(r"^\s*(?:int|const char \*)\s*(nvm_\w+)\s*\(", HEADER.read_text(), re.M))
-    assert "nvm_moe_forward" in names and len(names) >= 12
+    names = set()
+    for h in HEADERS:
+        names |= set(re.findall(r"^\s*(?:int|const char \*)\s*(nvm_\w+)\s*\(", h.read_text(), re.M))
+    assert {"nvm_moe_forward", "nvm_paged_attention"} <= names and len(names) >= 14
     _, lib = _lib()
     for n in sorted(names):
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
@@ -181,3 +183,45 @@ def test_torch_quantizer_agrees_with_oracle(act, gs):
     # dequantisation of the torch layout equals the oracle's formula
     deq = dequantize(wq, s, b, gs).numpy().astype(np.float64)
     assert np.array_equal(deq, O.dequantize(wq.numpy().view(np.uint32), s_t, b_t, gs))
+
+
+def _attn(lib, **kw):
+    a = dict(q=1, N=64, L=1, D=128, kp=1, vp=1, P=8, ps=16, kv=1, ks=None, vs=None, bt=1, B=2,
+             mp=4, lens=1, scale=0.1, causal=0, hkv=4, hq=32, out=1, ws=1, ws_bytes=1 << 40)
+    a.update(kw)
+    return lib.nvm_paged_attention(a["q"], a["N"], a["L"], a["D"], a["kp"], a["vp"], a["P"],
+                                   a["ps"], a["kv"], a["ks"], a["vs"], a["bt"], a["B"], a["mp"],
+                                   a["lens"], a["scale"], a["causal"], a["hkv"], a["hq"],
+                                   a["out"], a["ws"], a["ws_bytes"], None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    ({"hq": 30}, -1, "divisible by num_kv_heads"),
+    ({"N": 65}, -1, "divisible by num_heads"),
+    ({"B": 3}, -1, "batch size"),
+    ({"kv": 5}, -1, "kv dtype"),
+    ({"D": 512}, -2, "head dimension"),
+    ({"kv": 3}, -1, "key_scales and value_scales"),
+    ({"q": None}, -1, "null pointer"),
+    ({"ws": None, "mp": 80}, -3, "workspace"),
+    ({"P": 1 << 20, "ps": 64}, -2, "2 GiB"),
+])
+def test_paged_attention_validation(kw, code, msg):
+    """Argument checks of nvm_paged_attention (the reference's paged_attention
+    op checks, metal/src/paged_attention.cpp:21-63) return before device work."""
+    _, lib = _lib()
+    assert _attn(lib, **kw) == code
+    assert msg in _err(lib)
+
+
+def test_paged_attention_workspace_size():
+    _, lib = _lib()
+    sz = ctypes.c_size_t()
+    # decode, 32 requests x 4 kv heads, 1280 positions: the context is split
+    assert lib.nvm_paged_attention_workspace_size(32 * 32, 1, 128, 80, 16, 1, 4, 32,
+                                                  ctypes.byref(sz)) == 0
+    assert sz.value >= 32 * 32 * 2 * 128 * 4
+    # one row kernel (multi-query): no workspace
+    assert lib.nvm_paged_attention_workspace_size(32 * 32, 4, 128, 80, 16, 1, 4, 32,
+                                                  ctypes.byref(sz)) == 0
+    assert sz.value == 0
