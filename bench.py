@@ -300,9 +300,9 @@ DENSE_SHAPES = (("q_proj", 2048, 4096), ("k_proj", 2048, 512), ("o_proj", 4096, 
                 ("lm_head", 2048, 151936))
 
 
-def dense_bench(dev, rows=(1, 32, 4096), reps=20, n=10):
-    """Kernel time of quantized_matmul per call (HIP-graph replay of `reps`
-    calls, `n` replays) for the 30B-A3B dense projection shapes."""
+def dense_bench(dev, rows=(1, 32, 4096)):
+    """Kernel time of quantized_matmul per call (HIP-graph replay, _graph_us)
+    for the 30B-A3B dense projection shapes."""
     import torch
     from nano_vllm_metal_amd import quantized_matmul
 
@@ -320,32 +320,68 @@ def dense_bench(dev, rows=(1, 32, 4096), reps=20, n=10):
             if name == "lm_head" and M > 32:
                 continue
             a = torch.randn(M, N, device=dev, generator=g).to(torch.bfloat16)
-            fn = lambda: quantized_matmul(sc, bi, gs, 4, a, w, True)  # noqa: E731
-            st = torch.cuda.Stream()
-            st.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(st):
-                for _ in range(3):
-                    fn()
-            torch.cuda.current_stream().wait_stream(st)
-            torch.cuda.synchronize()
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                for _ in range(reps):
-                    fn()
-            graph.replay()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(n):
-                graph.replay()
-            e1.record()
-            torch.cuda.synchronize()
-            us = e0.elapsed_time(e1) * 1e3 / (n * reps)
+            us = _graph_us(lambda: quantized_matmul(sc, bi, gs, 4, a, w, True))
             res[str(M)] = {"us": us, "weight_gbs": wbytes / us / 1e3,
                            "tflops": 2.0 * M * N * K / us / 1e6}
-            del graph
         out[name] = res
         del w, sc, bi
+    return out
+
+
+# Paged decode attention of the same model: 32 query heads over 4 kv heads of
+# dim 128, bf16 pages of 16 slots; (requests, context positions).
+ATTN_SHAPE = dict(Hq=32, Hkv=4, D=128, page=16)
+ATTN_CASES = ((32, 1280), (1, 4096), (64, 2048))
+
+
+def _graph_us(fn, reps=20, n=10):
+    """Kernel time per call: HIP-graph replay of `reps` calls, `n` replays."""
+    import torch
+
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (n * reps)
+
+
+def attention_bench(dev):
+    """Paged decode attention: kernel time per call and K/V bytes read per
+    second (each request's context read once per kv head)."""
+    import torch
+    from nano_vllm_metal_amd import paged_attention
+
+    Hq, Hkv, D, ps = (ATTN_SHAPE[n] for n in ("Hq", "Hkv", "D", "page"))
+    out = {}
+    for B, ctx in ATTN_CASES:
+        g = torch.Generator(device=dev).manual_seed(B * 7 + ctx)
+        mp = (ctx + ps - 1) // ps
+        P = B * mp
+        q = torch.randn(B, Hq, 1, D, device=dev, generator=g)
+        kp = torch.randn(P, Hkv, ps, D, device=dev, generator=g).to(torch.bfloat16)
+        vp = torch.randn(P, Hkv, ps, D, device=dev, generator=g).to(torch.bfloat16)
+        bt = torch.randperm(P, device=dev, generator=g).to(torch.int32).reshape(B, mp)
+        lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+        us = _graph_us(lambda: paged_attention(q, kp, vp, bt, lens, ps))
+        kv_bytes = 2 * B * ctx * Hkv * D * 2
+        out[f"B{B}_ctx{ctx}"] = {"us": us, "kv_bytes": kv_bytes, "gbs": kv_bytes / us / 1e3,
+                                 "frac_hbm": kv_bytes / us / 1e3 / HBM_PEAK_GBS}
+        del q, kp, vp, bt
     return out
 
 
@@ -508,6 +544,8 @@ def main():
                     help="measure only the 4096-token prefill with uniform routing")
     ap.add_argument("--dense-only", action="store_true",
                     help="measure only the dense W4A16 projections (quantized_matmul)")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="measure only paged decode attention")
     ap.add_argument("--rocprof-summary", metavar="DIR",
                     help="summarise rocprofv3 CSV output under DIR and exit (no GPU)")
     ap.add_argument("--write-traffic", action="store_true",
@@ -536,6 +574,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.attention_only:
+        log("[bench] paged decode attention")
+        print(json.dumps({"attention": attention_bench(dev)}), flush=True)
+        return
     if args.dense_only:
         log("[bench] dense W4A16 projections")
         print(json.dumps({"dense": dense_bench(dev)}), flush=True)
@@ -619,6 +661,8 @@ def main():
                 del lay
         log("[bench] dense W4A16 projections")
         out["dense"] = dense_bench(dev)
+        log("[bench] paged decode attention")
+        out["attention"] = attention_bench(dev)
         u = out["prefill"]["uniform"]
         out["prefill_roofline"] = {
             "kernel": "gemm_kernel<bf16, gate/up+SwiGLU> (nvm_moe_expert_gateup, prefill)",

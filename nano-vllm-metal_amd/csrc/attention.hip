@@ -46,6 +46,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kTile = 64;           // context positions per wavefront step
 constexpr int kTargetBlocks = 512;  // decode: split the context until about this many blocks
 constexpr int kMaxRowDim = 256;     // head dim of the row kernel (4 values per lane)
+constexpr int kMaxSplits = 64;      // context splits of a decode row
 
 struct PagedArgs {
   const float *q;
@@ -139,18 +140,28 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[r][j] = 0.f;
 
+  // page ids of positions t0 + 16u + c16, one tile ahead of their use
+  auto page_ids = [&](int t0, int (&pg)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int pos = t0 + 16 * u + c16;
+      pg[u] = pos < p1 ? a.bt[bt_row + pos / a.page_size] : -1;
+    }
+  };
+  int pg_next[4];
+  page_ids(p0 + kTile * wv, pg_next);
   for (int t0 = p0 + kTile * wv; t0 < p1; t0 += 4 * kTile) {
     // element offsets of the key/value rows of positions t0 + 16u + c16
     int rowoff[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int pos = t0 + 16 * u + c16;
-      int pg = -1;
-      if (pos < p1) pg = a.bt[bt_row + pos / a.page_size];
+      const int pg = pg_next[u];
       rowoff[u] = (pg >= 0 && pg < a.P)
                       ? ((pg * a.Hkv + kvh) * a.page_size + pos % a.page_size) * DH
                       : -1;
     }
+    page_ids(t0 + 4 * kTile, pg_next);
     u32x4 kop[4][NC];
 #pragma unroll
     for (int u = 0; u < 4; ++u)
@@ -162,6 +173,15 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
     for (int u = 0; u < 4; ++u) {
       vmask[u] = (uint32_t)__builtin_amdgcn_ballot_w64(rowoff[u] >= 0) & 0xFFFFu;
       if (G == 0) s_row[wv][16 * u + c16] = rowoff[u];
+    }
+    wave_lds_sync();
+    // the value rows of this lane's P.V positions, loaded with the keys (one
+    // memory round trip per tile)
+    u32x4 vv[PPG];
+#pragma unroll
+    for (int mm = 0; mm < PPG; ++mm) {
+      const int ro = s_row[wv][pgrp * PPG + mm];
+      vv[mm] = bload16(vr, ro >= 0 ? (ro + dd) * 2 : kMaskedOffset, 0);
     }
 
     // S^T: lane (c16, G) holds head c16 at positions 16u + 4G + i
@@ -213,8 +233,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
 #pragma unroll
     for (int mm = 0; mm < PPG; ++mm) {
       const int tp = pgrp * PPG + mm;
-      const int ro = s_row[wv][tp];
-      const u32x4 v = bload16(vr, ro >= 0 ? (ro + dd) * 2 : kMaskedOffset, 0);
+      const u32x4 v = vv[mm];
       const float vf[8] = {A::lo(v[0]), A::hi(v[0]), A::lo(v[1]), A::hi(v[1]),
                            A::lo(v[2]), A::hi(v[2]), A::lo(v[3]), A::hi(v[3])};
 #pragma unroll
@@ -278,27 +297,48 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
 }
 
 // Splits of a row: out = sum_s 2^(M_s - M) O_s / sum_s 2^(M_s - M) L_s.
+// One block per row: the splits' (M_s, L_s) are read in parallel into LDS,
+// then thread d sums its dim over the splits with the loads of eight splits
+// in flight at a time.
 __global__ __launch_bounds__(256) void paged_combine_kernel(const float *__restrict__ part_o,
                                                             const float *__restrict__ part_ml,
-                                                            int S, int D, int64_t total,
+                                                            int S, int D,
                                                             float *__restrict__ out) {
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (e >= total) return;
-  const int64_t n = e / D;
-  const int d = (int)(e - n * D);
+  __shared__ float s_w[kMaxSplits];
+  __shared__ float s_inv;
+  const int64_t n = blockIdx.x;
   const float *ml = part_ml + n * S * 2;
-  float M = -INFINITY;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * s]);
-  float Ls = 0.f, Os = 0.f;
-  for (int s = 0; s < S; ++s) {
-    const float ms = ml[2 * s];
-    if (ms != -INFINITY) {
-      const float f = exp2f(ms - M);
-      Ls += f * ml[2 * s + 1];
-      Os += f * part_o[(n * S + s) * D + d];
+  const int t = threadIdx.x;
+  if (t < 64) {
+    // wavefront 0: the row maximum and the weighted sum of the L_s
+    float M = -INFINITY;
+    for (int s = t; s < S; s += 64) M = fmaxf(M, ml[2 * s]);
+#pragma unroll
+    for (int x = 32; x > 0; x >>= 1) M = fmaxf(M, __shfl_xor(M, x));
+    float Ls = 0.f;
+    for (int s = t; s < S; s += 64) {
+      const float ms = ml[2 * s];
+      const float w = ms != -INFINITY ? exp2f(ms - M) : 0.f;
+      s_w[s] = w;
+      Ls += w * ml[2 * s + 1];
     }
+#pragma unroll
+    for (int x = 32; x > 0; x >>= 1) Ls += __shfl_xor(Ls, x);
+    if (t == 0) s_inv = Ls > 0.f ? 1.f / Ls : 0.f;
   }
-  out[e] = Ls > 0.f ? Os / Ls : 0.f;
+  __syncthreads();
+  for (int d = t; d < D; d += 256) {
+    const float *po = part_o + n * S * D + d;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int s = 0;
+    for (; s + 8 <= S; s += 8) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc[u] += s_w[s + u] * po[(int64_t)(s + u) * D];
+    }
+    for (; s < S; ++s) acc[0] += s_w[s] * po[(int64_t)s * D];
+    const float o = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+    out[n * D + d] = o * s_inv;
+  }
 }
 
 template <int KVT>
@@ -393,6 +433,7 @@ AttnPlan attn_plan(int64_t N, int64_t L, int64_t D, int64_t max_pages, int64_t p
   const int64_t s0 = std::max<int64_t>(1, (kTargetBlocks + base - 1) / base);
   int64_t tps = std::max<int64_t>(1, (tiles + s0 - 1) / s0);
   if (tps >= 4) tps = (tps + 3) / 4 * 4;  // whole rounds of the four wavefronts
+  tps = std::max<int64_t>(tps, (tiles + kMaxSplits - 1) / kMaxSplits);
   p.S = (int)std::max<int64_t>(1, (tiles + tps - 1) / tps);
   p.span = (int)(tps * kTile);
   return p;
@@ -533,9 +574,8 @@ int nvm_paged_attention(const float *q, int64_t N, int64_t L, int64_t D, const v
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(NVM_ERR_HIP, "paged_attention: %s", hipGetErrorString(e));
     if (plan.S > 1) {
-      const int64_t total = N * D;
-      hipLaunchKernelGGL(paged_combine_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
-                         0, st, a.part_o, a.part_ml, plan.S, (int)D, total, out);
+      hipLaunchKernelGGL(paged_combine_kernel, dim3((unsigned)N), dim3(256), 0, st, a.part_o,
+                         a.part_ml, plan.S, (int)D, out);
       e = hipGetLastError();
       if (e != hipSuccess)
         return set_error(NVM_ERR_HIP, "paged_attention combine: %s", hipGetErrorString(e));
