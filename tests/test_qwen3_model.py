@@ -1,0 +1,217 @@
+"""The Qwen3 model port, its paged KV cache and LLM.generate.
+
+CPU: cache bookkeeping, config parsing, sampling filters.  GPU: a two-layer
+model (one dense-MLP layer, one MoE layer) against a plain-torch float32
+reference forward (tests/qwen3_reference.py) for the three attention paths
+(initial prefill, one-token decode, prefill after a prefix), the
+reference's incremental-decode comparison (tests/test_paged_attention.py:
+191-213: log-softmax of the paged model vs the dense one, position by
+position), batching, and LLM.generate.
+
+Bound: log-probabilities within atol 5e-2 of the reference.  The model and
+the reference round the same bf16 tensors but accumulate differently (the
+exact router-size products, the GEMV, the GEMM's bf16-rounded weights), so a
+bf16 activation can differ by an ulp (2^-8 relative) and that difference
+travels through two layers.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+DEV = "cuda:0"
+ATOL = 5e-2
+
+
+def _cfg(**kw):
+    from nano_vllm_metal_amd import Qwen3Config
+
+    d = dict(hidden_size=256, num_hidden_layers=2, num_attention_heads=4,
+             num_key_value_heads=2, head_dim=64, vocab_size=1024, intermediate_size=640,
+             moe_intermediate_size=128, num_experts=8, num_experts_per_tok=2,
+             norm_topk_prob=True, mlp_only_layers=[0], rms_norm_eps=1e-6,
+             rope_theta=10000.0, max_position_embeddings=512)
+    d.update(kw)
+    return Qwen3Config.from_dict(d)
+
+
+# ---------------------------------------------------------------- CPU
+
+
+def test_config_and_sparse_layers():
+    c = _cfg(num_hidden_layers=6, decoder_sparse_step=2, mlp_only_layers=[3])
+    assert [i for i in range(6) if c.is_sparse(i)] == [1, 5]
+    assert _cfg(head_dim=None).head_dim == 64
+    assert not _cfg(num_experts=0).is_sparse(1)
+
+
+def test_kv_cache_bookkeeping():
+    from nano_vllm_metal_amd import PagedKVCache
+
+    c = PagedKVCache(2, 2, 8, num_pages=6, page_size=4, dtype=torch.float32, device="cpu")
+    c.add(7)
+    c.add(9)
+    c.reserve(7, 5)                      # 2 pages
+    pages, slots = c.slot_mapping([7], 5)
+    assert slots.tolist() == [0, 1, 2, 3, 0]
+    assert pages.tolist() == [c.pages[7][0]] * 4 + [c.pages[7][1]]
+    k = torch.arange(5 * 2 * 8, dtype=torch.float32).reshape(1, 5, 2, 8)
+    c.write(1, k, -k, pages, slots)
+    c.advance([7], 5)
+    assert torch.equal(c.key_pages[1][c.pages[7][1], :, 0], k[0, 4])
+    assert torch.equal(c.value_pages[1][c.pages[7][0], :, 3], -k[0, 3])
+    c.reserve(9, 1)
+    bt, lens = c.block_table([7, 9], extra=1)
+    assert bt.shape == (2, 2) and bt[1, 1].item() == -1 and lens.tolist() == [6, 1]
+    assert c.free_pages == 3
+    c.free(7)
+    assert c.free_pages == 5 and 7 not in c.pages
+    with pytest.raises(RuntimeError, match="out of pages"):
+        c.reserve(9, 100)
+
+
+def test_sampling_filters():
+    from nano_vllm_metal_amd.llm import SamplingParams, sample
+
+    logits = torch.tensor([[0.0, 3.0, 1.0, 2.9], [5.0, 0.0, 0.0, 0.0]])
+    assert sample(logits, SamplingParams()).tolist() == [1, 0]
+    g = torch.Generator().manual_seed(0)
+    picks = {int(sample(logits[:1], SamplingParams(temperature=1.0, top_k=2), g)[0])
+             for _ in range(200)}
+    assert picks == {1, 3}
+    picks = {int(sample(logits[:1], SamplingParams(temperature=1.0, top_p=0.3), g)[0])
+             for _ in range(100)}
+    assert picks == {1}
+
+
+# ---------------------------------------------------------------- GPU
+
+
+def _model(seed=0, **kw):
+    from nano_vllm_metal_amd import Moe, QuantizedWeights, Qwen3Model, quantize
+    from nano_vllm_metal_amd.qwen3 import DenseMLP, Qwen3Layer
+
+    c = _cfg(**kw)
+    g = torch.Generator(device=DEV).manual_seed(seed)
+
+    def qw(*shape, std=0.05):
+        w = (torch.randn(shape, generator=g, device=DEV) * std).to(torch.bfloat16)
+        wq, s, b = quantize(w, 64, 4)
+        return QuantizedWeights(s, b, 64, 4, wq)
+
+    def norm(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=g, device=DEV)).to(torch.bfloat16)
+
+    H, D = c.hidden_size, c.head_dim
+    layers = []
+    for i in range(c.num_hidden_layers):
+        if c.is_sparse(i):
+            E, I = c.num_experts, c.moe_intermediate_size
+            mlp = Moe(qw(E, H, std=0.2), qw(E, I, H), qw(E, I, H), qw(E, H, I),
+                      c.num_experts_per_tok, c.norm_topk_prob)
+        else:
+            mlp = DenseMLP(qw(c.intermediate_size, H), qw(c.intermediate_size, H),
+                           qw(H, c.intermediate_size))
+        layers.append(Qwen3Layer(qw(c.num_attention_heads * D, H), qw(c.num_key_value_heads * D, H),
+                                 qw(c.num_key_value_heads * D, H), qw(H, c.num_attention_heads * D),
+                                 norm(D), norm(D), norm(H), norm(H), mlp))
+    return Qwen3Model(c, qw(c.vocab_size, H, std=1.0), layers, norm(H), qw(c.vocab_size, H))
+
+
+def _close(a, b, what):
+    la = torch.log_softmax(a.float(), -1)
+    lb = torch.log_softmax(b.float(), -1)
+    err = (la - lb).abs().max().item()
+    assert err <= ATOL, f"{what}: max |log p - log p_ref| = {err:.3g}"
+
+
+def _tokens(n, seed=1, vocab=1024):
+    return np.random.default_rng(seed).integers(0, vocab, n).tolist()
+
+
+@pytest.mark.gpu
+def test_prefill_matches_reference():
+    from qwen3_reference import reference_logits
+
+    m = _model()
+    toks = _tokens(12)
+    cache = m.create_kv_cache(16, page_size=4)
+    cache.add(0)
+    got = m.forward(torch.tensor([toks], device=DEV), cache, [0], last_only=False)[0]
+    _close(got, reference_logits(m, toks), "initial prefill")
+    assert cache.lens[0] == 12
+
+
+@pytest.mark.gpu
+def test_incremental_decode_matches_reference():
+    """tests/test_paged_attention.py:191-213: one token at a time through the
+    paged cache (decode attention kernel) against the dense reference."""
+    from qwen3_reference import reference_logits
+
+    m = _model(1)
+    toks = _tokens(10, seed=2)
+    ref = reference_logits(m, toks)
+    cache = m.create_kv_cache(16, page_size=4)
+    cache.add(3)
+    for i, t in enumerate(toks):
+        got = m.forward(torch.tensor([[t]], device=DEV), cache, [3])[0]
+        _close(got, ref[i], f"decode position {i}")
+
+
+@pytest.mark.gpu
+def test_prefill_after_prefix_matches_reference():
+    """A second prompt chunk attends to the cached prefix (paged attention,
+    several causal query rows)."""
+    from qwen3_reference import reference_logits
+
+    m = _model(2)
+    toks = _tokens(13, seed=3)
+    ref = reference_logits(m, toks)
+    cache = m.create_kv_cache(16, page_size=4)
+    cache.add(0)
+    m.forward(torch.tensor([toks[:5]], device=DEV), cache, [0])
+    got = m.forward(torch.tensor([toks[5:]], device=DEV), cache, [0], last_only=False)[0]
+    _close(got, ref[5:], "chunked prefill")
+
+
+@pytest.mark.gpu
+def test_batched_decode_matches_single_requests():
+    from qwen3_reference import reference_logits
+
+    m = _model(3)
+    prompts = [_tokens(n, seed=10 + n) for n in (3, 9, 6)]
+    cache = m.create_kv_cache(32, page_size=4)
+    for i, p in enumerate(prompts):
+        cache.add(i)
+        m.forward(torch.tensor([p[:-1]], device=DEV), cache, [i])
+    last = torch.tensor([[p[-1]] for p in prompts], device=DEV)
+    got = m.forward(last, cache, [0, 1, 2])
+    for i, p in enumerate(prompts):
+        _close(got[i], reference_logits(m, p)[-1], f"batched row {i}")
+
+
+@pytest.mark.gpu
+def test_generate_greedy_is_the_model_argmax_chain():
+    from nano_vllm_metal_amd import LLM, SamplingParams
+
+    m = _model(4)
+    prompts = [_tokens(n, seed=20 + n) for n in (5, 11, 8)]
+    llm = LLM(m, max_num_seqs=2, max_model_len=64, page_size=4)
+    outs = llm.generate(prompts, SamplingParams(max_tokens=6))
+    assert [len(o.token_ids) for o in outs] == [6, 6, 6]
+    assert llm.cache.free_pages == llm.cache.num_pages
+    for p, o in zip(prompts, outs):
+        cache = m.create_kv_cache(16, page_size=4)
+        cache.add(0)
+        seq = list(p)
+        logits = m.forward(torch.tensor([seq], device=DEV), cache, [0])
+        chain = []
+        for _ in range(6):
+            t = int(torch.argmax(logits[0]))
+            chain.append(t)
+            logits = m.forward(torch.tensor([[t]], device=DEV), cache, [0])
+        assert o.token_ids == chain
+    st = llm.stats
+    assert st.prefill_tokens == 24 and st.decode_tokens == 15
