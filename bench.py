@@ -385,6 +385,42 @@ def attention_bench(dev):
     return out
 
 
+def e2e_bench(dev, n_seqs=32, prompt_len=1024, gen=256, layers=48):
+    """Full Qwen3-30B-A3B-shaped model (random int4 weights) through
+    LLM.generate with the paged KV cache: n_seqs concurrent requests of
+    prompt_len random tokens, gen greedy tokens each (no early stop)."""
+    import numpy as np
+    import torch
+    from nano_vllm_metal_amd import LLM, Qwen3Model, SamplingParams, qwen3_30b_a3b_config
+
+    cfg = qwen3_30b_a3b_config(layers)
+    log(f"[bench] e2e: building a {layers}-layer 30B-A3B-shaped model (random int4 weights)")
+    model = Qwen3Model.random(cfg, device=dev, seed=7)
+    llm = LLM(model, max_num_seqs=n_seqs, max_model_len=prompt_len + gen + 16, page_size=16,
+              prefill_step=prompt_len)
+    rng = np.random.default_rng(3)
+    prompts = [rng.integers(0, cfg.vocab_size, prompt_len).tolist() for _ in range(n_seqs)]
+    llm.generate([p[:32] for p in prompts[:4]], SamplingParams(max_tokens=4))  # warm-up
+    from nano_vllm_metal_amd.llm import GenerateStats
+
+    llm.stats = GenerateStats()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    outs = llm.generate(prompts, SamplingParams(max_tokens=gen, ignore_eos=True))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    st = llm.stats
+    assert all(len(o.token_ids) == gen for o in outs)
+    res = {"layers": layers, "seqs": n_seqs, "prompt_len": prompt_len, "gen_tokens": gen,
+           "decode_tokens_per_s": st.decode_tokens / st.decode_s,
+           "decode_step_ms": st.decode_s / st.decode_steps * 1e3,
+           "prefill_tokens_per_s": st.prefill_tokens / st.prefill_s,
+           "wall_s": wall, "generated_tokens_per_s": n_seqs * gen / wall}
+    del llm, model
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(layer, T, seconds, dev):
     """The C restatement of the reference path (oracle/moe_ref.c) on host cores."""
     import numpy as np
@@ -546,6 +582,9 @@ def main():
                     help="measure only the dense W4A16 projections (quantized_matmul)")
     ap.add_argument("--attention-only", action="store_true",
                     help="measure only paged decode attention")
+    ap.add_argument("--e2e", action="store_true",
+                    help="measure only the full 48-layer model through LLM.generate "
+                         "(32 x 1024-token prompts, 256 greedy tokens)")
     ap.add_argument("--rocprof-summary", metavar="DIR",
                     help="summarise rocprofv3 CSV output under DIR and exit (no GPU)")
     ap.add_argument("--write-traffic", action="store_true",
@@ -574,6 +613,12 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.e2e:
+        r = e2e_bench(dev)
+        log(f"[bench] e2e: decode {r['decode_tokens_per_s']:.0f} tok/s "
+            f"({r['decode_step_ms']:.2f} ms/step), prefill {r['prefill_tokens_per_s']:.0f} tok/s")
+        print(json.dumps({"e2e": r}), flush=True)
+        return
     if args.attention_only:
         log("[bench] paged decode attention")
         print(json.dumps({"attention": attention_bench(dev)}), flush=True)

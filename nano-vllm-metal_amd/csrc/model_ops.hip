@@ -1,0 +1,253 @@
+// Fused element-wise steps of the Qwen3 layer (declared in include/nvm_model.h).
+//
+// residual_rms_norm_kernel: one 256-thread block per row; each thread keeps
+//   its pairs of the row in registers between the sum of squares and the
+//   scaling, so the row is read once and written once or twice.
+// qk_norm_rope_store_kernel: one wavefront per (token, head) of the fused
+//   q/k/v projection output; lane l holds elements 2l and 2l+1 of the head.
+//   q and k heads: RMSNorm over the head (wavefront sum), RoPE with the
+//   partner half one lane swap away (elements i and i + D/2 sit D/4 lanes
+//   apart), rounded like the reference at each step.  k and v heads go to
+//   their page slot; q to the float32 attention input.
+#include <math.h>
+
+#include "common.h"
+#include "internal.h"
+#include "nvm_model.h"
+
+namespace nvm {
+
+namespace {
+
+constexpr int kNormThreads = 256;
+constexpr int kMaxNormPairs = 16;  // H <= 2 * 256 * 16 = 8192
+
+template <int DT>
+__device__ __forceinline__ uint32_t round_pair(float a, float b) {
+  return Act<DT>::pack2(a, b);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kNormThreads) void residual_rms_norm_kernel(
+    const uint32_t *__restrict__ h, const uint32_t *__restrict__ r,
+    const uint32_t *__restrict__ w, int H2, float eps, uint32_t *__restrict__ h_out,
+    uint32_t *__restrict__ x_out) {
+  using A = Act<DT>;
+  __shared__ float s_part[kNormThreads / 64];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const uint32_t *hr = h + row * H2;
+  float v[kMaxNormPairs][2];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMaxNormPairs; ++k) {
+    const int i = tid + k * kNormThreads;
+    if (i < H2) {
+      float a = A::lo(hr[i]), b = A::hi(hr[i]);
+      if (r) {
+        const uint32_t rv = r[row * H2 + i];
+        const uint32_t sum = round_pair<DT>(a + A::lo(rv), b + A::hi(rv));
+        h_out[row * H2 + i] = sum;
+        a = A::lo(sum);
+        b = A::hi(sum);
+      }
+      v[k][0] = a;
+      v[k][1] = b;
+      ss = fmaf(a, a, fmaf(b, b, ss));
+    }
+  }
+#pragma unroll
+  for (int x = 32; x > 0; x >>= 1) ss += __shfl_xor(ss, x);
+  if ((tid & 63) == 0) s_part[tid >> 6] = ss;
+  __syncthreads();
+  const float tot = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+  const float inv = rsqrtf(tot / (float)(2 * H2) + eps);
+#pragma unroll
+  for (int k = 0; k < kMaxNormPairs; ++k) {
+    const int i = tid + k * kNormThreads;
+    if (i < H2) {
+      const uint32_t wv = w[i];
+      x_out[row * H2 + i] =
+          round_pair<DT>(v[k][0] * inv * A::lo(wv), v[k][1] * inv * A::hi(wv));
+    }
+  }
+}
+
+struct QkvArgs {
+  const uint32_t *qkv;
+  const uint32_t *qw, *kw;
+  const int32_t *pos, *pages, *slots;
+  const float *cos, *sin;
+  uint32_t *kp, *vp;
+  float *q_out, *k_out, *v_out;
+  int64_t T;
+  int Hq, Hkv, D, max_pos, P, page_size;
+  float eps;
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(QkvArgs a) {
+  using A = Act<DT>;
+  const int NH = a.Hq + 2 * a.Hkv;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= a.T * NH) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t t = item / NH;
+  const int head = (int)(item - t * NH);
+  const int D2 = a.D / 2, half = a.D / 2, Q = a.D / 4;  // pairs per head, half dims, lane offset
+  const bool on = lane < D2;
+  const uint32_t xv = on ? a.qkv[(t * NH + head) * D2 + lane] : 0u;
+  float x0 = A::lo(xv), x1 = A::hi(xv);
+  const bool is_q = head < a.Hq, is_v = head >= a.Hq + a.Hkv;
+  const int kvh = is_q ? 0 : (is_v ? head - a.Hq - a.Hkv : head - a.Hq);
+
+  if (!is_v) {
+    // RMSNorm over the head, rounded (the reference's q_norm / k_norm output)
+    float ss = fmaf(x0, x0, x1 * x1);
+#pragma unroll
+    for (int x = 32; x > 0; x >>= 1) ss += __shfl_xor(ss, x);
+    const float inv = rsqrtf(ss / (float)a.D + a.eps);
+    const uint32_t wv = on ? (is_q ? a.qw : a.kw)[lane] : 0u;
+    const uint32_t y = Act<DT>::pack2(x0 * inv * A::lo(wv), x1 * inv * A::hi(wv));
+    x0 = A::lo(y);
+    x1 = A::hi(y);
+    // RoPE: element e < D/2 pairs with e + D/2, held Q lanes further on
+    const bool lo_half = lane < Q;
+    const int partner = lo_half ? lane + Q : lane - Q;
+    const float p0 = __shfl(x0, partner), p1 = __shfl(x1, partner);
+    const int e = 2 * (lo_half ? lane : lane - Q);  // frequency index of element 2*lane
+    int p = a.pos[t];
+    p = min(max(p, 0), a.max_pos - 1);
+    const float c0 = on ? a.cos[(int64_t)p * half + e] : 0.f;
+    const float c1 = on ? a.cos[(int64_t)p * half + e + 1] : 0.f;
+    const float s0 = on ? a.sin[(int64_t)p * half + e] : 0.f;
+    const float s1 = on ? a.sin[(int64_t)p * half + e + 1] : 0.f;
+    float r0, r1;
+    {
+      // products rounded before the sum, as the reference's separate ops do
+#pragma clang fp contract(off)
+      if (lo_half) {
+        r0 = x0 * c0 - p0 * s0;
+        r1 = x1 * c1 - p1 * s1;
+      } else {
+        r0 = p0 * s0 + x0 * c0;
+        r1 = p1 * s1 + x1 * c1;
+      }
+    }
+    const uint32_t ro = Act<DT>::pack2(r0, r1);
+    x0 = A::lo(ro);
+    x1 = A::hi(ro);
+    if (is_q) {
+      if (on) {
+        float *qo = a.q_out + (t * a.Hq + head) * a.D + 2 * lane;
+        qo[0] = x0;
+        qo[1] = x1;
+      }
+      return;
+    }
+  }
+  // k (normed, rotated, rounded) or v (as projected): page slot and float copy
+  if (!on) return;
+  const int pg = a.pages[t];
+  const int slot = a.slots[t];
+  if (pg >= 0 && pg < a.P && slot >= 0 && slot < a.page_size) {
+    const int64_t off = (((int64_t)pg * a.Hkv + kvh) * a.page_size + slot) * D2 + lane;
+    (is_v ? a.vp : a.kp)[off] = Act<DT>::pack2(x0, x1);
+  }
+  float *fo = is_v ? a.v_out : a.k_out;
+  if (fo) {
+    float *o = fo + (t * a.Hkv + kvh) * a.D + 2 * lane;
+    o[0] = x0;
+    o[1] = x1;
+  }
+}
+
+}  // namespace
+
+}  // namespace nvm
+
+extern "C" {
+
+int nvm_residual_rms_norm(const void *h, const void *r, const void *w, int64_t T, int64_t H,
+                          float eps, int dtype, void *h_out, void *x_out, nvm_stream_t stream) {
+  using namespace nvm;
+  if (dtype != NVM_DTYPE_F16 && dtype != NVM_DTYPE_BF16)
+    return set_error(NVM_ERR_INVALID, "residual_rms_norm: dtype must be f16 or bf16");
+  if (T < 0 || H <= 0 || H % 2)
+    return set_error(NVM_ERR_INVALID, "residual_rms_norm: bad shape T=%lld H=%lld", (long long)T,
+                     (long long)H);
+  if (H > 2 * kNormThreads * kMaxNormPairs)
+    return set_error(NVM_ERR_UNSUPPORTED, "residual_rms_norm: H at most %d",
+                     2 * kNormThreads * kMaxNormPairs);
+  if (T == 0) return NVM_OK;
+  if (!h || !w || !x_out || (r && !h_out))
+    return set_error(NVM_ERR_INVALID, "residual_rms_norm: null pointer");
+  const int H2 = (int)(H / 2);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == NVM_DTYPE_BF16)
+    hipLaunchKernelGGL(residual_rms_norm_kernel<DT_BF16>, dim3((unsigned)T), dim3(kNormThreads), 0,
+                       st, (const uint32_t *)h, (const uint32_t *)r, (const uint32_t *)w, H2, eps,
+                       (uint32_t *)h_out, (uint32_t *)x_out);
+  else
+    hipLaunchKernelGGL(residual_rms_norm_kernel<DT_F16>, dim3((unsigned)T), dim3(kNormThreads), 0,
+                       st, (const uint32_t *)h, (const uint32_t *)r, (const uint32_t *)w, H2, eps,
+                       (uint32_t *)h_out, (uint32_t *)x_out);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(NVM_ERR_HIP, "residual_rms_norm: %s", hipGetErrorString(e));
+  return NVM_OK;
+}
+
+int nvm_qk_norm_rope_store(const void *qkv, int64_t T, int Hq, int Hkv, int64_t D,
+                           const void *q_norm_w, const void *k_norm_w, float eps,
+                           const int32_t *positions, const float *cos, const float *sin,
+                           int64_t max_pos, const int32_t *page_ids, const int32_t *slots,
+                           void *key_pages, void *value_pages, int64_t P, int64_t page_size,
+                           int dtype, float *q_out, float *k_out, float *v_out,
+                           nvm_stream_t stream) {
+  using namespace nvm;
+  if (dtype != NVM_DTYPE_F16 && dtype != NVM_DTYPE_BF16)
+    return set_error(NVM_ERR_INVALID, "qk_norm_rope_store: dtype must be f16 or bf16");
+  if (T < 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_pos <= 0 || P < 0 || page_size <= 0)
+    return set_error(NVM_ERR_INVALID, "qk_norm_rope_store: bad shape");
+  if (D % 4 || D > 128)
+    return set_error(NVM_ERR_UNSUPPORTED, "qk_norm_rope_store: head dim %lld must be a multiple "
+                     "of 4, at most 128", (long long)D);
+  if (T == 0) return NVM_OK;
+  if (!qkv || !q_norm_w || !k_norm_w || !positions || !cos || !sin || !page_ids || !slots ||
+      !q_out || (P > 0 && (!key_pages || !value_pages)))
+    return set_error(NVM_ERR_INVALID, "qk_norm_rope_store: null pointer");
+  QkvArgs a{};
+  a.qkv = (const uint32_t *)qkv;
+  a.qw = (const uint32_t *)q_norm_w;
+  a.kw = (const uint32_t *)k_norm_w;
+  a.pos = positions;
+  a.pages = page_ids;
+  a.slots = slots;
+  a.cos = cos;
+  a.sin = sin;
+  a.kp = (uint32_t *)key_pages;
+  a.vp = (uint32_t *)value_pages;
+  a.q_out = q_out;
+  a.k_out = k_out;
+  a.v_out = v_out;
+  a.T = T;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.D = (int)D;
+  a.max_pos = (int)max_pos;
+  a.P = (int)P;
+  a.page_size = (int)page_size;
+  a.eps = eps;
+  const int64_t items = T * (Hq + 2 * Hkv);
+  const unsigned grid = (unsigned)((items + 3) / 4);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == NVM_DTYPE_BF16)
+    hipLaunchKernelGGL(qk_norm_rope_store_kernel<DT_BF16>, dim3(grid), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(qk_norm_rope_store_kernel<DT_F16>, dim3(grid), dim3(256), 0, st, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(NVM_ERR_HIP, "qk_norm_rope_store: %s", hipGetErrorString(e));
+  return NVM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,65 @@
+"""Fused element-wise steps of the Qwen3 layer on the GPU (include/nvm_model.h).
+
+``residual_rms_norm`` is the residual add plus ``RMSNorm`` of the reference's
+block (``models/qwen3.py:244-252``, ``layers/layernorm.py``);
+``qk_norm_rope_store`` is the attention block between the projections and the
+attention (``models/qwen3.py:103-133``): per-head RMSNorm of q and k, RoPE,
+and the k/v store into the layer's page pool.  No CPU fallback.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+
+def residual_rms_norm(h: torch.Tensor, r: Optional[torch.Tensor], weight: torch.Tensor,
+                      eps: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``(h + r, rms_norm(h + r) * weight)``; with ``r`` None, ``(h, rms_norm(h) * weight)``."""
+    lib = _lib.load()
+    dev = _lib.require_device(h, r, weight)
+    H = h.shape[-1]
+    h2 = h.reshape(-1, H).contiguous()
+    r2 = None if r is None else r.reshape(-1, H).contiguous()
+    w = weight.to(h.dtype).contiguous()
+    x = torch.empty_like(h2)
+    h_out = torch.empty_like(h2) if r is not None else None
+    _lib.check(lib.nvm_residual_rms_norm(h2.data_ptr(), _lib.ptr(r2), w.data_ptr(), h2.shape[0],
+                                         H, float(eps), _lib.dtype_code(h.dtype), _lib.ptr(h_out),
+                                         x.data_ptr(), _lib.stream_of(dev)))
+    out_h = h if h_out is None else h_out.reshape(h.shape)
+    return out_h, x.reshape(h.shape)
+
+
+def qk_norm_rope_store(qkv: torch.Tensor, num_heads: int, num_kv_heads: int, head_dim: int,
+                       q_norm: torch.Tensor, k_norm: torch.Tensor, eps: float,
+                       positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                       page_ids: torch.Tensor, slots: torch.Tensor, key_pages: torch.Tensor,
+                       value_pages: torch.Tensor, want_kv: bool = False):
+    """``qkv [..., (Hq + 2 Hkv) * D]`` -> float32 ``q [T, Hq, D]`` (and, with
+    ``want_kv``, float32 ``k, v [T, Hkv, D]``); k and v are stored at
+    ``key_pages/value_pages[page_ids[t], :, slots[t]]``."""
+    lib = _lib.load()
+    dev = _lib.require_device(qkv, q_norm, k_norm, positions, cos, sin, page_ids, slots,
+                              key_pages, value_pages)
+    D = head_dim
+    x = qkv.reshape(-1, (num_heads + 2 * num_kv_heads) * D).contiguous()
+    T = x.shape[0]
+    if key_pages.dtype != qkv.dtype or value_pages.dtype != qkv.dtype:
+        raise ValueError("qk_norm_rope_store: pages must have the activation dtype")
+    q = torch.empty((T, num_heads, D), dtype=torch.float32, device=dev)
+    k = torch.empty((T, num_kv_heads, D), dtype=torch.float32, device=dev) if want_kv else None
+    v = torch.empty((T, num_kv_heads, D), dtype=torch.float32, device=dev) if want_kv else None
+    _lib.check(lib.nvm_qk_norm_rope_store(
+        x.data_ptr(), T, num_heads, num_kv_heads, D, q_norm.to(qkv.dtype).contiguous().data_ptr(),
+        k_norm.to(qkv.dtype).contiguous().data_ptr(), float(eps),
+        positions.to(torch.int32).reshape(-1).contiguous().data_ptr(),
+        cos.contiguous().data_ptr(), sin.contiguous().data_ptr(), cos.shape[0],
+        page_ids.to(torch.int32).reshape(-1).contiguous().data_ptr(),
+        slots.to(torch.int32).reshape(-1).contiguous().data_ptr(), key_pages.data_ptr(),
+        value_pages.data_ptr(), key_pages.shape[0], key_pages.shape[2],
+        _lib.dtype_code(qkv.dtype), q.data_ptr(), _lib.ptr(k), _lib.ptr(v), _lib.stream_of(dev)))
+    return q, k, v

@@ -30,7 +30,10 @@ class PagedKVCache:
         self.page_size = page_size
         self.dtype = dtype
         self.device = torch.device(device)
-        shape = (num_pages, num_kv_heads, page_size, head_dim)
+        # one page past the pool takes the writes of padding rows and of
+        # graph warm-up/capture runs; it is never handed to a request
+        self.scratch_page = num_pages
+        shape = (num_pages + 1, num_kv_heads, page_size, head_dim)
         self.key_pages = [torch.zeros(shape, dtype=dtype, device=self.device)
                           for _ in range(num_layers)]
         self.value_pages = [torch.zeros(shape, dtype=dtype, device=self.device)
@@ -82,14 +85,15 @@ class PagedKVCache:
                 pages.append(plist[j // ps])
                 slots.append(j % ps)
         dev = self.device
-        return (torch.tensor(pages, dtype=torch.long, device=dev),
-                torch.tensor(slots, dtype=torch.long, device=dev))
+        return (torch.tensor(pages, dtype=torch.int32, device=dev),
+                torch.tensor(slots, dtype=torch.int32, device=dev))
 
     def write(self, layer: int, k: torch.Tensor, v: torch.Tensor, page_ids: torch.Tensor,
               slots: torch.Tensor) -> None:
         """Store ``k``/``v [B, L, num_kv_heads, D]`` at the mapped slots."""
         kk = k.reshape(-1, self.num_kv_heads, self.head_dim).to(self.dtype)
         vv = v.reshape(-1, self.num_kv_heads, self.head_dim).to(self.dtype)
+        page_ids, slots = page_ids.long(), slots.long()
         self.key_pages[layer][page_ids, :, slots, :] = kk
         self.value_pages[layer][page_ids, :, slots, :] = vv
 
@@ -97,10 +101,11 @@ class PagedKVCache:
         for s in seq_ids:
             self.lens[s] += n_new
 
-    def block_table(self, seq_ids: Sequence[int], extra: int = 0):
-        """``block_table [B, max_pages]`` (-1 past a request's pages) and
-        ``context_lens [B]`` (current length + ``extra``) as int32 tensors."""
-        width = max(1, max(len(self.pages[s]) for s in seq_ids))
+    def block_table(self, seq_ids: Sequence[int], extra: int = 0, width: int | None = None):
+        """``block_table [B, width]`` (-1 past a request's pages; width defaults
+        to the longest page list) and ``context_lens [B]`` (current length +
+        ``extra``) as int32 tensors."""
+        width = width or max(1, max(len(self.pages[s]) for s in seq_ids))
         rows = [self.pages[s] + [-1] * (width - len(self.pages[s])) for s in seq_ids]
         dev = self.device
         return (torch.tensor(rows, dtype=torch.int32, device=dev),

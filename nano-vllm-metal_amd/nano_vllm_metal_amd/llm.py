@@ -23,7 +23,8 @@ from typing import List, Optional, Sequence, Union
 
 import torch
 
-from .qwen3 import Qwen3Model
+from .moe import Moe
+from .qwen3 import Qwen3Model, StepInputs
 
 
 @dataclass
@@ -71,6 +72,38 @@ def sample(logits: torch.Tensor, sp: SamplingParams, generator=None) -> torch.Te
     return torch.multinomial(probs, 1, generator=generator)[:, 0]
 
 
+class _DecodeGraph:
+    """One decode step of B requests captured in a HIP graph: static index
+    buffers are refilled before each replay.  Warm-up and capture run with
+    empty contexts and write only the cache's scratch page."""
+
+    def __init__(self, model: Qwen3Model, cache, B: int, width: int):
+        dev = model.device
+        self.tokens = torch.zeros((B, 1), dtype=torch.long, device=dev)
+        self.step = StepInputs(
+            positions=torch.zeros((B,), dtype=torch.int32, device=dev),
+            page_ids=torch.full((B,), cache.scratch_page, dtype=torch.int32, device=dev),
+            slots=torch.zeros((B,), dtype=torch.int32, device=dev),
+            block_table=torch.full((B, width), -1, dtype=torch.int32, device=dev),
+            lens=torch.zeros((B,), dtype=torch.int32, device=dev), initial=False)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                model.run(self.tokens, self.step, cache)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = model.run(self.tokens, self.step, cache)
+
+    def __call__(self, tokens: torch.Tensor, step: StepInputs) -> torch.Tensor:
+        self.tokens.copy_(tokens)
+        for name in ("positions", "page_ids", "slots", "block_table", "lens"):
+            getattr(self.step, name).copy_(getattr(step, name))
+        self.graph.replay()
+        return self.logits
+
+
 class _Request:
     def __init__(self, rid: int, prompt, ids: List[int], sp: SamplingParams):
         self.rid = rid
@@ -89,7 +122,7 @@ class LLM:
     def __init__(self, model: Union[str, Qwen3Model], max_num_seqs: int = 8,
                  max_model_len: int = 4096, page_size: int = 16, prefill_step: int = 2048,
                  tokenizer=None, device="cuda", dtype: torch.dtype = torch.bfloat16,
-                 eos_token_id: Optional[int] = None):
+                 eos_token_id: Optional[int] = None, use_graphs: bool = True):
         if isinstance(model, Qwen3Model):
             self.model = model
         else:
@@ -101,7 +134,19 @@ class LLM:
         self.max_model_len = max_model_len
         self.prefill_step = prefill_step
         pages_per_seq = -(-max_model_len // page_size)
+        self.pages_per_seq = pages_per_seq
         self.cache = self.model.create_kv_cache(max_num_seqs * pages_per_seq, page_size)
+        # decode steps replay HIP graphs (one per batch size).  The MoE
+        # workspaces are sized for the largest step first, so a captured graph
+        # never refers to a buffer that a later, larger call reallocates.
+        self.use_graphs = use_graphs
+        self._graphs = {}
+        c = self.model.config
+        t_max = max(prefill_step, max_num_seqs)
+        for layer in self.model.layers:
+            if isinstance(layer.mlp, Moe):
+                layer.mlp._workspace(t_max, c.hidden_size, c.moe_intermediate_size,
+                                     c.num_experts, self.model.device)
         if eos_token_id is None and tokenizer is not None:
             eos_token_id = getattr(tokenizer, "eos_token_id", None)
         self.eos_token_id = eos_token_id
@@ -114,7 +159,7 @@ class LLM:
             return list(self.tokenizer.encode(prompt))
         return [int(t) for t in prompt]
 
-    def _decode(self, ids: List[int]) -> str:
+    def _detok(self, ids: List[int]) -> str:
         return self.tokenizer.decode(ids) if self.tokenizer is not None else ""
 
     def _finished(self, r: _Request, tok: int) -> bool:
@@ -123,6 +168,19 @@ class LLM:
         if not r.sp.ignore_eos and self.eos_token_id is not None and tok == self.eos_token_id:
             return True
         return len(r.ids) + len(r.out) >= self.max_model_len
+
+    def _decode_step(self, tokens: torch.Tensor, seq_ids: List[int]) -> torch.Tensor:
+        """One decode step of the running requests (graph replay when enabled)."""
+        m, cache = self.model, self.cache
+        if not self.use_graphs:
+            return m.forward(tokens, cache, seq_ids)
+        step = m.prepare(cache, seq_ids, 1, width=self.pages_per_seq)
+        B = len(seq_ids)
+        if B not in self._graphs:
+            self._graphs[B] = _DecodeGraph(m, cache, B, self.pages_per_seq)
+        logits = self._graphs[B](tokens, step)
+        cache.advance(seq_ids, 1)
+        return logits
 
     def _prefill(self, r: _Request) -> int:
         """Run the prompt in chunks; returns the first sampled token."""
@@ -174,7 +232,7 @@ class LLM:
             torch.cuda.synchronize(m.device)
             t0 = time.perf_counter()
             last = torch.tensor([[r.out[-1]] for r in running], dtype=torch.long, device=m.device)
-            logits = m.forward(last, cache, [r.rid for r in running])
+            logits = self._decode_step(last, [r.rid for r in running])
             nxt = sample(logits, sp).tolist()
             self.stats.decode_s += time.perf_counter() - t0
             self.stats.decode_steps += 1
@@ -188,7 +246,7 @@ class LLM:
                 else:
                     still.append(r)
             running = still
-        return [GenerationOutput(r.prompt, self._decode(r.out), r.out) for r in reqs]
+        return [GenerationOutput(r.prompt, self._detok(r.out), r.out) for r in reqs]
 
 
 def _local_tokenizer(path):

@@ -13,10 +13,14 @@ A torch port of the reference's ``Qwen3PagedModel`` (``models/qwen3.py``):
 * the model (``:263-394``): quantised embedding (``layers/embed_head.py``),
   final RMSNorm, lm head (or the tied embedding as a linear).
 
-Every matrix product runs on this package's HIP kernels (``quantized_linear``,
-``Moe``, ``paged_attention``); norms, RoPE, residual adds and the initial
-prefill's SDPA are torch GPU ops.  Activations are bf16 (or fp16) like the
-reference's ``precision``; norms and RoPE compute in float32 and round once.
+Every step runs on this package's HIP kernels: the q/k/v projections as one
+``quantized_linear`` over stacked weights, per-head norm + RoPE + k/v store
+in one kernel, ``paged_attention``, ``Moe``, and the residual adds fused with
+the RMSNorm that follows each.  The initial prefill's causal attention over
+the new tokens is torch's SDPA (float32, as the reference's
+``mx.fast.scaled_dot_product_attention``).  Activations are bf16 (or fp16)
+like the reference's ``precision``; norms and RoPE compute in float32 and
+round where the reference materialises a tensor.
 """
 
 from __future__ import annotations
@@ -29,6 +33,7 @@ import torch
 import torch.nn.functional as F
 
 from .attention import paged_attention
+from .fused import qk_norm_rope_store, residual_rms_norm
 from .kv_cache import PagedKVCache
 from .linear import QuantizedWeights, dequantize, quantized_linear
 from .moe import Moe
@@ -70,33 +75,18 @@ class Qwen3Config:
                 and (layer + 1) % (self.decoder_sparse_step or 1) == 0)
 
 
-def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """``mx.fast.rms_norm`` (layers/layernorm.py): float32, one rounding."""
-    xf = x.float()
-    y = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps) * weight.float()
-    return y.to(x.dtype)
-
-
 class RoPE:
-    """``layers/rotary_embedding.py:RoPE`` with ``traditional=False``: rotate
-    the halves [x1, x2] by float32 cos/sin tables of ``base ** (-i / (D/2))``."""
+    """The float32 cos/sin tables of ``layers/rotary_embedding.py:RoPE``
+    (``traditional=False``): angle ``position * base ** (-i / (D/2))``; the
+    rotation itself runs in the fused q/k kernel."""
 
     def __init__(self, dims: int, max_positions: int, base: float, device):
         half = dims // 2
         inv = torch.pow(torch.tensor(float(base), dtype=torch.float32),
                         -(torch.arange(half, dtype=torch.float32) / half))
         freqs = torch.outer(torch.arange(max_positions, dtype=torch.float32), inv)
-        self.cos = torch.cos(freqs).to(device)
-        self.sin = torch.sin(freqs).to(device)
-        self.half = half
-
-    def __call__(self, x: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
-        """``x [B, L, heads, D]``, ``positions [B, L]``."""
-        cos = self.cos[positions][:, :, None, :]
-        sin = self.sin[positions][:, :, None, :]
-        xf = x.float()
-        x1, x2 = xf[..., :self.half], xf[..., self.half:2 * self.half]
-        return torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], dim=-1).to(x.dtype)
+        self.cos = torch.cos(freqs).to(device).contiguous()
+        self.sin = torch.sin(freqs).to(device).contiguous()
 
 
 class DenseMLP:
@@ -113,6 +103,18 @@ class DenseMLP:
 
 
 @dataclass
+class StepInputs:
+    """Device index tensors of one model step (see ``Qwen3Model.prepare``)."""
+
+    positions: torch.Tensor    # [B*L] int32: position of each new token
+    page_ids: torch.Tensor     # [B*L] int32: its page
+    slots: torch.Tensor        # [B*L] int32: its slot in the page
+    block_table: torch.Tensor  # [B, max_pages] int32
+    lens: torch.Tensor         # [B] int32: context length after the step
+    initial: bool              # every request starts from an empty cache
+
+
+@dataclass
 class Qwen3Layer:
     wq: QuantizedWeights
     wk: QuantizedWeights
@@ -123,6 +125,17 @@ class Qwen3Layer:
     input_norm: torch.Tensor
     post_norm: torch.Tensor
     mlp: object  # Moe or DenseMLP
+    wqkv: Optional[QuantizedWeights] = None  # q, k and v stacked along the output rows
+
+
+def stack_outputs(*ws: QuantizedWeights) -> QuantizedWeights:
+    """One product for several projections of the same input: rows, scales
+    and biases concatenated along the output dimension."""
+    gs, bits = ws[0].group_size, ws[0].bits
+    if any(w.group_size != gs or w.bits != bits for w in ws):
+        raise ValueError("stack_outputs: projections differ in group_size or bits")
+    return QuantizedWeights(torch.cat([w.scales for w in ws]), torch.cat([w.biases for w in ws]),
+                            gs, bits, torch.cat([w.weight for w in ws]))
 
 
 class Qwen3Model:
@@ -138,6 +151,9 @@ class Qwen3Model:
         self.device = embed.weight.device
         self.rope = RoPE(config.head_dim, config.max_position_embeddings, config.rope_theta,
                          self.device)
+        for layer in self.layers:
+            if layer.wqkv is None:
+                layer.wqkv = stack_outputs(layer.wq, layer.wk, layer.wv)
 
     # ---------------------------------------------------------------- pieces
 
@@ -153,62 +169,76 @@ class Qwen3Model:
                           w.bits)
         return rows.to(self.dtype)
 
-    def _attention(self, li: int, layer: Qwen3Layer, x: torch.Tensor, positions: torch.Tensor,
-                   cache: PagedKVCache, page_ids, slots, block_table, lens,
-                   initial: bool) -> torch.Tensor:
+    def _attention(self, li: int, layer: Qwen3Layer, x: torch.Tensor, step: "StepInputs",
+                   cache: PagedKVCache) -> torch.Tensor:
         c = self.config
         B, L, _ = x.shape
         Hq, Hkv, D = c.num_attention_heads, c.num_key_value_heads, c.head_dim
-        q = quantized_linear(x, layer.wq).reshape(B, L, Hq, D)
-        k = quantized_linear(x, layer.wk).reshape(B, L, Hkv, D)
-        v = quantized_linear(x, layer.wv).reshape(B, L, Hkv, D)
-        q = self.rope(rms_norm(q, layer.q_norm, c.rms_norm_eps), positions)
-        k = self.rope(rms_norm(k, layer.k_norm, c.rms_norm_eps), positions)
-        cache.write(li, k, v, page_ids, slots)
+        qkv = quantized_linear(x, layer.wqkv)
+        q, k, v = qk_norm_rope_store(qkv, Hq, Hkv, D, layer.q_norm, layer.k_norm, c.rms_norm_eps,
+                                     step.positions, self.rope.cos, self.rope.sin, step.page_ids,
+                                     step.slots, cache.key_pages[li], cache.value_pages[li],
+                                     want_kv=step.initial)
+        q = q.view(B, L, Hq, D).transpose(1, 2)
         scale = D ** -0.5
-        if initial:
+        if step.initial:
             # every request starts from an empty cache: causal attention over
             # the new tokens only (models/qwen3.py:134-141)
-            qf = q.transpose(1, 2).float()
-            kf = k.transpose(1, 2).float().repeat_interleave(Hq // Hkv, dim=1)
-            vf = v.transpose(1, 2).float().repeat_interleave(Hq // Hkv, dim=1)
-            o = F.scaled_dot_product_attention(qf, kf, vf, is_causal=True, scale=scale)
+            kf = k.view(B, L, Hkv, D).transpose(1, 2).repeat_interleave(Hq // Hkv, dim=1)
+            vf = v.view(B, L, Hkv, D).transpose(1, 2).repeat_interleave(Hq // Hkv, dim=1)
+            o = F.scaled_dot_product_attention(q, kf, vf, is_causal=True, scale=scale)
         else:
-            o = paged_attention(q.transpose(1, 2), cache.key_pages[li], cache.value_pages[li],
-                                block_table, lens, cache.page_size, scale=scale, mask="causal")
+            o = paged_attention(q, cache.key_pages[li], cache.value_pages[li], step.block_table,
+                                step.lens, cache.page_size, scale=scale, mask="causal")
         o = o.to(x.dtype).transpose(1, 2).reshape(B, L, Hq * D)
         return quantized_linear(o, layer.wo)
 
     # ---------------------------------------------------------------- forward
+
+    def prepare(self, cache: PagedKVCache, seq_ids: Sequence[int], L: int,
+                width: Optional[int] = None) -> "StepInputs":
+        """Host bookkeeping of one step: reserve pages for the next L tokens of
+        every request and build the step's index tensors."""
+        starts = [cache.lens[s] for s in seq_ids]
+        for s in seq_ids:
+            cache.reserve(s, L)
+        page_ids, slots = cache.slot_mapping(seq_ids, L)
+        block_table, lens = cache.block_table(seq_ids, extra=L, width=width)
+        positions = torch.tensor([st + j for st in starts for j in range(L)], dtype=torch.int32,
+                                 device=self.device)
+        return StepInputs(positions, page_ids, slots, block_table, lens,
+                          L > 1 and all(st == 0 for st in starts))
+
+    def run(self, tokens: torch.Tensor, step: "StepInputs", cache: PagedKVCache,
+            last_only: bool = True) -> torch.Tensor:
+        """The device work of one step (no host synchronisation: it can be
+        captured in a HIP graph)."""
+        eps = self.config.rms_norm_eps
+        h = self.embed(tokens)
+        # residual adds fused with the norm that follows them
+        _, x = residual_rms_norm(h, None, self.layers[0].input_norm, eps)
+        n = len(self.layers)
+        for li, layer in enumerate(self.layers):
+            h, x = residual_rms_norm(h, self._attention(li, layer, x, step, cache),
+                                     layer.post_norm, eps)
+            nxt = self.layers[li + 1].input_norm if li + 1 < n else self.norm
+            h, x = residual_rms_norm(h, layer.mlp(x), nxt, eps)
+        if last_only:
+            x = x[:, -1]
+        return quantized_linear(x, self.lm_head if self.lm_head is not None else self.embed_w)
 
     def forward(self, tokens: torch.Tensor, cache: PagedKVCache, seq_ids: Sequence[int],
                 last_only: bool = True) -> torch.Tensor:
         """Run ``tokens [B, L]`` (the next L tokens of each request) through the
         model, appending their keys/values to ``cache``.  Returns the logits of
         the last position ``[B, vocab]`` or of every position ``[B, L, vocab]``."""
-        c = self.config
         B, L = tokens.shape
         if len(seq_ids) != B:
             raise ValueError("forward: one sequence id per batch row")
-        starts = [cache.lens[s] for s in seq_ids]
-        for s in seq_ids:
-            cache.reserve(s, L)
-        page_ids, slots = cache.slot_mapping(seq_ids, L)
-        block_table, lens = cache.block_table(seq_ids, extra=L)
-        positions = (torch.tensor(starts, dtype=torch.long, device=self.device)[:, None]
-                     + torch.arange(L, device=self.device)[None, :])
-        initial = L > 1 and all(st == 0 for st in starts)
-        h = self.embed(tokens.to(self.device))
-        for li, layer in enumerate(self.layers):
-            x = rms_norm(h, layer.input_norm, c.rms_norm_eps)
-            h = h + self._attention(li, layer, x, positions, cache, page_ids, slots, block_table,
-                                    lens, initial)
-            h = h + layer.mlp(rms_norm(h, layer.post_norm, c.rms_norm_eps))
+        step = self.prepare(cache, seq_ids, L)
+        logits = self.run(tokens.to(self.device), step, cache, last_only)
         cache.advance(seq_ids, L)
-        if last_only:
-            h = h[:, -1]
-        h = rms_norm(h, self.norm, c.rms_norm_eps)
-        return quantized_linear(h, self.lm_head if self.lm_head is not None else self.embed_w)
+        return logits
 
     __call__ = forward
 

@@ -225,3 +225,21 @@ def test_paged_attention_workspace_size():
     assert lib.nvm_paged_attention_workspace_size(32 * 32, 4, 128, 80, 16, 1, 4, 32,
                                                   ctypes.byref(sz)) == 0
     assert sz.value == 0
+
+
+@pytest.mark.parametrize("call,code,msg", [
+    (lambda lib: lib.nvm_residual_rms_norm(1, 1, 1, 4, 2047, 1e-6, 1, 1, 1, None), -1, "bad shape"),
+    (lambda lib: lib.nvm_residual_rms_norm(1, 1, 1, 4, 16384, 1e-6, 1, 1, 1, None), -2, "at most"),
+    (lambda lib: lib.nvm_residual_rms_norm(1, 1, 1, 4, 2048, 1e-6, 7, 1, 1, None), -1, "dtype"),
+    (lambda lib: lib.nvm_residual_rms_norm(1, 1, 1, 4, 2048, 1e-6, 1, None, 1, None), -1, "null"),
+    (lambda lib: lib.nvm_qk_norm_rope_store(1, 4, 32, 4, 130, 1, 1, 1e-6, 1, 1, 1, 100, 1, 1, 1, 1,
+                                            8, 16, 1, 1, None, None, None), -2, "multiple of 4"),
+    (lambda lib: lib.nvm_qk_norm_rope_store(1, 4, 32, 4, 128, 1, 1, 1e-6, 1, 1, 1, 100, 1, 1, 1, 1,
+                                            8, 16, 1, None, None, None, None), -1, "null"),
+])
+def test_model_ops_validation(call, code, msg):
+    """nvm_residual_rms_norm / nvm_qk_norm_rope_store reject bad arguments
+    before any device work."""
+    _, lib = _lib()
+    assert call(lib) == code
+    assert msg in _err(lib)

@@ -1,0 +1,87 @@
+"""GPU parity of the fused layer steps (include/nvm_model.h) against plain
+torch float32 restatements of the reference ops (tests/qwen3_reference.py):
+residual add + RMSNorm (layers/layernorm.py) and per-head q/k RMSNorm + RoPE
++ k/v page store (models/qwen3.py:103-133, layers/rotary_embedding.py).
+
+The residual sum is one rounding of an exact sum: bit-identical.  Normalised
+and rotated values may differ from torch by one activation ulp where the
+float32 sum of squares rounds differently (different summation order):
+bounded by 2 ulps, and at least 95 % of the values identical.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from qwen3_reference import _rms, _rope
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+ULP = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}
+
+
+def _near(a, b, dt, what):
+    a, b = a.float(), b.float()
+    tol = 2 * ULP[dt] * b.abs() + 1e-6
+    bad = (a - b).abs() > tol
+    assert not bad.any(), f"{what}: {int(bad.sum())} values beyond 2 ulps"
+    assert (a == b).float().mean().item() > 0.95, f"{what}: too few identical values"
+
+
+@pytest.mark.parametrize("T,H,dt", [(37, 2048, torch.bfloat16), (5, 640, torch.float16),
+                                    (1, 8192, torch.bfloat16)])
+def test_residual_rms_norm(T, H, dt):
+    from nano_vllm_metal_amd.fused import residual_rms_norm
+
+    g = torch.Generator(device=DEV).manual_seed(T + H)
+    h = (torch.randn(T, H, device=DEV, generator=g) * 3).to(dt)
+    r = torch.randn(T, H, device=DEV, generator=g).to(dt)
+    w = (1 + 0.1 * torch.randn(H, device=DEV, generator=g)).to(dt)
+    h2, x = residual_rms_norm(h, r, w, 1e-6)
+    assert torch.equal(h2, (h.float() + r.float()).to(dt))
+    _near(x, _rms(h2, w, 1e-6), dt, "norm after residual")
+    h3, x3 = residual_rms_norm(h, None, w, 1e-6)
+    assert h3 is h
+    _near(x3, _rms(h, w, 1e-6), dt, "norm")
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,dt", [(32, 4, 128, torch.bfloat16), (8, 2, 64, torch.float16),
+                                         (4, 4, 128, torch.bfloat16)])
+def test_qk_norm_rope_store(Hq, Hkv, D, dt):
+    from nano_vllm_metal_amd.fused import qk_norm_rope_store
+    from nano_vllm_metal_amd.qwen3 import RoPE
+
+    T, P, ps, max_pos = 9, 6, 4, 300
+    g = torch.Generator(device=DEV).manual_seed(Hq + D)
+    qkv = torch.randn(T, (Hq + 2 * Hkv) * D, device=DEV, generator=g).to(dt)
+    qn = (1 + 0.2 * torch.randn(D, device=DEV, generator=g)).to(dt)
+    kn = (1 + 0.2 * torch.randn(D, device=DEV, generator=g)).to(dt)
+    pos = torch.randint(0, max_pos, (T,), device=DEV, generator=g).to(torch.int32)
+    rope = RoPE(D, max_pos, 1e6, DEV)
+    pages = torch.randperm(P, device=DEV, generator=g)[:3].to(torch.int32)
+    page_ids = pages.repeat_interleave(3)[:T].clone()
+    slots = (torch.arange(T, device=DEV) % 3).to(torch.int32)
+    page_ids[4] = -1  # not stored
+    kp = torch.zeros(P, Hkv, ps, D, dtype=dt, device=DEV)
+    vp = torch.zeros_like(kp)
+    q, k, v = qk_norm_rope_store(qkv, Hq, Hkv, D, qn, kn, 1e-6, pos, rope.cos, rope.sin, page_ids,
+                                 slots, kp, vp, want_kv=True)
+    x = qkv.view(T, Hq + 2 * Hkv, D)
+    rq = _rope(_rms(x[:, :Hq], qn, 1e-6), pos.long(), 1e6)
+    rk = _rope(_rms(x[:, Hq:Hq + Hkv], kn, 1e-6), pos.long(), 1e6)
+    rv = x[:, Hq + Hkv:]
+    _near(q, rq, dt, "q")
+    _near(k, rk, dt, "k")
+    assert torch.equal(v, rv.float())
+    for t in range(T):
+        if t == 4:
+            continue
+        pg, sl = int(page_ids[t]), int(slots[t])
+        assert torch.equal(kp[pg, :, sl], k[t].to(dt))
+        assert torch.equal(vp[pg, :, sl], rv[t])
+    written = torch.zeros(P, ps, dtype=torch.bool, device=DEV)
+    for t in range(T):
+        if t != 4:
+            written[int(page_ids[t]), int(slots[t])] = True
+    assert not kp.permute(0, 2, 1, 3)[~written].any()

@@ -193,12 +193,15 @@ def test_batched_decode_matches_single_requests():
 
 
 @pytest.mark.gpu
-def test_generate_greedy_is_the_model_argmax_chain():
+@pytest.mark.parametrize("graphs", [False, True])
+def test_generate_greedy_is_the_model_argmax_chain(graphs):
+    """Continuous batching (3 requests, 2 slots) with eager or graph-replayed
+    decode steps gives each request the greedy chain it gets alone."""
     from nano_vllm_metal_amd import LLM, SamplingParams
 
     m = _model(4)
     prompts = [_tokens(n, seed=20 + n) for n in (5, 11, 8)]
-    llm = LLM(m, max_num_seqs=2, max_model_len=64, page_size=4)
+    llm = LLM(m, max_num_seqs=2, max_model_len=64, page_size=4, use_graphs=graphs)
     outs = llm.generate(prompts, SamplingParams(max_tokens=6))
     assert [len(o.token_ids) for o in outs] == [6, 6, 6]
     assert llm.cache.free_pages == llm.cache.num_pages
@@ -215,3 +218,27 @@ def test_generate_greedy_is_the_model_argmax_chain():
         assert o.token_ids == chain
     st = llm.stats
     assert st.prefill_tokens == 24 and st.decode_tokens == 15
+
+
+@pytest.mark.gpu
+def test_graph_decode_matches_eager_logits():
+    """Replayed decode steps give the eager step's logits (same kernels,
+    same inputs) on every replay, and the capture touched no live page."""
+    from nano_vllm_metal_amd import LLM
+
+    m = _model(5)
+    prompts = [_tokens(n, seed=40 + n) for n in (7, 4)]
+    eager = LLM(m, max_num_seqs=2, max_model_len=32, page_size=4, use_graphs=False)
+    graph = LLM(m, max_num_seqs=2, max_model_len=32, page_size=4, use_graphs=True)
+    for llm in (eager, graph):
+        for i, p in enumerate(prompts):
+            llm.cache.add(i)
+            m.forward(torch.tensor([p], device=DEV), llm.cache, [i])
+    toks = [3, 17]
+    for step in range(4):
+        t = torch.tensor([[x] for x in toks], device=DEV)
+        a = eager._decode_step(t, [0, 1]).float()
+        b = graph._decode_step(t, [0, 1]).float()
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"step {step}"
+        toks = [int(x) for x in torch.argmax(a, -1)]
