@@ -11,7 +11,8 @@ them.  The decode value is timed over HIP-graph replays of the layer calls;
 per-kernel durations come from HIP events around each stage in an eager pass.
 
 Also reported: decode batches 1/8/64, prefill of 4096 tokens with uniform and
-Zipf(1.1) routing (MFMA roofline), the dense W4A16 projections of the same
+Zipf(1.1) routing (MFMA roofline), the Qwen3-235B-A22B-shaped MoE layer
+(decode 32, prefill 2048), the dense W4A16 projections of the same
 model through quantized_matmul (q/k/o and the lm head, 1/32/4096 rows), and
 the CPU baseline (the C restatement of the reference algorithm in oracle/,
 timed on a bounded sample).
@@ -37,6 +38,8 @@ HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
 MFMA_BF16_PEAK_TFLOPS = 2500.0   # dense bf16 MFMA
 METRIC = "MoE-layer tokens/s + HBM GB/s, 30B-A3B shape, decode B=32 / prefill 4K"
 SHAPE = dict(H=2048, E=128, I=768, k=8, gs=64)
+# Qwen3-235B-A22B's MoE layer (also reported: decode B=32, prefill 2048)
+SHAPE_235B = dict(H=4096, E=128, I=1536, k=8, gs=64)
 
 
 def log(*a):
@@ -54,7 +57,7 @@ def router_bytes(H, E, gs):
     return E * H // 2 + 2 * 2 * E * (H // gs)
 
 
-def make_layers(n_layers, H, E, I, gs, dev, seed=1234, zipf_s=None):
+def make_layers(n_layers, H, E, I, gs, dev, seed=1234, zipf_s=None, k=None):
     import torch
     from nano_vllm_metal_amd import Moe, QuantizedWeights, quantize
 
@@ -78,7 +81,7 @@ def make_layers(n_layers, H, E, I, gs, dev, seed=1234, zipf_s=None):
             p = ranks ** (-zipf_s)
             bias = torch.log(p / p.sum())
         moe = Moe(q((E, H), router_bias=bias), q((E, I, H)), q((E, I, H)), q((E, H, I)),
-                  num_experts_per_tok=SHAPE["k"], norm_topk_prob=True)
+                  num_experts_per_tok=k or SHAPE["k"], norm_topk_prob=True)
         layers.append(moe)
     torch.cuda.synchronize()
     return layers
@@ -239,8 +242,8 @@ def eager_fused_pass(layers, xs, steps, warmup, dev):
     return e0.elapsed_time(e1) * 1e3 / steps
 
 
-def decode_bench(layers, T, steps, warmup, dev, use_graph=True):
-    H, E, I, k, gs = (SHAPE[n] for n in ("H", "E", "I", "k", "gs"))
+def decode_bench(layers, T, steps, warmup, dev, use_graph=True, shape=None):
+    H, E, I, k, gs = ((shape or SHAPE)[n] for n in ("H", "E", "I", "k", "gs"))
     xs = make_inputs(8, T, H, dev)
     stage_us, eager_layer_us, touched, _ = eager_stage_pass(layers, xs, steps, warmup, dev)
     fused_us = eager_fused_pass(layers, xs, steps, warmup, dev)
@@ -268,10 +271,10 @@ def decode_bench(layers, T, steps, warmup, dev, use_graph=True):
     }
 
 
-def prefill_bench(layers, T, steps, warmup, dev, zipf):
+def prefill_bench(layers, T, steps, warmup, dev, zipf, shape=None):
     import torch
 
-    H, E, I, k, gs = (SHAPE[n] for n in ("H", "E", "I", "k", "gs"))
+    H, E, I, k, gs = ((shape or SHAPE)[n] for n in ("H", "E", "I", "k", "gs"))
     xs = make_inputs(2, T, H, dev, seed=7 if zipf else 5, zipf=zipf)
     stage_us, layer_us, touched, ids = eager_stage_pass(layers, xs, steps, warmup, dev)
     N = T * k
@@ -293,6 +296,23 @@ def prefill_bench(layers, T, steps, warmup, dev, zipf):
         "expert_load_max_over_mean": float(counts.max() / counts.mean()),
         "experts_touched": int((counts > 0).sum()),
     }
+
+
+def shape_235b_bench(dev, steps):
+    """The Qwen3-235B-A22B MoE layer (hidden 4096, 128 experts, top-8,
+    intermediate 1536, int4 g64): decode batch 32 and prefill 2048 tokens,
+    over 3 distinct layers of weights (1.2 GB each)."""
+    import torch
+
+    sh = SHAPE_235B
+    layers = make_layers(3, sh["H"], sh["E"], sh["I"], sh["gs"], dev, seed=2350, k=sh["k"])
+    d = decode_bench(layers, 32, max(steps // 2, 16), 10, dev, True, shape=sh)
+    p = prefill_bench(layers, 2048, max(steps // 20, 8), 3, dev, False, shape=sh)
+    log(f"[bench] 235B decode B=32: {d['layer_us']:.1f} us/layer, {d['hbm_gbs']:.0f} GB/s; "
+        f"prefill 2048: {p['layer_us']:.1f} us/layer, {p['layer_tflops']:.0f} TFLOP/s")
+    del layers
+    torch.cuda.empty_cache()
+    return {"decode_32": d, "prefill_2048": p}
 
 
 # Dense W4A16 projections of the same model (quantized_linear): name, in, out.
@@ -582,6 +602,8 @@ def main():
                     help="measure only the dense W4A16 projections (quantized_matmul)")
     ap.add_argument("--attention-only", action="store_true",
                     help="measure only paged decode attention")
+    ap.add_argument("--moe-235b-only", action="store_true",
+                    help="measure only the 235B-A22B-shaped MoE layer (decode 32, prefill 2048)")
     ap.add_argument("--e2e", action="store_true",
                     help="measure only the full 48-layer model through LLM.generate "
                          "(32 x 1024-token prompts, 256 greedy tokens)")
@@ -613,6 +635,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.moe_235b_only:
+        print(json.dumps({"moe_235b": shape_235b_bench(dev, args.steps)}), flush=True)
+        return
     if args.e2e:
         r = e2e_bench(dev)
         log(f"[bench] e2e: decode {r['decode_tokens_per_s']:.0f} tok/s "
@@ -704,6 +729,8 @@ def main():
                 f"{r['layer_tflops']:.0f} TFLOP/s, kernels {r['kernel_us']}")
             if zipf:
                 del lay
+        log("[bench] 235B-A22B-shaped MoE layer")
+        out["moe_235b"] = shape_235b_bench(dev, args.steps)
         log("[bench] dense W4A16 projections")
         out["dense"] = dense_bench(dev)
         log("[bench] paged decode attention")
