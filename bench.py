@@ -417,7 +417,7 @@ def e2e_bench(dev, n_seqs=32, prompt_len=1024, gen=256, layers=48):
     log(f"[bench] e2e: building a {layers}-layer 30B-A3B-shaped model (random int4 weights)")
     model = Qwen3Model.random(cfg, device=dev, seed=7)
     llm = LLM(model, max_num_seqs=n_seqs, max_model_len=prompt_len + gen + 16, page_size=16,
-              prefill_step=prompt_len)
+              prefill_step=8 * prompt_len)
     rng = np.random.default_rng(3)
     prompts = [rng.integers(0, cfg.vocab_size, prompt_len).tolist() for _ in range(n_seqs)]
     llm.generate([p[:32] for p in prompts[:4]], SamplingParams(max_tokens=4))  # warm-up

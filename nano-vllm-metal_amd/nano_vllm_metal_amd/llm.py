@@ -3,8 +3,9 @@
 Mirrors the reference's high-level entry point (``llm.py:21-93``,
 ``sampling_params.py``) and its scheduler's loop (``engine/scheduler.py``):
 requests wait in a queue; while fewer than ``max_num_seqs`` run and the page
-pool has room, the next request is admitted and its prompt prefilled (in
-chunks of ``prefill_step`` tokens); then every running request decodes one
+pool has room, requests are admitted and prefilled (requests of one prompt
+length together, up to ``prefill_step`` tokens per step; a longer prompt in
+chunks of ``prefill_step``); then every running request decodes one
 token in a single batched step; a request that reaches ``max_tokens`` (or its
 end-of-sequence token) is retired and its pages freed.  Sampling follows
 ``layers/sampler.py``: greedy at temperature 0, else temperature with top-k
@@ -182,17 +183,56 @@ class LLM:
         cache.advance(seq_ids, 1)
         return logits
 
-    def _prefill(self, r: _Request) -> int:
-        """Run the prompt in chunks; returns the first sampled token."""
+    def _prefill(self, batch: List[_Request]) -> List[int]:
+        """Prefill requests of one prompt length together (B x L tokens, at
+        most ``prefill_step``), or one long prompt in chunks; returns the first
+        sampled token of each."""
         m, cache = self.model, self.cache
-        cache.add(r.rid)
-        logits = None
-        for s in range(0, len(r.ids), self.prefill_step):
-            chunk = torch.tensor([r.ids[s:s + self.prefill_step]], dtype=torch.long,
-                                 device=m.device)
-            logits = m.forward(chunk, cache, [r.rid])
-        self.stats.prefill_tokens += len(r.ids)
-        return int(sample(logits, r.sp)[0])
+        for r in batch:
+            cache.add(r.rid)
+        L = len(batch[0].ids)
+        if L <= self.prefill_step:
+            toks = torch.tensor([r.ids for r in batch], dtype=torch.long, device=m.device)
+            logits = m.forward(toks, cache, [r.rid for r in batch])
+        else:
+            (r,) = batch
+            for s in range(0, L, self.prefill_step):
+                chunk = torch.tensor([r.ids[s:s + self.prefill_step]], dtype=torch.long,
+                                     device=m.device)
+                logits = m.forward(chunk, cache, [r.rid])
+        self.stats.prefill_tokens += L * len(batch)
+        return [int(t) for t in sample(logits, batch[0].sp).tolist()]
+
+    def _admit(self, waiting: deque, running: List[_Request]) -> None:
+        """Admit waiting requests while a sequence slot is free, prefill them
+        (equal prompt lengths batched) and move the unfinished ones to running."""
+        cache = self.cache
+        admitted: List[_Request] = []
+        while waiting and len(running) + len(admitted) < self.max_num_seqs:
+            r = waiting[0]
+            need = -(-(len(r.ids) + r.sp.max_tokens) // cache.page_size)
+            if need > cache.free_pages and (running or admitted):
+                break
+            admitted.append(waiting.popleft())
+        by_len = {}
+        for r in admitted:
+            by_len.setdefault(len(r.ids), []).append(r)
+        for L, group in by_len.items():
+            per = max(1, self.prefill_step // L)
+            for i in range(0, len(group), per):
+                batch = group[i:i + per]
+                torch.cuda.synchronize(self.model.device)
+                t0 = time.perf_counter()
+                toks = self._prefill(batch)
+                torch.cuda.synchronize(self.model.device)
+                self.stats.prefill_s += time.perf_counter() - t0
+                for r, tok in zip(batch, toks):
+                    r.out.append(tok)
+                    if self._finished(r, tok):
+                        r.done = True
+                        cache.free(r.rid)
+                    else:
+                        running.append(r)
 
     def generate(self, prompts: Union[str, Sequence], sampling_params: Optional[SamplingParams] = None
                  ) -> List[GenerationOutput]:
@@ -209,24 +249,7 @@ class LLM:
         running: List[_Request] = []
         m, cache = self.model, self.cache
         while waiting or running:
-            # admit while a sequence slot and pages for the whole request are free
-            while waiting and len(running) < self.max_num_seqs:
-                r = waiting[0]
-                need = -(-(len(r.ids) + r.sp.max_tokens) // cache.page_size)
-                if need > cache.free_pages and running:
-                    break
-                waiting.popleft()
-                torch.cuda.synchronize(m.device)
-                t0 = time.perf_counter()
-                tok = self._prefill(r)
-                torch.cuda.synchronize(m.device)
-                self.stats.prefill_s += time.perf_counter() - t0
-                r.out.append(tok)
-                if self._finished(r, tok):
-                    r.done = True
-                    cache.free(r.rid)
-                else:
-                    running.append(r)
+            self._admit(waiting, running)
             if not running:
                 continue
             torch.cuda.synchronize(m.device)

@@ -195,15 +195,17 @@ def test_batched_decode_matches_single_requests():
 @pytest.mark.gpu
 @pytest.mark.parametrize("graphs", [False, True])
 def test_generate_greedy_is_the_model_argmax_chain(graphs):
-    """Continuous batching (3 requests, 2 slots) with eager or graph-replayed
-    decode steps gives each request the greedy chain it gets alone."""
+    """Continuous batching (5 requests, 4 slots; two 8-token prompts prefilled
+    together under a 16-token budget) with eager or graph-replayed decode
+    steps gives each request the greedy chain it gets alone."""
     from nano_vllm_metal_amd import LLM, SamplingParams
 
     m = _model(4)
-    prompts = [_tokens(n, seed=20 + n) for n in (5, 11, 8)]
-    llm = LLM(m, max_num_seqs=2, max_model_len=64, page_size=4, use_graphs=graphs)
+    prompts = [_tokens(n, seed=20 + i) for i, n in enumerate((5, 11, 8, 8, 8))]
+    llm = LLM(m, max_num_seqs=4, max_model_len=64, page_size=4, use_graphs=graphs,
+              prefill_step=16)
     outs = llm.generate(prompts, SamplingParams(max_tokens=6))
-    assert [len(o.token_ids) for o in outs] == [6, 6, 6]
+    assert [len(o.token_ids) for o in outs] == [6] * 5
     assert llm.cache.free_pages == llm.cache.num_pages
     for p, o in zip(prompts, outs):
         cache = m.create_kv_cache(16, page_size=4)
@@ -217,7 +219,7 @@ def test_generate_greedy_is_the_model_argmax_chain(graphs):
             logits = m.forward(torch.tensor([[t]], device=DEV), cache, [0])
         assert o.token_ids == chain
     st = llm.stats
-    assert st.prefill_tokens == 24 and st.decode_tokens == 15
+    assert st.prefill_tokens == 40 and st.decode_tokens == 25
 
 
 @pytest.mark.gpu
