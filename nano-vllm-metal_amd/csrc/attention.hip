@@ -22,9 +22,11 @@
 //     reference.  C holds head c, positions 4G..4G+3 of each subtile.
 //   * Softmax in base 2 (scores pre-scaled by scale * log2 e): the tile's
 //     row maximum is two lane swaps, the row sums stay lane-partial.
-//   * P . V on the VALU: the tile's probabilities go to LDS; a group of D/8
-//     lanes (8 dims each, 16-byte value loads) covers a value row, and each
-//     of the 64/(D/8) groups takes D/8 consecutive positions of the tile.
+//   * P . V on the matrix cores as well, O^T += V^T . P^T per 32-position
+//     chunk: the S^T layout leaves each lane holding exactly its B operand
+//     (its head's probabilities at the chunk's k-slots), split into three
+//     page-dtype parts like q; the value rows (16-byte loads issued with the
+//     key loads) are staged in LDS and read back transposed as the A operand.
 //   * The four wavefronts' (max, sum, output) partials meet in LDS; with more
 //     than one split per row they go to the workspace and a second launch
 //     combines them.
@@ -90,12 +92,19 @@ template <int DT, int DH, int RP>
 __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
   using A = Act<DT>;
   constexpr int NC = DH / 32;        // 32-dim chunks of a score MFMA
-  constexpr int LPD = DH / 8;        // lanes per value row in P.V, 8 dims each
-  constexpr int PPG = LPD;           // positions per lane group per tile (64 / (64 / LPD))
-  __shared__ float s_p[4][kTile][RP];
-  __shared__ float s_alpha[4][RP];
+  constexpr int NT = DH / 16;        // 16-dim output tiles of a P.V MFMA
+  constexpr int LPD = DH / 8;        // lanes per value row in the V loads, 8 dims each
+  constexpr int PG = 64 / LPD;       // position groups of the V loads
+  constexpr int PPG = kTile / PG;    // positions per lane per tile
+  constexpr int VP = DH + 8;         // LDS pitch of a staged value row (16-bit elements)
+  // one 32-position chunk of values per wavefront during the tile loop; the
+  // wavefronts' output partials afterwards (the same LDS)
+  constexpr int kVBytes = 4 * 32 * VP * 2, kOBytes = 4 * RP * DH * 4;
+  __shared__ __attribute__((aligned(16))) char s_buf[kVBytes > kOBytes ? kVBytes : kOBytes];
+  auto s_v = reinterpret_cast<uint16_t(*)[32][VP]>(s_buf);
+  auto s_o = reinterpret_cast<float(*)[RP][DH]>(s_buf);
+  __shared__ u32x4 s_q[NC][3][64];  // the score MFMAs' B operand, per lane
   __shared__ int s_row[4][kTile];
-  __shared__ float s_o[4][RP][DH];
   __shared__ float s_m[4][RP], s_l[4][RP];
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -113,9 +122,10 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
   const int p0 = s * a.span;
   const int p1 = min(p0 + a.span, ctx);
 
-  // B operand of the score MFMAs: query head c16, dims 32k + 8G .. +7
-  u32x4 qb[NC][3];
-  {
+  // B operand of the score MFMAs (query head c16, dims 32k + 8G .. +7), the
+  // same for every wavefront: built once into LDS, read back per tile (it
+  // would hold 12 * NC VGPRs for the whole loop)
+  if (wv == 0) {
     const bool ok = c16 < nh;
     const float *qp = a.q + (n0 + (ok ? c16 : 0)) * DH;
 #pragma unroll
@@ -124,9 +134,14 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
       const f32x4 x0 = ok ? *(const f32x4 *)(qp + d0) : f32x4{0.f, 0.f, 0.f, 0.f};
       const f32x4 x1 = ok ? *(const f32x4 *)(qp + d0 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
       const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-      split3<DT>(x, qb[k][0], qb[k][1], qb[k][2]);
+      u32x4 q0, q1, q2;
+      split3<DT>(x, q0, q1, q2);
+      s_q[k][0][lane] = q0;
+      s_q[k][1][lane] = q1;
+      s_q[k][2][lane] = q2;
     }
   }
+  __syncthreads();
 
   const uint32_t kv_bytes = (uint32_t)((int64_t)a.P * a.Hkv * a.page_size * DH * 2);
   const rsrc_t kr = make_rsrc(a.kp, kv_bytes), vr = make_rsrc(a.vp, kv_bytes);
@@ -134,11 +149,10 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
   const int dd = 8 * (lane % LPD), pgrp = lane / LPD;
 
   float m_run = -INFINITY, l_run = 0.f;  // head c16; l_run is this lane's share
-  float o[RP][8];
+  // O^T tiles: lane (c16, G) holds head c16, dims 16t + 4G + i
+  f32x4 oacc[NT];
 #pragma unroll
-  for (int r = 0; r < RP; ++r)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o[r][j] = 0.f;
+  for (int t = 0; t < NT; ++t) oacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // page ids of positions t0 + 16u + c16, one tile ahead of their use
   auto page_ids = [&](int t0, int (&pg)[4]) {
@@ -175,12 +189,12 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
       if (G == 0) s_row[wv][16 * u + c16] = rowoff[u];
     }
     wave_lds_sync();
-    // the value rows of this lane's P.V positions, loaded with the keys (one
-    // memory round trip per tile)
+    // the value rows, loaded with the keys (one memory round trip per tile):
+    // lane group pgrp holds dims dd..dd+7 of positions pgrp + PG*mm
     u32x4 vv[PPG];
 #pragma unroll
     for (int mm = 0; mm < PPG; ++mm) {
-      const int ro = s_row[wv][pgrp * PPG + mm];
+      const int ro = s_row[wv][pgrp + PG * mm];
       vv[mm] = bload16(vr, ro >= 0 ? (ro + dd) * 2 : kMaskedOffset, 0);
     }
 
@@ -192,7 +206,8 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
 #pragma unroll
       for (int k = 0; k < NC; ++k)
 #pragma unroll
-        for (int part = 0; part < 3; ++part) acc[u] = A::mfma16(kop[u][k], qb[k][part], acc[u]);
+        for (int part = 0; part < 3; ++part)
+          acc[u] = A::mfma16(kop[u][k], s_q[k][part][lane], acc[u]);
     }
     float sc[4][4];
     float tmax = -INFINITY;
@@ -210,56 +225,61 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
     const bool any = m_new != -INFINITY;
     const float alpha = any ? exp2f(m_run - m_new) : 1.f;
     float psum = 0.f;
+    float pv[4][4];
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = any ? exp2f(sc[u][i] - m_new) : 0.f;
-        psum += p;
-        if (c16 < RP) s_p[wv][16 * u + 4 * G + i][c16] = p;
+        pv[u][i] = any ? exp2f(sc[u][i] - m_new) : 0.f;
+        psum += pv[u][i];
       }
     l_run = l_run * alpha + psum;
     m_run = m_new;
-    if (G == 0 && c16 < RP) s_alpha[wv][c16] = alpha;
-    wave_lds_sync();
+#pragma unroll
+    for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
 
-    // P . V: lane group pgrp takes positions pgrp*PPG .. +PPG-1 of the tile
+    // P . V on the matrix cores, one 32-position chunk at a time: O^T += V^T P^T.
+    // k-slot 8G + j of the chunk is position 4G + j (j < 4) or 16 + 4G + j - 4,
+    // so the B operand (P^T, head c16) is this lane's own probabilities of
+    // subtiles 2kc and 2kc+1, and the A operand (V^T, dim 16t + c16) is read
+    // from the chunk staged in LDS (pitch VP keeps the four lane groups on
+    // disjoint banks).
 #pragma unroll
-    for (int r = 0; r < RP; ++r) {
-      const float al = s_alpha[wv][r];
+    for (int kc = 0; kc < 2; ++kc) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[r][j] *= al;
-    }
+      for (int mm = kc * (32 / PG); mm < (kc + 1) * (32 / PG); ++mm)
+        *(u32x4 *)&s_v[wv][pgrp + PG * mm - 32 * kc][dd] = vv[mm];
+      wave_lds_sync();
+      const float x[8] = {pv[2 * kc][0], pv[2 * kc][1], pv[2 * kc][2], pv[2 * kc][3],
+                          pv[2 * kc + 1][0], pv[2 * kc + 1][1], pv[2 * kc + 1][2],
+                          pv[2 * kc + 1][3]};
+      u32x4 pb[3];
+      split3<DT>(x, pb[0], pb[1], pb[2]);
 #pragma unroll
-    for (int mm = 0; mm < PPG; ++mm) {
-      const int tp = pgrp * PPG + mm;
-      const u32x4 v = vv[mm];
-      const float vf[8] = {A::lo(v[0]), A::hi(v[0]), A::lo(v[1]), A::hi(v[1]),
-                           A::lo(v[2]), A::hi(v[2]), A::lo(v[3]), A::hi(v[3])};
+      for (int t = 0; t < NT; ++t) {
+        const int d = 16 * t + c16;
+        u32x4 va;
 #pragma unroll
-      for (int r = 0; r < RP; ++r) {
-        const float pr = s_p[wv][tp][r];
+        for (int jj = 0; jj < 4; ++jj) {
+          const int r0 = jj < 2 ? 4 * G + 2 * jj : 16 + 4 * G + 2 * jj - 4;
+          va[jj] = (uint32_t)s_v[wv][r0][d] | ((uint32_t)s_v[wv][r0 + 1][d] << 16);
+        }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[r][j] = fmaf(pr, vf[j], o[r][j]);
+        for (int part = 0; part < 3; ++part) oacc[t] = A::mfma16(va, pb[part], oacc[t]);
       }
+      wave_lds_sync();
     }
-    wave_lds_sync();
   }
 
-  // sum the lane groups' outputs and the lane shares of the row sums
-#pragma unroll
-  for (int x = LPD; x < 64; x <<= 1)
-#pragma unroll
-    for (int r = 0; r < RP; ++r)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) o[r][j] += __shfl_xor(o[r][j], x);
+  // the lane shares of the row sums; the outputs are whole in oacc
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
-  if (lane < LPD) {
+  __syncthreads();  // every wavefront is past its last use of s_v
+  if (c16 < RP) {
 #pragma unroll
-    for (int r = 0; r < RP; ++r)
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) s_o[wv][r][dd + j] = o[r][j];
+      for (int i = 0; i < 4; ++i) s_o[wv][c16][16 * t + 4 * G + i] = oacc[t][i];
   }
   if (G == 0 && c16 < RP) {
     s_m[wv][c16] = m_run;
