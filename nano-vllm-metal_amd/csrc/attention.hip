@@ -46,7 +46,7 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kTile = 64;           // context positions per wavefront step
-constexpr int kTargetBlocks = 512;  // decode: split the context until about this many blocks
+constexpr int kTargetBlocks = 256;  // decode: split the context until about this many blocks
 constexpr int kMaxRowDim = 256;     // head dim of the row kernel (4 values per lane)
 constexpr int kMaxSplits = 64;      // context splits of a decode row
 
