@@ -13,8 +13,9 @@ per-kernel durations come from HIP events around each stage in an eager pass.
 Also reported: decode batches 1/8/64, prefill of 4096 tokens with uniform and
 Zipf(1.1) routing (MFMA roofline), the Qwen3-235B-A22B-shaped MoE layer
 (decode 32, prefill 2048), the dense W4A16 projections of the same
-model through quantized_matmul (q/k/o and the lm head, 1/32/4096 rows), and
-the CPU baseline (the C restatement of the reference algorithm in oracle/,
+model through quantized_matmul (q/k/o and the lm head, 1/32/4096 rows), paged
+decode attention, the full 48-layer model through LLM.generate (32 x 1024-token
+prompts, 256 greedy tokens: end-to-end decode tokens/s), and the CPU baseline (the C restatement of the reference algorithm in oracle/,
 timed on a bounded sample).
 
 Prints one JSON line on stdout; progress goes to stderr.
@@ -735,6 +736,9 @@ def main():
         out["dense"] = dense_bench(dev)
         log("[bench] paged decode attention")
         out["attention"] = attention_bench(dev)
+        out["e2e"] = e2e_bench(dev)
+        log(f"[bench] e2e: decode {out['e2e']['decode_tokens_per_s']:.0f} tok/s, "
+            f"prefill {out['e2e']['prefill_tokens_per_s']:.0f} tok/s")
         u = out["prefill"]["uniform"]
         out["prefill_roofline"] = {
             "kernel": "gemm_kernel<bf16, gate/up+SwiGLU> (nvm_moe_expert_gateup, prefill)",

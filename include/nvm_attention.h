@@ -37,7 +37,9 @@ enum nvm_kv_dtype { NVM_KV_F16 = 0, NVM_KV_BF16 = 1, NVM_KV_F32 = 2, NVM_KV_I8 =
  *   value_scales [P, num_kv_heads, page_size] float32 (NVM_KV_I8), else NULL
  *   block_table  [B, max_pages] int32: page of each logical page of a request
  *   context_lens [B] int32
- *   out          [N, L, D] float32
+ *   out          [N, L, D] of out_dtype: NVM_KV_F32 (the reference op's
+ *                output), or NVM_KV_BF16 / NVM_KV_F16, the float32 result
+ *                rounded once (the model's cast back to its activations)
  *
  * Key position j of request b (j < min(context_lens[b], max_pages *
  * page_size)) lives in page block_table[b, j / page_size], slot j % page_size.
@@ -60,8 +62,8 @@ int nvm_paged_attention(const float *q, int64_t N, int64_t L, int64_t D, const v
                         const float *key_scales, const float *value_scales,
                         const int32_t *block_table, int64_t B, int64_t max_pages,
                         const int32_t *context_lens, float scale, int is_causal,
-                        int num_kv_heads, int num_heads, float *out, void *workspace,
-                        size_t workspace_bytes, nvm_stream_t stream);
+                        int num_kv_heads, int num_heads, int out_dtype, void *out,
+                        void *workspace, size_t workspace_bytes, nvm_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -55,10 +55,23 @@ struct PagedArgs {
   const void *kp, *vp;
   const float *ks, *vs;
   const int32_t *bt, *lens;
-  float *out, *part_o, *part_ml;
+  void *out;
+  float *part_o, *part_ml;
+  int out_dt;  // NVM_KV_F32, NVM_KV_BF16 or NVM_KV_F16
   int P, L, D, page_size, max_pages, Hkv, Hq, R, HG, S, span, causal;
   float scale2;  // scale * log2(e): scores are kept in base 2
 };
+
+// Output element i: float32, or rounded to bf16/f16 (the model's
+// `.astype(x.dtype)` after the op, models/qwen3.py:150-161).
+__device__ __forceinline__ void store_out(void *out, int dt, int64_t i, float v) {
+  if (dt == NVM_KV_F32)
+    ((float *)out)[i] = v;
+  else if (dt == NVM_KV_BF16)
+    ((uint16_t *)out)[i] = Act<DT_BF16>::from_f32(v);
+  else
+    ((uint16_t *)out)[i] = Act<DT_F16>::from_f32(v);
+}
 
 // Hand-over of LDS data between the lanes of one wavefront: its LDS
 // operations execute in program order, so only the compiler must not move
@@ -305,7 +318,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
     }
     const int64_t n = n0 + r;
     if (a.S == 1) {
-      a.out[n * DH + d] = Ls > 0.f ? Os / Ls : 0.f;
+      store_out(a.out, a.out_dt, n * DH + d, Ls > 0.f ? Os / Ls : 0.f);
     } else {
       a.part_o[(n * a.S + s) * DH + d] = Os;
       if (d == 0) {
@@ -322,8 +335,8 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
 // in flight at a time.
 __global__ __launch_bounds__(256) void paged_combine_kernel(const float *__restrict__ part_o,
                                                             const float *__restrict__ part_ml,
-                                                            int S, int D,
-                                                            float *__restrict__ out) {
+                                                            int S, int D, void *out,
+                                                            int out_dt) {
   __shared__ float s_w[kMaxSplits];
   __shared__ float s_inv;
   const int64_t n = blockIdx.x;
@@ -357,7 +370,7 @@ __global__ __launch_bounds__(256) void paged_combine_kernel(const float *__restr
     }
     for (; s < S; ++s) acc[0] += s_w[s] * po[(int64_t)s * D];
     const float o = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
-    out[n * D + d] = o * s_inv;
+    store_out(out, out_dt, n * D + d, o * s_inv);
   }
 }
 
@@ -431,7 +444,7 @@ __global__ __launch_bounds__(256) void paged_rows_kernel(PagedArgs a, int64_t ro
 #pragma unroll
   for (int k = 0; k < KD; ++k) {
     const int d = lane + 64 * k;
-    if (d < a.D) a.out[row * a.D + d] = l > 0.f ? ov[k] / l : 0.f;
+    if (d < a.D) store_out(a.out, a.out_dt, row * a.D + d, l > 0.f ? ov[k] / l : 0.f);
   }
 }
 
@@ -529,11 +542,14 @@ int nvm_paged_attention(const float *q, int64_t N, int64_t L, int64_t D, const v
                         const float *key_scales, const float *value_scales,
                         const int32_t *block_table, int64_t B, int64_t max_pages,
                         const int32_t *context_lens, float scale, int is_causal,
-                        int num_kv_heads, int num_heads, float *out, void *workspace,
+                        int num_kv_heads, int num_heads, int out_dtype, void *out,
+                        void *workspace,
                         size_t workspace_bytes, nvm_stream_t stream) {
   using namespace nvm;
   if (int r = check_attention(N, L, D, max_pages, page_size, kv_dtype, num_kv_heads, num_heads))
     return r;
+  ATTN_REQUIRE(out_dtype == NVM_KV_F32 || out_dtype == NVM_KV_BF16 || out_dtype == NVM_KV_F16,
+               "paged_attention: out dtype must be f32, bf16 or f16");
   ATTN_REQUIRE(B >= 0 && N / num_heads == B,
                "paged_attention: q batch size must match block_table batch size");
   ATTN_REQUIRE(P >= 0 && P <= 0x7FFFFFFFll, "paged_attention: bad page count %lld", (long long)P);
@@ -564,6 +580,7 @@ int nvm_paged_attention(const float *q, int64_t N, int64_t L, int64_t D, const v
   a.bt = block_table;
   a.lens = context_lens;
   a.out = out;
+  a.out_dt = out_dtype;
   a.P = (int)P;
   a.L = (int)L;
   a.D = (int)D;
@@ -595,7 +612,7 @@ int nvm_paged_attention(const float *q, int64_t N, int64_t L, int64_t D, const v
     if (e != hipSuccess) return set_error(NVM_ERR_HIP, "paged_attention: %s", hipGetErrorString(e));
     if (plan.S > 1) {
       hipLaunchKernelGGL(paged_combine_kernel, dim3((unsigned)N), dim3(256), 0, st, a.part_o,
-                         a.part_ml, plan.S, (int)D, out);
+                         a.part_ml, plan.S, (int)D, out, out_dtype);
       e = hipGetLastError();
       if (e != hipSuccess)
         return set_error(NVM_ERR_HIP, "paged_attention combine: %s", hipGetErrorString(e));

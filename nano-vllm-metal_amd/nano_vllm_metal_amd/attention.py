@@ -20,7 +20,8 @@ def paged_attention(query: torch.Tensor, key_pages: torch.Tensor, value_pages: t
                     block_table: torch.Tensor, context_lens: torch.Tensor, page_size: int,
                     key_scales: torch.Tensor | None = None,
                     value_scales: torch.Tensor | None = None, scale: float | None = None,
-                    mask: str | None = None) -> torch.Tensor:
+                    mask: str | None = None, out_dtype: torch.dtype = torch.float32
+                    ) -> torch.Tensor:
     """``softmax(query . paged_key^T * scale) . paged_value``.
 
     ``query [B, num_heads, L, D]``; ``key_pages``/``value_pages``
@@ -29,7 +30,8 @@ def paged_attention(query: torch.Tensor, key_pages: torch.Tensor, value_pages: t
     ``block_table [B, max_pages]`` physical page ids (negative: no page);
     ``context_lens [B]``.  ``mask`` is None or ``"causal"`` (query row i of L
     sees key positions j <= i + context_len - L).  Returns float32
-    ``[B, num_heads, L, D]``.
+    ``[B, num_heads, L, D]`` (or, with ``out_dtype`` bf16/f16, that result
+    rounded once, as the model's cast after the op).
     """
     if isinstance(mask, torch.Tensor):
         raise NotImplementedError("Paged attention only supports mask=None or causal")
@@ -66,7 +68,9 @@ def paged_attention(query: torch.Tensor, key_pages: torch.Tensor, value_pages: t
             raise ValueError("paged_attention: int8 pages need key_scales and value_scales")
         ks = key_scales.to(torch.float32).reshape(P, Hkv, ps).contiguous()
         vs = value_scales.to(torch.float32).reshape(P, Hkv, ps).contiguous()
-    out = torch.empty((B * Hq, L, D), dtype=torch.float32, device=dev)
+    if out_dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise ValueError(f"paged_attention: unsupported out_dtype {out_dtype}")
+    out = torch.empty((B * Hq, L, D), dtype=out_dtype, device=dev)
     kv = _lib.KV_DTYPE_CODES[key_pages.dtype]
     size = ctypes.c_size_t(0)
     _lib.check(lib.nvm_paged_attention_workspace_size(B * Hq, L, D, bt.shape[1], page_size, kv,
@@ -75,6 +79,7 @@ def paged_attention(query: torch.Tensor, key_pages: torch.Tensor, value_pages: t
     _lib.check(lib.nvm_paged_attention(
         q.data_ptr(), B * Hq, L, D, kp.data_ptr(), vp.data_ptr(), P, page_size, kv,
         _lib.ptr(ks), _lib.ptr(vs), bt.data_ptr(), B, bt.shape[1], lens.data_ptr(),
-        float(factor), int(mask == "causal"), Hkv, Hq, out.data_ptr(), ws.data_ptr(),
+        float(factor), int(mask == "causal"), Hkv, Hq, _lib.KV_DTYPE_CODES[out_dtype],
+        out.data_ptr(), ws.data_ptr(),
         size.value, _lib.stream_of(dev)))
     return out.reshape(B, Hq, L, D)

@@ -189,7 +189,8 @@ class Qwen3Model:
             o = F.scaled_dot_product_attention(q, kf, vf, is_causal=True, scale=scale)
         else:
             o = paged_attention(q, cache.key_pages[li], cache.value_pages[li], step.block_table,
-                                step.lens, cache.page_size, scale=scale, mask="causal")
+                                step.lens, cache.page_size, scale=scale, mask="causal",
+                                out_dtype=x.dtype)
         o = o.to(x.dtype).transpose(1, 2).reshape(B, L, Hq * D)
         return quantized_linear(o, layer.wo)
 

@@ -187,12 +187,13 @@ def test_torch_quantizer_agrees_with_oracle(act, gs):
 
 def _attn(lib, **kw):
     a = dict(q=1, N=64, L=1, D=128, kp=1, vp=1, P=8, ps=16, kv=1, ks=None, vs=None, bt=1, B=2,
-             mp=4, lens=1, scale=0.1, causal=0, hkv=4, hq=32, out=1, ws=1, ws_bytes=1 << 40)
+             mp=4, lens=1, scale=0.1, causal=0, hkv=4, hq=32, odt=2, out=1, ws=1,
+             ws_bytes=1 << 40)
     a.update(kw)
     return lib.nvm_paged_attention(a["q"], a["N"], a["L"], a["D"], a["kp"], a["vp"], a["P"],
                                    a["ps"], a["kv"], a["ks"], a["vs"], a["bt"], a["B"], a["mp"],
                                    a["lens"], a["scale"], a["causal"], a["hkv"], a["hq"],
-                                   a["out"], a["ws"], a["ws_bytes"], None)
+                                   a["odt"], a["out"], a["ws"], a["ws_bytes"], None)
 
 
 @pytest.mark.parametrize("kw,code,msg", [
@@ -205,6 +206,7 @@ def _attn(lib, **kw):
     ({"q": None}, -1, "null pointer"),
     ({"ws": None, "mp": 80}, -3, "workspace"),
     ({"P": 1 << 20, "ps": 64}, -2, "2 GiB"),
+    ({"odt": 3}, -1, "out dtype"),
 ])
 def test_paged_attention_validation(kw, code, msg):
     """Argument checks of nvm_paged_attention (the reference's paged_attention

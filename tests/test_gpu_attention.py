@@ -171,3 +171,22 @@ def test_graph_replay_matches_eager():
         eager2 = paged_attention(q, kp, vp, bt, lens, ps)
         torch.cuda.synchronize()
         assert torch.equal(eager2, eager)
+
+
+@pytest.mark.parametrize("odt", [torch.bfloat16, torch.float16])
+def test_output_in_activation_dtype(odt):
+    """out_dtype bf16/f16 is the float32 result rounded once (decode kernel
+    with and without a split, and the row kernel)."""
+    from nano_vllm_metal_amd import paged_attention
+
+    g = torch.Generator(device=DEV).manual_seed(3)
+    for B, L, ctx in ((32, 1, 1200), (64, 1, 2048), (2, 3, 90)):
+        mp = -(-ctx // 16)
+        q = torch.randn(B, 32, L, 128, device=DEV, generator=g)
+        kp = torch.randn(B * mp, 4, 16, 128, device=DEV, generator=g).to(torch.bfloat16)
+        vp = torch.randn(B * mp, 4, 16, 128, device=DEV, generator=g).to(torch.bfloat16)
+        bt = torch.randperm(B * mp, device=DEV, generator=g).to(torch.int32).reshape(B, mp)
+        lens = torch.full((B,), ctx, dtype=torch.int32, device=DEV)
+        f = paged_attention(q, kp, vp, bt, lens, 16, mask="causal")
+        h = paged_attention(q, kp, vp, bt, lens, 16, mask="causal", out_dtype=odt)
+        assert h.dtype == odt and torch.equal(h, f.to(odt)), (B, L, ctx)
