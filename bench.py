@@ -730,15 +730,23 @@ def main():
                 f"{r['layer_tflops']:.0f} TFLOP/s, kernels {r['kernel_us']}")
             if zipf:
                 del lay
-        log("[bench] 235B-A22B-shaped MoE layer")
-        out["moe_235b"] = shape_235b_bench(dev, args.steps)
-        log("[bench] dense W4A16 projections")
-        out["dense"] = dense_bench(dev)
-        log("[bench] paged decode attention")
-        out["attention"] = attention_bench(dev)
-        out["e2e"] = e2e_bench(dev)
-        log(f"[bench] e2e: decode {out['e2e']['decode_tokens_per_s']:.0f} tok/s, "
-            f"prefill {out['e2e']['prefill_tokens_per_s']:.0f} tok/s")
+        # the other reported workloads: a failure in one is recorded in its
+        # field and does not take the headline line down with it
+        extras = (("moe_235b", "235B-A22B-shaped MoE layer", lambda: shape_235b_bench(dev, args.steps)),
+                  ("dense", "dense W4A16 projections", lambda: dense_bench(dev)),
+                  ("attention", "paged decode attention", lambda: attention_bench(dev)),
+                  ("e2e", "48-layer model through LLM.generate", lambda: e2e_bench(dev)))
+        for key, what, fn in extras:
+            log(f"[bench] {what}")
+            try:
+                out[key] = fn()
+            except Exception as e:  # noqa: BLE001 - reported in the JSON line
+                log(f"[bench] {what} failed: {e!r}")
+                out[key] = {"error": repr(e)}
+                torch.cuda.synchronize()
+        if "decode_tokens_per_s" in out["e2e"]:
+            log(f"[bench] e2e: decode {out['e2e']['decode_tokens_per_s']:.0f} tok/s, "
+                f"prefill {out['e2e']['prefill_tokens_per_s']:.0f} tok/s")
         u = out["prefill"]["uniform"]
         out["prefill_roofline"] = {
             "kernel": "gemm_kernel<bf16, gate/up+SwiGLU> (nvm_moe_expert_gateup, prefill)",
