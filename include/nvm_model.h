@@ -52,6 +52,26 @@ int nvm_qk_norm_rope_store(const void *qkv, int64_t T, int Hq, int Hkv, int64_t 
                            int dtype, float *q_out, float *k_out, float *v_out,
                            nvm_stream_t stream);
 
+/*
+ * The MoE block with its combine fused into the residual add and RMSNorm
+ * that follow it in the model (models/qwen3.py:249-252 around
+ * layers/moe.py:69-86): the stages of nvm_moe_forward, then per token
+ * y = rnd(sum_j rnd(down_j * score_j)) in slot order (bit-identical to
+ * nvm_moe_forward's y), h_out = rnd(h + y), x_out = rnd(rms_norm(h_out) * w).
+ * Arguments as nvm_moe_forward, with h [T, H], norm_w [H], eps, h_out and
+ * x_out [T, H] in place of y / ids_out / scores_out (16-byte aligned).  H a
+ * multiple of 8, at most 8192.  Workspace: nvm_moe_workspace_size.
+ */
+int nvm_moe_forward_residual_norm(const void *x, int64_t T, int64_t H, int64_t I, int64_t E,
+                                  int top_k, int norm_topk_prob, int group_size, int bits,
+                                  int dtype, const uint32_t *wr, const void *sr, const void *br,
+                                  const uint32_t *wg, const void *sg, const void *bg,
+                                  const uint32_t *wu, const void *su, const void *bu,
+                                  const uint32_t *wd, const void *sd, const void *bd,
+                                  const void *h, const void *norm_w, float eps, void *h_out,
+                                  void *x_out, int regime, void *workspace,
+                                  size_t workspace_bytes, nvm_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

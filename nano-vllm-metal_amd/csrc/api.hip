@@ -6,6 +6,7 @@
 #include <string>
 
 #include "internal.h"
+#include "nvm_model.h"
 #include "nvm_moe.h"
 
 namespace {
@@ -179,6 +180,17 @@ int run_products(int dtype, bool decode, bool dual, nvm::GroupedArgs &g, int64_t
   }
   return NVM_OK;
 }
+
+// Routing, dispatch and both expert products of the block (everything but
+// the combine), on the caller's workspace; `scores` is where the routing
+// scores went.
+int moe_stages(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int top_k,
+               int norm_topk_prob, int group_size, int bits, int dtype, const uint32_t *wr,
+               const void *sr, const void *br, const uint32_t *wg, const void *sg,
+               const void *bg, const uint32_t *wu, const void *su, const void *bu,
+               const uint32_t *wd, const void *sd, const void *bd, int32_t *ids_out,
+               void *scores_out, int regime, void *workspace, size_t workspace_bytes,
+               nvm_stream_t stream, MoeWs &ws, uint16_t *&scores);
 
 }  // namespace
 
@@ -474,20 +486,69 @@ int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, i
                     const uint32_t *wd, const void *sd, const void *bd, void *y, int32_t *ids_out,
                     void *scores_out, int regime, void *workspace, size_t workspace_bytes,
                     nvm_stream_t stream) {
+  NVM_REQUIRE(y || T == 0, "moe: null pointer");
+  MoeWs ws{};
+  uint16_t *scores = nullptr;
+  if (int r = moe_stages(x, T, H, I, E, top_k, norm_topk_prob, group_size, bits, dtype, wr, sr,
+                         br, wg, sg, bg, wu, su, bu, wd, sd, bd, ids_out, scores_out, regime,
+                         workspace, workspace_bytes, stream, ws, scores))
+    return r;
+  if (T == 0) return NVM_OK;
+  return nvm_moe_combine(ws.down, scores, T, top_k, H, dtype, y, stream);
+}
+
+int nvm_moe_forward_residual_norm(const void *x, int64_t T, int64_t H, int64_t I, int64_t E,
+                                  int top_k, int norm_topk_prob, int group_size, int bits,
+                                  int dtype, const uint32_t *wr, const void *sr, const void *br,
+                                  const uint32_t *wg, const void *sg, const void *bg,
+                                  const uint32_t *wu, const void *su, const void *bu,
+                                  const uint32_t *wd, const void *sd, const void *bd,
+                                  const void *h, const void *norm_w, float eps, void *h_out,
+                                  void *x_out, int regime, void *workspace,
+                                  size_t workspace_bytes, nvm_stream_t stream) {
+  NVM_SUPPORTED(nvm::combine_residual_norm_supports(H),
+                "moe_residual_norm: hidden %lld must be a multiple of 8, at most 8192",
+                (long long)H);
+  NVM_REQUIRE(T == 0 || (h && norm_w && h_out && x_out), "moe_residual_norm: null pointer");
+  // the fused kernel moves rows in 16-byte pieces
+  NVM_REQUIRE(((uintptr_t)h | (uintptr_t)norm_w | (uintptr_t)h_out | (uintptr_t)x_out) % 16 == 0,
+              "moe_residual_norm: h, norm_w, h_out and x_out must be 16-byte aligned");
+  MoeWs ws{};
+  uint16_t *scores = nullptr;
+  if (int r = moe_stages(x, T, H, I, E, top_k, norm_topk_prob, group_size, bits, dtype, wr, sr,
+                         br, wg, sg, bg, wu, su, bu, wd, sd, bd, nullptr, nullptr, regime,
+                         workspace, workspace_bytes, stream, ws, scores))
+    return r;
+  if (T == 0) return NVM_OK;
+  NVM_TRY_HIP(nvm::launch_combine_residual_norm(dtype, ws.down, scores, T, top_k, H, h, norm_w,
+                                                eps, h_out, x_out, (hipStream_t)stream));
+  return NVM_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+int moe_stages(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int top_k,
+               int norm_topk_prob, int group_size, int bits, int dtype, const uint32_t *wr,
+               const void *sr, const void *br, const uint32_t *wg, const void *sg,
+               const void *bg, const uint32_t *wu, const void *su, const void *bu,
+               const uint32_t *wd, const void *sd, const void *bd, int32_t *ids_out,
+               void *scores_out, int regime, void *workspace, size_t workspace_bytes,
+               nvm_stream_t stream, MoeWs &ws, uint16_t *&scores) {
   if (int r = check_products(H, I, E, top_k, group_size, bits, dtype, regime)) return r;
   NVM_REQUIRE(T >= 0, "moe: bad shape");
-  NVM_REQUIRE(x && y && wr && sr && br && wg && sg && bg && wu && su && bu && wd && sd && bd,
+  NVM_REQUIRE(x && wr && sr && br && wg && sg && bg && wu && su && bu && wd && sd && bd,
               "moe: null pointer");
   if (T == 0) return NVM_OK;
   const size_t need = carve_moe(nullptr, T, H, I, E, top_k).bytes;
   if (!workspace || workspace_bytes < need)
     return fail(NVM_ERR_WORKSPACE, "moe: workspace of %zu bytes needed", need);
-  MoeWs ws = carve_moe(workspace, T, H, I, E, top_k);
+  ws = carve_moe(workspace, T, H, I, E, top_k);
   int32_t *ids = ids_out ? ids_out : ws.ids;
-  uint16_t *scores = scores_out ? (uint16_t *)scores_out : ws.scores;
+  scores = scores_out ? (uint16_t *)scores_out : ws.scores;
   const int64_t N = T * top_k;
   hipStream_t st = (hipStream_t)stream;
-
   if (int r = run_route_dispatch(dtype, x, T, H, wr, sr, br, E, group_size, top_k, norm_topk_prob,
                                  nullptr, ids, scores, ws.offsets, ws.sorted, ws.partial,
                                  ws.counts, ws.done, st))
@@ -495,10 +556,8 @@ int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, i
   if (int r = nvm_moe_expert_gateup(x, T, H, I, E, top_k, group_size, bits, dtype, wg, sg, bg,
                                     wu, su, bu, ws.offsets, ws.sorted, ws.h, regime, stream))
     return r;
-  if (int r = nvm_moe_expert_down(ws.h, N, H, I, E, group_size, bits, dtype, wd, sd, bd,
-                                  ws.offsets, ws.sorted, ws.down, regime, stream))
-    return r;
-  return nvm_moe_combine(ws.down, scores, T, top_k, H, dtype, y, stream);
+  return nvm_moe_expert_down(ws.h, N, H, I, E, group_size, bits, dtype, wd, sd, bd, ws.offsets,
+                             ws.sorted, ws.down, regime, stream);
 }
 
-}  // extern "C"
+}  // namespace

@@ -76,6 +76,14 @@ constexpr int kGemmBN = 128;   // prefill tile columns per weight matrix
 hipError_t launch_gemm(int dtype, bool dual, const GroupedArgs &a, int64_t max_m_tiles,
                        hipStream_t st);
 
+// Combine fused with the residual add and RMSNorm that follow the MoE block
+// in the model (rows of H <= 8192, a multiple of 8).
+hipError_t launch_combine_residual_norm(int dtype, const void *down, const void *scores,
+                                        int64_t T, int k, int64_t H, const void *h,
+                                        const void *w, float eps, void *h_out, void *x_out,
+                                        hipStream_t st);
+bool combine_residual_norm_supports(int64_t H);
+
 // Combine: y[t] = rnd(sum_j rnd(down[t*k+j] * score[t,j])).
 hipError_t launch_combine(int dtype, const void *down, const void *scores, int64_t T, int k,
                           int64_t H, void *y, hipStream_t st);

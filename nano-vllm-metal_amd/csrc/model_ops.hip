@@ -73,6 +73,83 @@ __global__ __launch_bounds__(kNormThreads) void residual_rms_norm_kernel(
   }
 }
 
+// MoE combine + residual add + RMSNorm, one block per token: the token's k
+// expert outputs summed in slot order exactly as the combine kernel does
+// (y = rnd(sum_j rnd(down_j * score_j))), then h_out = rnd(h + y) and
+// x_out = rnd(rms_norm(h_out) * w).  Eight pairs' loads are in flight at once.
+constexpr int kCombChunks = 4;  // 8-value chunks per thread: H <= 256 * 4 * 8
+
+template <int DT>
+__global__ __launch_bounds__(kNormThreads) void moe_combine_residual_norm_kernel(
+    const uint16_t *__restrict__ down, const uint16_t *__restrict__ scores, int k, int H8,
+    const uint16_t *__restrict__ h, const uint16_t *__restrict__ w, float eps,
+    uint16_t *__restrict__ h_out, uint16_t *__restrict__ x_out) {
+  using A = Act<DT>;
+  __shared__ float s_part[kNormThreads / 64];
+  const int64_t t = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t H = (int64_t)H8 * 8;
+  float hv[kCombChunks][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < kCombChunks; ++q) {
+    const int c = tid + kNormThreads * q;
+    if (c >= H8) continue;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < k; j0 += 8) {
+      u32x4 v[8];
+      uint32_t sv[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        v[jj] = u32x4{0u, 0u, 0u, 0u};
+        sv[jj] = 0u;
+        if (j0 + jj < k) {
+          v[jj] = ldg16(down + ((t * k + j0 + jj) * H + 8 * c));
+          sv[jj] = scores[t * k + j0 + jj];
+        }
+      }
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        if (j0 + jj >= k) break;
+        const float sc = A::to_f32(sv[jj]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[2 * i] += round_act<DT>(A::lo(v[jj][i]) * sc);
+          acc[2 * i + 1] += round_act<DT>(A::hi(v[jj][i]) * sc);
+        }
+      }
+    }
+    const u32x4 hh = ldg16(h + t * H + 8 * c);
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t y = A::pack2(acc[2 * i], acc[2 * i + 1]);
+      o[i] = A::pack2(A::lo(hh[i]) + A::lo(y), A::hi(hh[i]) + A::hi(y));
+      hv[q][2 * i] = A::lo(o[i]);
+      hv[q][2 * i + 1] = A::hi(o[i]);
+      ss = fmaf(hv[q][2 * i], hv[q][2 * i], fmaf(hv[q][2 * i + 1], hv[q][2 * i + 1], ss));
+    }
+    *(u32x4 *)(h_out + t * H + 8 * c) = o;
+  }
+#pragma unroll
+  for (int x = 32; x > 0; x >>= 1) ss += __shfl_xor(ss, x);
+  if ((tid & 63) == 0) s_part[tid >> 6] = ss;
+  __syncthreads();
+  const float tot = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+  const float inv = rsqrtf(tot / (float)H + eps);
+#pragma unroll
+  for (int q = 0; q < kCombChunks; ++q) {
+    const int c = tid + kNormThreads * q;
+    if (c >= H8) continue;
+    const u32x4 wv = ldg16(w + 8 * c);
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[i] = A::pack2(hv[q][2 * i] * inv * A::lo(wv[i]), hv[q][2 * i + 1] * inv * A::hi(wv[i]));
+    *(u32x4 *)(x_out + t * H + 8 * c) = o;
+  }
+}
+
 struct QkvArgs {
   const uint32_t *qkv;
   const uint32_t *qw, *kw;
@@ -163,6 +240,26 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(QkvArgs a) {
 }
 
 }  // namespace
+
+hipError_t launch_combine_residual_norm(int dtype, const void *down, const void *scores,
+                                        int64_t T, int k, int64_t H, const void *h,
+                                        const void *w, float eps, void *h_out, void *x_out,
+                                        hipStream_t st) {
+  if (T == 0) return hipSuccess;
+  if (dtype == DT_BF16)
+    hipLaunchKernelGGL(moe_combine_residual_norm_kernel<DT_BF16>, dim3((unsigned)T),
+                       dim3(kNormThreads), 0, st, (const uint16_t *)down, (const uint16_t *)scores,
+                       k, (int)(H / 8), (const uint16_t *)h, (const uint16_t *)w, eps,
+                       (uint16_t *)h_out, (uint16_t *)x_out);
+  else
+    hipLaunchKernelGGL(moe_combine_residual_norm_kernel<DT_F16>, dim3((unsigned)T),
+                       dim3(kNormThreads), 0, st, (const uint16_t *)down, (const uint16_t *)scores,
+                       k, (int)(H / 8), (const uint16_t *)h, (const uint16_t *)w, eps,
+                       (uint16_t *)h_out, (uint16_t *)x_out);
+  return hipGetLastError();
+}
+
+bool combine_residual_norm_supports(int64_t H) { return H % 8 == 0 && H <= 8 * kNormThreads * kCombChunks; }
 
 }  // namespace nvm
 

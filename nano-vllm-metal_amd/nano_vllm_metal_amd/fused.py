@@ -63,3 +63,35 @@ def qk_norm_rope_store(qkv: torch.Tensor, num_heads: int, num_kv_heads: int, hea
         value_pages.data_ptr(), key_pages.shape[0], key_pages.shape[2],
         _lib.dtype_code(qkv.dtype), q.data_ptr(), _lib.ptr(k), _lib.ptr(v), _lib.stream_of(dev)))
     return q, k, v
+
+
+def moe_residual_rms_norm(moe, x: torch.Tensor, h: torch.Tensor, weight: torch.Tensor,
+                          eps: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The ``Moe`` block on ``x`` with its combine fused into the residual add
+    and RMSNorm that follow it: ``(h + moe(x), rms_norm(h + moe(x)) * weight)``,
+    where ``moe(x)`` is bit-identical to ``moe.forward(x)``."""
+    from .moe import REGIMES, Moe
+
+    if not isinstance(moe, Moe):
+        raise TypeError("moe_residual_rms_norm: a Moe block is required")
+    lib = _lib.load()
+    dev = _lib.require_device(x, h, weight, moe.w_router.weight)
+    *lead, H = x.shape
+    x2 = x.reshape(-1, H).contiguous()
+    h2 = h.reshape(-1, H).contiguous()
+    T = x2.shape[0]
+    E = moe.w_router.weight.shape[0]
+    I = moe.w_gate.weight.shape[1]
+    ws = moe._workspace(T, H, I, E, dev)
+    (wr, sr, br), (wg, sg, bg), (wu, su, bu), (wd, sd, bd) = moe._operands()
+    w = weight.to(x.dtype).contiguous()
+    h_out = torch.empty_like(h2)
+    x_out = torch.empty_like(x2)
+    _lib.check(lib.nvm_moe_forward_residual_norm(
+        x2.data_ptr(), T, H, I, E, moe.num_experts_per_tok, int(bool(moe.norm_topk_prob)),
+        moe.w_gate.group_size, moe.w_gate.bits, _lib.dtype_code(x.dtype),
+        wr.data_ptr(), sr.data_ptr(), br.data_ptr(), wg.data_ptr(), sg.data_ptr(), bg.data_ptr(),
+        wu.data_ptr(), su.data_ptr(), bu.data_ptr(), wd.data_ptr(), sd.data_ptr(), bd.data_ptr(),
+        h2.data_ptr(), w.data_ptr(), float(eps), h_out.data_ptr(), x_out.data_ptr(),
+        REGIMES[moe.regime], ws.data_ptr(), ws.numel(), _lib.stream_of(dev)))
+    return h_out.reshape(h.shape), x_out.reshape(x.shape)

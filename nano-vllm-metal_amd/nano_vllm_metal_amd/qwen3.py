@@ -33,7 +33,7 @@ import torch
 import torch.nn.functional as F
 
 from .attention import paged_attention
-from .fused import qk_norm_rope_store, residual_rms_norm
+from .fused import moe_residual_rms_norm, qk_norm_rope_store, residual_rms_norm
 from .kv_cache import PagedKVCache
 from .linear import QuantizedWeights, dequantize, quantized_linear
 from .moe import Moe
@@ -223,7 +223,11 @@ class Qwen3Model:
             h, x = residual_rms_norm(h, self._attention(li, layer, x, step, cache),
                                      layer.post_norm, eps)
             nxt = self.layers[li + 1].input_norm if li + 1 < n else self.norm
-            h, x = residual_rms_norm(h, layer.mlp(x), nxt, eps)
+            if isinstance(layer.mlp, Moe):
+                # the MoE combine fused into this residual add and norm
+                h, x = moe_residual_rms_norm(layer.mlp, x, h, nxt, eps)
+            else:
+                h, x = residual_rms_norm(h, layer.mlp(x), nxt, eps)
         if last_only:
             x = x[:, -1]
         return quantized_linear(x, self.lm_head if self.lm_head is not None else self.embed_w)

@@ -238,6 +238,15 @@ def test_paged_attention_workspace_size():
                                             8, 16, 1, 1, None, None, None), -2, "multiple of 4"),
     (lambda lib: lib.nvm_qk_norm_rope_store(1, 4, 32, 4, 128, 1, 1, 1e-6, 1, 1, 1, 100, 1, 1, 1, 1,
                                             8, 16, 1, None, None, None, None), -1, "null"),
+    (lambda lib: lib.nvm_moe_forward_residual_norm(1, 4, 2052, 768, 128, 8, 1, 64, 4, 1,
+                                                   *([1] * 12), 1, 1, 1e-6, 1, 1, 0, 1, 1 << 40,
+                                                   None), -2, "multiple of 8"),
+    (lambda lib: lib.nvm_moe_forward_residual_norm(1, 4, 2048, 768, 128, 8, 1, 64, 4, 1,
+                                                   *([1] * 12), None, 1, 1e-6, 1, 1, 0, 1,
+                                                   1 << 40, None), -1, "null pointer"),
+    (lambda lib: lib.nvm_moe_forward_residual_norm(1, 4, 2048, 768, 128, 8, 1, 64, 4, 1,
+                                                   *([1] * 12), 24, 16, 1e-6, 16, 16, 0, 1,
+                                                   1 << 40, None), -1, "16-byte aligned"),
 ])
 def test_model_ops_validation(call, code, msg):
     """nvm_residual_rms_norm / nvm_qk_norm_rope_store reject bad arguments

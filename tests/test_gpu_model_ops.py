@@ -85,3 +85,27 @@ def test_qk_norm_rope_store(Hq, Hkv, D, dt):
         if t != 4:
             written[int(page_ids[t]), int(slots[t])] = True
     assert not kp.permute(0, 2, 1, 3)[~written].any()
+
+
+@pytest.mark.parametrize("T,dt", [(32, torch.bfloat16), (300, torch.float16)])
+def test_moe_combine_residual_norm(T, dt):
+    """nvm_moe_forward_residual_norm: h_out is bit-identical to h + Moe(x)
+    (the combine's arithmetic, then one rounding), x_out the norm of it."""
+    from nano_vllm_metal_amd import Moe, QuantizedWeights, quantize
+    from nano_vllm_metal_amd.fused import moe_residual_rms_norm, residual_rms_norm
+
+    H, E, I, k = 512, 16, 128, 4
+    g = torch.Generator(device=DEV).manual_seed(T)
+
+    def qw(*shape, std=0.05):
+        wq, s, b = quantize((torch.randn(shape, generator=g, device=DEV) * std).to(dt), 64, 4)
+        return QuantizedWeights(s, b, 64, 4, wq)
+
+    moe = Moe(qw(E, H, std=0.3), qw(E, I, H), qw(E, I, H), qw(E, H, I), k, True)
+    x = torch.randn(T, H, device=DEV, generator=g).to(dt)
+    h = (torch.randn(T, H, device=DEV, generator=g) * 2).to(dt)
+    w = (1 + 0.1 * torch.randn(H, device=DEV, generator=g)).to(dt)
+    h_ref, x_ref = residual_rms_norm(h, moe(x), w, 1e-6)
+    h2, x2 = moe_residual_rms_norm(moe, x, h, w, 1e-6)
+    assert torch.equal(h2, h_ref)
+    _near(x2, x_ref, dt, "norm of the residual")
