@@ -90,7 +90,9 @@ class PagedKVCache:
 
     def write(self, layer: int, k: torch.Tensor, v: torch.Tensor, page_ids: torch.Tensor,
               slots: torch.Tensor) -> None:
-        """Store ``k``/``v [B, L, num_kv_heads, D]`` at the mapped slots."""
+        """Store ``k``/``v [B, L, num_kv_heads, D]`` at the mapped slots (for
+        callers that compute k/v themselves; the model's fused q/k kernel
+        stores them directly)."""
         kk = k.reshape(-1, self.num_kv_heads, self.head_dim).to(self.dtype)
         vv = v.reshape(-1, self.num_kv_heads, self.head_dim).to(self.dtype)
         page_ids, slots = page_ids.long(), slots.long()
