@@ -24,14 +24,14 @@ TORCH = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.
 
 
 def _run(seed, B, Hq, Hkv, D, ps, lens, L=1, dtype="bfloat16", causal=False, P=None,
-         holes=0, past_pool=0, int8=False):
+         holes=0, past_pool=0, int8=False, q_scale=1.0):
     from nano_vllm_metal_amd import paged_attention
 
     rng = np.random.default_rng(seed)
     lens = np.asarray(lens, np.int32)
     mp = max(1, int(-(-lens.max() // ps)))
     P = P or B * mp + 3
-    q = torch.from_numpy(rng.standard_normal((B, Hq, L, D)).astype(np.float32))
+    q = torch.from_numpy((rng.standard_normal((B, Hq, L, D)) * q_scale).astype(np.float32))
     kf, vf = AO.make_pool(rng, P, Hkv, ps, D)
     if int8:
         kc, ksc = AO.quantize_int8(kf)
@@ -97,6 +97,16 @@ def test_decode_page_sizes(ps):
     """Pages smaller than a 16-row subtile, larger than a tile, and not a
     power of two; page ids past the pool are skipped."""
     _run(103, 2, 32, 4, 128, ps, [500, 131], holes=2, past_pool=1)
+
+
+@pytest.mark.parametrize("dtype,q_std", [("float16", 0.2), ("float16", 3.0),
+                                          ("bfloat16", 3.0)])
+def test_decode_query_magnitudes(dtype, q_std):
+    """The float32 query enters the score MFMAs as three page-dtype parts:
+    query entries of std 0.2 (the f16 third part near the subnormal range)
+    and of std 3 (scores of std 3 against unit keys: a sharp softmax) both
+    stay within the bound."""
+    _run(111, 4, 32, 4, 128, 16, [900, 37, 1200, 5], dtype=dtype, q_scale=q_std)
 
 
 def test_decode_one_request_long_context():

@@ -244,3 +244,24 @@ def test_graph_decode_matches_eager_logits():
         torch.cuda.synchronize()
         assert torch.equal(a, b), f"step {step}"
         toks = [int(x) for x in torch.argmax(a, -1)]
+
+
+@pytest.mark.gpu
+def test_generate_sampling_stays_in_filtered_set():
+    """Temperature sampling with top-k: every sampled token is among the k
+    most likely of its step (checked by replaying the step), lengths hold."""
+    from nano_vllm_metal_amd import LLM, SamplingParams
+
+    m = _model(6)
+    prompts = [_tokens(n, seed=60 + n) for n in (6, 9)]
+    llm = LLM(m, max_num_seqs=2, max_model_len=64, page_size=4, use_graphs=False)
+    outs = llm.generate(prompts, SamplingParams(max_tokens=5, temperature=0.8, top_k=3))
+    for p, o in zip(prompts, outs):
+        assert len(o.token_ids) == 5
+        cache = m.create_kv_cache(16, page_size=4)
+        cache.add(0)
+        logits = m.forward(torch.tensor([p], device=DEV), cache, [0])
+        for t in o.token_ids:
+            top = torch.topk(logits[0].float(), 3).indices.tolist()
+            assert t in top, (t, top)
+            logits = m.forward(torch.tensor([[t]], device=DEV), cache, [0])
