@@ -130,6 +130,35 @@ class Stages:
         self.L.check(self.lib.nvm_route_dispatch_workspace_size(T, H, E, k, ctypes.byref(size)))
         self.rws = torch.empty(max(size.value, 1), dtype=torch.uint8, device=dev)
 
+    def launch(self, stage, x):
+        """One stage alone, on the routing its last run() left (route,
+        gateup, down or combine)."""
+        lib, L, m = self.lib, self.L, self.moe
+        st = L.stream_of(self.dev)
+        T, H, I, E, k = self.T, self.H, self.I, self.E, self.k
+        gs = m.w_gate.group_size
+        r, g, u, d = m.w_router, m.w_gate, m.w_up, m.w_down
+        if stage == "route":
+            L.check(lib.nvm_moe_route_dispatch(
+                x.data_ptr(), T, H, r.weight.data_ptr(), r.scales.data_ptr(),
+                r.biases.data_ptr(), E, gs, 4, k, 1, 1, None, self.ids.data_ptr(),
+                self.scores.data_ptr(), self.offsets.data_ptr(), self.sorted.data_ptr(),
+                self.rws.data_ptr(), self.rws.numel(), st))
+        elif stage == "gateup":
+            L.check(lib.nvm_moe_expert_gateup(
+                x.data_ptr(), T, H, I, E, k, gs, 4, 1, g.weight.data_ptr(), g.scales.data_ptr(),
+                g.biases.data_ptr(), u.weight.data_ptr(), u.scales.data_ptr(),
+                u.biases.data_ptr(), self.offsets.data_ptr(), self.sorted.data_ptr(),
+                self.h.data_ptr(), 0, st))
+        elif stage == "down":
+            L.check(lib.nvm_moe_expert_down(
+                self.h.data_ptr(), T * k, H, I, E, gs, 4, 1, d.weight.data_ptr(),
+                d.scales.data_ptr(), d.biases.data_ptr(), self.offsets.data_ptr(),
+                self.sorted.data_ptr(), self.down.data_ptr(), 0, st))
+        else:
+            L.check(lib.nvm_moe_combine(self.down.data_ptr(), self.scores.data_ptr(), T, k, H, 1,
+                                        self.y.data_ptr(), st))
+
     def run(self, x, events=None):
         lib, L, m = self.lib, self.L, self.moe
         st = L.stream_of(self.dev)
@@ -197,32 +226,91 @@ def eager_stage_pass(layers, xs, steps, warmup, dev):
     return {n: v / steps for n, v in dur.items()}, total / steps, touched, ids_snap
 
 
-def graph_pass(layers, xs, steps, warmup, dev):
-    """Layer time (us) over HIP-graph replays of len(layers) fused layer calls."""
+def timed_steps(layers, xs, steps, warmup, dev):
+    """Exactly `steps` layer calls, timed as one region: `warmup` untimed calls,
+    then one HIP graph holding the `steps` calls (weight sets and inputs
+    cycled, as consecutive layers of a model run) replayed once between two
+    synchronisations.  Returns the mean layer time (us)."""
     import torch
 
     L = len(layers)
-    for i in range(max(warmup, L)):
+    for i in range(max(warmup, 1)):
         layers[i % L](xs[i % len(xs)])
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        for i in range(L):
-            layers[i](xs[i % len(xs)])
-    torch.cuda.synchronize()
-    reps = max(1, steps // L)
-    for _ in range(2):
-        g.replay()
+        for i in range(steps):
+            layers[i % L](xs[i % len(xs)])
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(reps):
-        g.replay()
+    g.replay()
     e1.record()
     torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / (reps * L)
-    return us, reps * L
+    return e0.elapsed_time(e1) * 1e3 / steps
+
+
+def median_steps(layers, xs, n, warmup=10):
+    """Median and mean layer time (us) over `n` individually timed layer calls
+    (one HIP graph per weight set, replayed in turn with an event between
+    consecutive replays), after `warmup` untimed replays."""
+    import statistics
+
+    import torch
+
+    L = len(layers)
+    graphs = []
+    for i in range(L):
+        layers[i](xs[i % len(xs)])
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            layers[i](xs[i % len(xs)])
+        graphs.append(g)
+    for i in range(warmup):
+        graphs[i % L].replay()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    ev[0].record()
+    for i in range(n):
+        graphs[i % L].replay()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    d = [ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(n)]
+    return statistics.median(d), sum(d) / n
+
+
+def stage_kernel_us(stages, xs, stage, n=64):
+    """Duration (us) of one stage's launch: a HIP graph of `n` back-to-back
+    launches of that stage alone (weight sets cycled, routing of each set
+    computed beforehand), timed with events; the mean per launch.  This is
+    the kernel's own time plus the short gap between graph kernels, the figure
+    that `rocprofv3 --kernel-trace` reports as the kernel's average."""
+    import torch
+
+    for i, s in enumerate(stages):
+        s.run(xs[i % len(xs)])
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i, s in enumerate(stages):
+            s.launch(stage, xs[i % len(xs)])
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            stages[i % len(stages)].launch(stage, xs[i % len(stages) % len(xs)])
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / n
 
 
 def eager_fused_pass(layers, xs, steps, warmup, dev):
@@ -242,32 +330,49 @@ def eager_fused_pass(layers, xs, steps, warmup, dev):
     return e0.elapsed_time(e1) * 1e3 / steps
 
 
-def decode_bench(layers, T, steps, warmup, dev, use_graph=True, shape=None):
+def decode_bench(layers, T, steps, warmup, dev, use_graph=True, shape=None, n_median=100):
+    """Decode layer at T tokens.  `layer_us` is the mean of exactly `steps`
+    layer calls in one timed region (a HIP graph of the calls); the median
+    (and mean) over max(n_median, steps) individually timed layer calls is
+    reported beside it, as is each stage's kernel time from back-to-back
+    launches of that stage (the roofline's duration)."""
     H, E, I, k, gs = ((shape or SHAPE)[n] for n in ("H", "E", "I", "k", "gs"))
     xs = make_inputs(8, T, H, dev)
-    stage_us, eager_layer_us, touched, _ = eager_stage_pass(layers, xs, steps, warmup, dev)
-    fused_us = eager_fused_pass(layers, xs, steps, warmup, dev)
-    graph_us, graph_steps = graph_pass(layers, xs, steps, warmup, dev) if use_graph else (None, 0)
+    stage_us, eager_layer_us, touched, _ = eager_stage_pass(layers, xs, min(steps, 64),
+                                                            warmup, dev)
+    fused_us = eager_fused_pass(layers, xs, min(steps, 64), warmup, dev)
+    if use_graph:
+        layer_us = timed_steps(layers, xs, steps, warmup, dev)
+        med_us, mean_us = median_steps(layers, xs, max(n_median, steps))
+    else:
+        layer_us, med_us, mean_us = fused_us, None, None
+    stages = [Stages(m, T, dev) for m in layers]
+    graph_kernel_us = {n: stage_kernel_us(stages, xs, n) for n in ("gateup", "down")}
+    del stages
     gu_b, dn_b = bytes_per_expert(H, I, gs)
     avg_touched = sum(touched) / len(touched)
     layer_bytes = avg_touched * (gu_b + dn_b) + router_bytes(H, E, gs) + 2 * T * H * 2
     gateup_bytes = avg_touched * gu_b + T * H * 2
-    layer_us = graph_us if graph_us is not None else fused_us
     return {
         "tokens": T,
         "tokens_per_s": T / (layer_us * 1e-6),
         "layer_us": layer_us,
-        "timing": "hipGraph replay" if graph_us is not None else "eager",
+        "timing": (f"one HIP-graph replay of exactly {steps} layer calls" if use_graph
+                   else "eager"),
+        "layer_us_median": med_us,
+        "layer_us_mean_individual": mean_us,
+        "median_samples": max(n_median, steps) if use_graph else 0,
+        "tokens_per_s_median": T / (med_us * 1e-6) if med_us else None,
         "eager_layer_us": fused_us,
         "eager_staged_layer_us": eager_layer_us,
         "kernel_us": stage_us,
+        "kernel_us_back_to_back": graph_kernel_us,
         "touched_experts_avg": avg_touched,
         "layer_algorithmic_bytes": layer_bytes,
         "hbm_gbs": layer_bytes / (layer_us * 1e-6) / 1e9,
         "gateup_algorithmic_bytes": gateup_bytes,
-        "gateup_gbs": gateup_bytes / (stage_us["gateup"] * 1e-6) / 1e9,
-        "down_gbs": avg_touched * dn_b / (stage_us["down"] * 1e-6) / 1e9,
-        "graph_steps": graph_steps,
+        "gateup_gbs": gateup_bytes / (graph_kernel_us["gateup"] * 1e-6) / 1e9,
+        "down_gbs": avg_touched * dn_b / (graph_kernel_us["down"] * 1e-6) / 1e9,
     }
 
 
@@ -441,8 +546,53 @@ def e2e_bench(dev, n_seqs=32, prompt_len=1024, gen=256, layers=48):
     return res
 
 
-def cpu_baseline(layer, T, seconds, dev):
-    """The C restatement of the reference path (oracle/moe_ref.c) on host cores."""
+def host_cpus():
+    """The host's CPU model, its logical/physical cores and the cores this
+    process may use (affinity and cgroup quota)."""
+    info = {"nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
+    model, cores = None, set()
+    try:
+        phys = core = None
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "model name" and model is None:
+                model = val
+            elif key == "physical id":
+                phys = val
+            elif key == "core id":
+                core = val
+            elif not line.strip() and phys is not None:
+                cores.add((phys, core))
+                phys = core = None
+    except OSError:
+        pass
+    info["cpu_model"] = model
+    info["physical_cores"] = len(cores) or None
+    quota = None
+    try:
+        q, per = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if q != "max":
+            quota = int(q) / int(per)
+    except (OSError, ValueError):
+        pass
+    info["cgroup_cpu_quota"] = quota
+    usable = info["affinity_cpus"]
+    if quota:
+        usable = min(usable, max(1, int(quota)))
+    if info["physical_cores"]:
+        usable = min(usable, info["physical_cores"])
+    info["usable_cores"] = usable
+    return info
+
+
+def cpu_baseline(layer, T, seconds, dev, runs=10, warmup=2):
+    """The C restatement of the reference path (oracle/moe_ref.c) on the host
+    cores: one decode layer of T tokens, median of `runs` timed runs after
+    `warmup`, at 1 thread and at all usable cores (affinity and cgroup
+    quota, at most one thread per physical core)."""
+    import statistics
+
     import numpy as np
     import torch
 
@@ -450,7 +600,7 @@ def cpu_baseline(layer, T, seconds, dev):
     from oracle import moe_ref as R
 
     R.build()
-    threads = R.threads(min(16, len(os.sched_getaffinity(0))))
+    host = host_cpus()
     ops = []
     for w in (layer.w_router, layer.w_gate, layer.w_up, layer.w_down):
         ops += [w.weight.cpu().numpy().view(np.uint32),
@@ -462,24 +612,38 @@ def cpu_baseline(layer, T, seconds, dev):
     # routing agreement of the CPU restatement and the GPU path on the sample
     _, gids, _ = layer.forward(xs[0], return_routing=True)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    n = 0
-    cids = None
-    while True:
-        _, ids, _ = R.forward(xb[n % len(xb)], cl, SHAPE["k"], True, SHAPE["gs"])
-        if n == 0:
-            cids = ids
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and n >= 2:
-            break
+
+    def timed(nthreads):
+        R.threads(nthreads)
+        cids = None
+        for i in range(warmup):
+            _, ids, _ = R.forward(xb[i % len(xb)], cl, SHAPE["k"], True, SHAPE["gs"])
+            cids = ids if cids is None else cids
+        d = []
+        t_start = time.perf_counter()
+        for i in range(runs):
+            t0 = time.perf_counter()
+            R.forward(xb[i % len(xb)], cl, SHAPE["k"], True, SHAPE["gs"])
+            d.append(time.perf_counter() - t0)
+            if len(d) >= 3 and time.perf_counter() - t_start > seconds:
+                break  # bounded sample: at least three runs
+        med = statistics.median(d)
+        return {"tokens_per_s": T / med, "median_s": med, "runs": len(d),
+                "threads": R.threads(0)}, cids
+
+    one, cids = timed(1)
+    allc, _ = timed(host["usable_cores"])
     return {
-        "value": T * n / el,
+        "value": allc["tokens_per_s"],
         "unit": "tokens/s",
-        "cores": threads,
+        "cores": allc["threads"],
         "kind": "port",
-        "sample": f"{n} decode layers of {T} tokens at the 30B-A3B shape (one weight set), "
-                  f"{el:.1f} s, OpenMP over routed pairs",
+        "sample": f"decode layers of {T} tokens at the 30B-A3B shape (one weight set, 4 inputs "
+                  f"cycled), median of {allc['runs']} runs after {warmup} warm-ups at "
+                  f"{allc['threads']} threads; OpenMP over routed pairs",
+        "single_thread": one,
+        "all_cores": allc,
+        "host": host,
         "routing_matches_gpu": bool(np.array_equal(cids, gids.cpu().numpy())),
     }
 
@@ -501,6 +665,35 @@ KERNEL_KEYS = (
     ("dispatch", "dispatch_kernel"),
     ("combine", "combine_kernel<1"),
 )
+
+
+PROFILE_DECODE = ROOT / "profiles" / "decode_b32_kernel_trace.txt"
+
+
+def read_rocprof_avg_us(key, path=PROFILE_DECODE):
+    """A kernel's average duration (us) from a committed rocprofv3 summary
+    (the `<key> calls=... avg=... us` lines written by --rocprof-summary)."""
+    import re
+
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        m = re.match(rf"\s*{re.escape(key)}\s+calls=\s*\d+\s+avg=\s*([0-9.]+) us", line)
+        if m:
+            return float(m.group(1))
+    return None
+
+
+def rocprof_check(key, algorithmic_bytes, achieved_gbs):
+    """The roofline recomputed from the committed rocprof average of the same
+    kernel at the same workload, beside the live figure."""
+    avg = read_rocprof_avg_us(key)
+    if avg is None:
+        return {"rocprof_avg_us": None}
+    gbs = algorithmic_bytes / (avg * 1e-6) / 1e9
+    return {"rocprof_avg_us": avg, "rocprof_profile": str(PROFILE_DECODE.relative_to(ROOT)),
+            "frac_from_rocprof": gbs / HBM_PEAK_GBS,
+            "live_vs_rocprof": achieved_gbs / gbs}
 
 
 def read_traffic(name):
@@ -704,7 +897,10 @@ def main():
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": read_traffic("decode_gateup"),
             "algorithmic_bytes_per_launch": head["gateup_algorithmic_bytes"],
-            "avg_launch_us": head["kernel_us"]["gateup"],
+            "avg_launch_us": head["kernel_us_back_to_back"]["gateup"],
+            "timing": "HIP events around a graph of 64 back-to-back gate/up launches "
+                      "(8 weight sets cycled), mean per launch",
+            **rocprof_check("decode_gateup", head["gateup_algorithmic_bytes"], achieved),
         },
         "layer_roofline": {"bound": "hbm", "achieved": head["hbm_gbs"], "peak": HBM_PEAK_GBS,
                            "unit": "GB/s", "frac": head["hbm_gbs"] / HBM_PEAK_GBS,
@@ -756,8 +952,10 @@ def main():
     if not args.no_cpu:
         log(f"[bench] CPU baseline (~{args.cpu_seconds:.0f} s)")
         out["cpu_baseline"] = cpu_baseline(layers[0], args.batch, args.cpu_seconds, dev)
-        log(f"[bench] CPU baseline: {out['cpu_baseline']['value']:.0f} tokens/s on "
-            f"{out['cpu_baseline']['cores']} threads")
+        cb = out["cpu_baseline"]
+        log(f"[bench] CPU baseline: {cb['value']:.0f} tokens/s on {cb['cores']} threads, "
+            f"{cb['single_thread']['tokens_per_s']:.0f} tokens/s on 1 thread "
+            f"({cb['host']['cpu_model']})")
     print(json.dumps(out), flush=True)
 
 

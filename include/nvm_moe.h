@@ -68,7 +68,9 @@ const char *nvm_last_error(void);
  * layer, prefill batches) run on the expert-product kernels as one expert,
  * accumulating in float32 as the reference's kernels do
  * (quantized_matmul.metal:25-44, :100-110), when N is a multiple of 64 up to
- * 8192 and K a multiple of 16; other shapes take the float64 path.
+ * 8192 and K a multiple of 16; other shapes take the float64 path (exact,
+ * but bound by the float64 matrix cores: slow for large products).  Operands
+ * of more than 2 GiB (a or b) are rejected with NVM_ERR_UNSUPPORTED.
  * Needs no workspace.
  */
 int nvm_quantized_matmul(const void *scales, const void *biases, int group_size, int bits,
@@ -83,6 +85,7 @@ int nvm_quantized_matmul(const void *scales, const void *biases, int group_size,
  * Replaces `route_topk` (layers/moe.py:37-49).
  *   x [T,H] act; wr [E,H/8]; sr, br [E,H/group] act
  *   probs [T,E] act (may be NULL); ids [T,k] int32; scores [T,k] act
+ * x and the router weights must each stay below 2 GiB (NVM_ERR_UNSUPPORTED).
  * Workspace: nvm_route_workspace_size.
  */
 int nvm_route_workspace_size(int64_t T, int64_t H, int64_t E, size_t *bytes);

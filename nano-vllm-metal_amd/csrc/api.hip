@@ -50,6 +50,9 @@ constexpr int kMaxTopK = 64;
 // reduction dimensions the product kernels are built and tested for
 constexpr int64_t kMaxProductK = 8192;
 
+// Largest buffer the kernels' 32-bit buffer descriptors and offsets address.
+constexpr int64_t k2GiB = 0x7FFF0000ll;
+
 // Bump allocator over the caller's workspace (256-byte aligned slices).
 struct Carve {
   size_t off = 0;
@@ -163,13 +166,18 @@ int check_route(const void *x, int64_t T, int64_t H, const uint32_t *wr, const v
   NVM_REQUIRE(top_k >= 1 && top_k <= E, "route: top_k=%d outside [1, E=%lld]", top_k,
               (long long)E);
   NVM_SUPPORTED(top_k <= kMaxTopK, "route: top_k at most %d", kMaxTopK);
+  // the router kernels address x and the router weights through 32-bit
+  // buffer offsets
+  NVM_SUPPORTED(T * H * 2 <= k2GiB && E * (H / 2) <= k2GiB,
+                "route: activations of %lld bytes or router weights of %lld bytes exceed 2 GiB; "
+                "split the batch", (long long)(T * H * 2), (long long)(E * (H / 2)));
   return NVM_OK;
 }
 
 int run_products(int dtype, bool decode, bool dual, nvm::GroupedArgs &g, int64_t pairs,
                  hipStream_t st) {
   // the kernels address activations through 32-bit buffer offsets
-  NVM_SUPPORTED(g.act_rows * g.act_ld * 2 <= 0x7FFF0000ll,
+  NVM_SUPPORTED(g.act_rows * g.act_ld * 2 <= k2GiB,
                 "expert products: activation buffer of %lld bytes exceeds 2 GiB; split the batch",
                 (long long)(g.act_rows * g.act_ld * 2));
   if (decode) {
@@ -222,8 +230,11 @@ int nvm_quantized_matmul(const void *scales, const void *biases, int group_size,
   if (M == 0) return NVM_OK;
   // (the product kernels address weights and activations through 32-bit
   // buffer offsets)
-  if ((K > kExactOutMax || M > kExactRowsMax) && K % 16 == 0 && N % 64 == 0 && N <= kMaxProductK &&
-      K * (N / 2) <= 0x7FFF0000ll && M * N * 2 <= 0x7FFF0000ll) {
+  // (the float64 path below has the same 32-bit limits)
+  NVM_SUPPORTED(K * (N / 2) <= k2GiB && M * N * 2 <= k2GiB,
+                "quantized_matmul: operands of more than 2 GiB (a %lld bytes, b %lld bytes); "
+                "split the product", (long long)(M * N * 2), (long long)(K * (N / 2)));
+  if ((K > kExactOutMax || M > kExactRowsMax) && K % 16 == 0 && N % 64 == 0 && N <= kMaxProductK) {
     nvm::GroupedArgs g{};
     g.act = (const uint16_t *)a;
     g.act_ld = N;

@@ -102,6 +102,22 @@ __device__ __forceinline__ float round_act(float f) {
   return Act<DT>::to_f32(Act<DT>::from_f32(f));
 }
 
+// silu of layers/activation.py:21-24 on an act value g, with the result of
+// each of its ops rounded to the activation dtype, as the reference's act
+// tensors are: e = exp(-|g|), d = 1 + e, s = 1 / d, sg = where(g < 0, 1 - s,
+// s), g * sg.  1 + e, 1 - s and g * sg are exact in float32 before their
+// rounding.  The reciprocal is v_rcp_f32 (1 ulp): 1 / d of an act value d in
+// [1, 2] lies at least 2^-23 (fp16) or 2^-17 (bf16) from an act rounding tie
+// unless it is exact, so its rounded value is the correctly rounded one.
+template <int DT>
+__device__ __forceinline__ float silu_act(float g) {
+  const float e = round_act<DT>(__expf(-fabsf(g)));
+  const float d = round_act<DT>(1.0f + e);
+  const float s = round_act<DT>(__builtin_amdgcn_rcpf(d));
+  const float sg = g < 0.0f ? round_act<DT>(1.0f - s) : s;
+  return round_act<DT>(g * sg);
+}
+
 // Round a float64 value to a floating format with `prec` significant bits and
 // smallest normal exponent `emin`, ties to even, directly from float64.  The
 // scaling by a power of two and rint() are both exact, so this is the single

@@ -1,8 +1,9 @@
 // Prefill-regime grouped W4A16 expert products (many routed rows per expert).
 //
 // Replaces `mx.gather_qmm` inside grouped_expert_linear (layers/moe.py:21-32)
-// for prefill-sized batches, with SwiGLU (layers/moe.py:84) fused into the
-// gate/up epilogue.  Work is a list of (expert, 128-row m-tile, n-tile)
+// for prefill-sized batches, with SwiGLU (layers/moe.py:84; silu op by op as
+// layers/activation.py:21-24 evaluates it, silu_act) fused into the gate/up
+// epilogue.  Work is a list of (expert, 128-row m-tile, n-tile)
 // triples built on the device from the expert offsets (prefix sum of
 // ceil(count_e / 128)), so no host synchronisation is needed and empty experts
 // cost nothing.
@@ -15,14 +16,24 @@
 // wavefront owns 2 x 32 weight rows (gate/up: the same 32 columns of both
 // matrices, so the SwiGLU pair lands in one lane) and all 128 routed rows
 // (4 x 2 tiles of v_mfma_f32_32x32x16).  Each weight word is dequantised once
-// per tile, in registers, right before its MFMA: w = q*s + b in float32,
-// rounded to the activation dtype.
+// per tile, in registers, right before its MFMA.
+//
+// Operands are fp16 for both activation dtypes.  A weight q*s + b (s, b of
+// 8 or 11 significant bits, q of 4) needs about 12 significant bits: rounded
+// to bf16 it would carry a 2^-9 relative error, which at the 235B-A22B shape
+// alone makes a mean output error above 1e-3 against the exact products;
+// rounded to fp16 (one v_pk_fma_f16, single rounding) the error is 2^-12 and
+// the outputs are those of exact weights.  bf16 activations convert to fp16
+// exactly in fp16's range (|x| <= 65504; post-norm activations are far
+// inside it), and the fp16 MFMA runs at the bf16 rate.
 //
 // k-order inside a k-step: MFMA chunk c (16 wide) and lane half h cover
-// k = 8*(4h + c) + i, i = 0..7, in both operands.  A lane's B operand for
-// chunk c is then packed word 4h + c of its weight row (one 16-byte LDS read
-// serves all four chunks) and its A operand is 16 bytes at offset
-// 16*(4h + c) of the activation row.
+// the eight k = 8*(4h + c) + i, i = 0..7, in both operands, in the slot
+// order i = 0,4,1,5,2,6,3,7 that the nibble expansion of one packed word
+// produces.  A lane's B operand for chunk c is then packed word 4h + c of its
+// weight row (one 16-byte LDS read serves all four chunks) and its A operand
+// is the 16 bytes at offset 16*(4h + c) of the activation row, which staging
+// stores in that slot order.
 #include "common.h"
 #include "internal.h"
 
@@ -40,26 +51,70 @@ constexpr int B_STAGE = WROWS * B_PITCH;
 constexpr int STAGE = A_STAGE + B_STAGE;
 constexpr int kGemmLds = 2 * STAGE;
 
-__device__ __forceinline__ float byte_f32(uint32_t v, int j) {
-  return (float)((v >> (8 * j)) & 0xFFu);  // v_cvt_f32_ubyte<j>
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pk_fma_h(uint32_t a, uint32_t b, uint32_t c) {  // v_pk_fma_f16
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_fma(__builtin_bit_cast(h2_t, a),
+                                                      __builtin_bit_cast(h2_t, b),
+                                                      __builtin_bit_cast(h2_t, c)));
+}
+__device__ __forceinline__ uint32_t pk_add_h(uint32_t a, uint32_t b) {  // v_pk_add_f16
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, a) + __builtin_bit_cast(h2_t, b));
 }
 
-// One packed word (codes q0..q7, q_i at bits 4i) -> 8 act values q_i*s + b in
-// natural order: dword j holds (k = 2j, k = 2j + 1).
+// One packed word (codes q0..q7, q_i at bits 4i) -> the 8 weights q_i*s + b
+// as fp16, each the correctly rounded value of the exact q*s + b (one
+// v_pk_fma_f16 per pair, single rounding), in the pair order
+// (q0,q4)(q1,q5)(q2,q6)(q3,q7): the codes become the exact fp16 values
+// 1024 + q by OR-ing them into the mantissa of 1024.0 (whose ulp is 1) and
+// 1024 is then taken off exactly.  s2, b2: (s, s) and (b, b) as fp16 pairs.
+__device__ __forceinline__ u32x4 dequant8_h(uint32_t w, uint32_t s2, uint32_t b2, uint32_t mask,
+                                            uint32_t magic) {
+  u32x4 d = nibble_pairs_v<0>(w, mask, magic);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) d[i] = pk_fma_h(pk_add_h(d[i], 0xE400E400u), s2, b2);
+  return d;
+}
+
+// Eight consecutive activations x0..x7 (one 16-byte chunk of a row) -> fp16
+// in the pair order (x0,x4)(x1,x5)(x2,x6)(x3,x7) of dequant8_h.  bf16 values
+// convert exactly (fp16 carries more significand bits) within fp16's range;
+// v_cvt_pkrtz_f16_f32 only rounds below it (|x| < 2^-14, with a contribution
+// far under the product's rounding) and saturates above 65504.
 template <int DT>
-__device__ __forceinline__ u32x4 dequant8(uint32_t w, float s, float b) {
-  using A = Act<DT>;
-  uint32_t lo = w & 0x0F0F0F0Fu;         // byte j = q_{2j}
-  uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // byte j = q_{2j+1}
-  // opaque to the optimiser, which would otherwise re-derive every byte with
-  // its own mask instead of converting bytes of the masked word directly
-  asm("" : "+v"(lo), "+v"(hi));
-  u32x4 o;
-  o.x = A::pack2(fmaf(byte_f32(lo, 0), s, b), fmaf(byte_f32(hi, 0), s, b));
-  o.y = A::pack2(fmaf(byte_f32(lo, 1), s, b), fmaf(byte_f32(hi, 1), s, b));
-  o.z = A::pack2(fmaf(byte_f32(lo, 2), s, b), fmaf(byte_f32(hi, 2), s, b));
-  o.w = A::pack2(fmaf(byte_f32(lo, 3), s, b), fmaf(byte_f32(hi, 3), s, b));
-  return o;
+__device__ __forceinline__ u32x4 act_to_h(u32x4 v) {
+  if constexpr (DT == DT_F16) {
+    return pair_order(v);
+  } else {
+    u32x4 o;
+    const float x0 = __uint_as_float(v.x << 16), x1 = __uint_as_float(v.x & 0xFFFF0000u);
+    const float x2 = __uint_as_float(v.y << 16), x3 = __uint_as_float(v.y & 0xFFFF0000u);
+    const float x4 = __uint_as_float(v.z << 16), x5 = __uint_as_float(v.z & 0xFFFF0000u);
+    const float x6 = __uint_as_float(v.w << 16), x7 = __uint_as_float(v.w & 0xFFFF0000u);
+    o.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x0, x4));
+    o.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x1, x5));
+    o.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x2, x6));
+    o.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x3, x7));
+    return o;
+  }
+}
+
+// A scale or bias (act bits) as the fp16 pair (v, v); bf16 values convert
+// with round to nearest even (exactly, inside fp16's normal range).
+template <int DT>
+__device__ __forceinline__ uint32_t sb_pair_h(uint32_t bits) {
+  uint32_t h;
+  if constexpr (DT == DT_F16)
+    h = bits & 0xFFFFu;
+  else
+    h = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float(bits << 16));
+  return h | (h << 16);
+}
+
+__device__ __forceinline__ f32x16 mfma32_h(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
 template <int DT, bool DUAL>
@@ -194,7 +249,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
     uint8_t *Bs = As + A_STAGE;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      *(u32x4 *)(As + ((tid >> 3) + 32 * c) * A_PITCH + 16 * (tid & 7)) = g.a[c];
+      *(u32x4 *)(As + ((tid >> 3) + 32 * c) * A_PITCH + 16 * (tid & 7)) = act_to_h<DT>(g.a[c]);
 #pragma unroll
     for (int c = 0; c < 2; ++c)
       *(u32x4 *)(Bs + ((tid >> 1) + 128 * c) * B_PITCH + 16 * (tid & 1)) = g.b[c];
@@ -208,14 +263,18 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[s][i][r] = 0.f;
 
-  float sc[2], bi[2];
+  // this k-step's scale and bias of the lane's two weight rows, fp16 pairs
+  uint32_t sc[2], bi[2];
   auto take_sb = [&](const Stage &g) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      sc[s] = A::to_f32(g.s[s]);
-      bi[s] = A::to_f32(g.z[s]);
+      sc[s] = sb_pair_h<DT>(g.s[s]);
+      bi[s] = sb_pair_h<DT>(g.z[s]);
     }
   };
+  // nibble-expansion constants in registers (one v_and_or_b32 per dword)
+  const uint32_t nib_mask = sgpr_const(0x000F000Fu);
+  const uint32_t magic = vgpr_const(0x64006400u);  // fp16 (1024, 1024)
   // Software-pipelined over the four 16-wide chunks: the A reads and the
   // dequantisation of chunk c + 1 are issued ahead of chunk c's MFMAs.
   auto compute = [&](int buf) {
@@ -231,7 +290,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
     };
     auto deq = [&](int c, u32x4 (&bf)[2]) {
 #pragma unroll
-      for (int s = 0; s < 2; ++s) bf[s] = dequant8<DT>(bw[s][c], sc[s], bi[s]);
+      for (int s = 0; s < 2; ++s) bf[s] = dequant8_h(bw[s][c], sc[s], bi[s], nib_mask, magic);
     };
     u32x4 af[4], bf[2];
     load_a(0, af);
@@ -246,7 +305,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
 #pragma unroll
       for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[s][i] = A::mfma32(af[i], bf[s], acc[s][i]);
+        for (int i = 0; i < 4; ++i) acc[s][i] = mfma32_h(af[i], bf[s], acc[s][i]);
       if (c < 3) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) af[i] = afn[i];
@@ -296,7 +355,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
         if (col < R) {
           const float gv = round_act<DT>(acc[0][i][r]);
           const float uv = round_act<DT>(acc[1][i][r]);
-          op[col] = A::from_f32(gv / (1.0f + __expf(-gv)) * uv);
+          op[col] = A::from_f32(silu_act<DT>(gv) * uv);
         }
       } else {
 #pragma unroll

@@ -2,7 +2,7 @@
 //
 // Replaces `mx.gather_qmm` inside grouped_expert_linear (layers/moe.py:21-32)
 // for decode-sized batches, fused with SwiGLU (layers/moe.py:84,
-// layers/activation.py:21-24) for the gate/up pair.
+// layers/activation.py:21-24, op by op: silu_act) for the gate/up pair.
 //
 // Weight bytes dominate, so the kernel is shaped to stream them at HBM rate:
 //
@@ -394,10 +394,11 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
         int64_t orow;
         if constexpr (DUAL) {
           // reference rounding points: gate and up outputs are act tensors,
-          // silu(gate) * up is rounded once more
+          // silu's ops each round (silu_act), and silu(gate) * up rounds once
+          // more (its float32 product is exact)
           const float gv = round_act<DT>(sum[0]);
           const float uv = round_act<DT>(sum[NM - 1]);
-          r = A::from_f32(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * uv);
+          r = A::from_f32(silu_act<DT>(gv) * uv);
           orow = (second ? ep_slot0[UPB - 1] : ep_slot0[0]) + tok;
         } else {
           r = A::from_f32(sum[0]);

@@ -50,18 +50,42 @@ def qk_norm_rope_store(qkv: torch.Tensor, num_heads: int, num_kv_heads: int, hea
     T = x.shape[0]
     if key_pages.dtype != qkv.dtype or value_pages.dtype != qkv.dtype:
         raise ValueError("qk_norm_rope_store: pages must have the activation dtype")
+    # the kernel addresses page p, kv head h, slot s at ((p * Hkv + h) * ps + s) * D
+    for name, pg in (("key_pages", key_pages), ("value_pages", value_pages)):
+        if pg.dim() != 4 or pg.shape[1] != num_kv_heads or pg.shape[3] != D:
+            raise ValueError(f"qk_norm_rope_store: {name} must be [P, {num_kv_heads}, page_size, "
+                             f"{D}], got {tuple(pg.shape)}")
+        if not pg.is_contiguous():
+            raise ValueError(f"qk_norm_rope_store: {name} must be contiguous")
+    if value_pages.shape != key_pages.shape:
+        raise ValueError("qk_norm_rope_store: key and value pages differ in shape")
+    if q_norm.numel() != D or k_norm.numel() != D:
+        raise ValueError(f"qk_norm_rope_store: q_norm/k_norm must have {D} elements")
+    if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != D // 2:
+        raise ValueError(f"qk_norm_rope_store: cos/sin must be [max_pos, {D // 2}]")
+    # Converted operands are bound to locals that live until the library call
+    # has been enqueued: a temporary freed inside the argument list would hand
+    # its block to the next conversion, and two arguments would alias.
+    idx = []
+    for name, t in (("positions", positions), ("page_ids", page_ids), ("slots", slots)):
+        ti = t.reshape(-1).to(torch.int32).contiguous()
+        if ti.numel() != T:
+            raise ValueError(f"qk_norm_rope_store: {name} must have {T} elements, got {ti.numel()}")
+        idx.append(ti)
+    pos_i, page_i, slot_i = idx
+    qn = q_norm.to(qkv.dtype).contiguous()
+    kn = k_norm.to(qkv.dtype).contiguous()
+    cos_c = cos.to(torch.float32).contiguous()
+    sin_c = sin.to(torch.float32).contiguous()
     q = torch.empty((T, num_heads, D), dtype=torch.float32, device=dev)
     k = torch.empty((T, num_kv_heads, D), dtype=torch.float32, device=dev) if want_kv else None
     v = torch.empty((T, num_kv_heads, D), dtype=torch.float32, device=dev) if want_kv else None
     _lib.check(lib.nvm_qk_norm_rope_store(
-        x.data_ptr(), T, num_heads, num_kv_heads, D, q_norm.to(qkv.dtype).contiguous().data_ptr(),
-        k_norm.to(qkv.dtype).contiguous().data_ptr(), float(eps),
-        positions.to(torch.int32).reshape(-1).contiguous().data_ptr(),
-        cos.contiguous().data_ptr(), sin.contiguous().data_ptr(), cos.shape[0],
-        page_ids.to(torch.int32).reshape(-1).contiguous().data_ptr(),
-        slots.to(torch.int32).reshape(-1).contiguous().data_ptr(), key_pages.data_ptr(),
-        value_pages.data_ptr(), key_pages.shape[0], key_pages.shape[2],
-        _lib.dtype_code(qkv.dtype), q.data_ptr(), _lib.ptr(k), _lib.ptr(v), _lib.stream_of(dev)))
+        x.data_ptr(), T, num_heads, num_kv_heads, D, qn.data_ptr(), kn.data_ptr(), float(eps),
+        pos_i.data_ptr(), cos_c.data_ptr(), sin_c.data_ptr(), cos_c.shape[0], page_i.data_ptr(),
+        slot_i.data_ptr(), key_pages.data_ptr(), value_pages.data_ptr(), key_pages.shape[0],
+        key_pages.shape[2], _lib.dtype_code(qkv.dtype), q.data_ptr(), _lib.ptr(k), _lib.ptr(v),
+        _lib.stream_of(dev)))
     return q, k, v
 
 
@@ -75,13 +99,15 @@ def moe_residual_rms_norm(moe, x: torch.Tensor, h: torch.Tensor, weight: torch.T
     if not isinstance(moe, Moe):
         raise TypeError("moe_residual_rms_norm: a Moe block is required")
     lib = _lib.load()
-    dev = _lib.require_device(x, h, weight, moe.w_router.weight)
+    dev = _lib.require_device(x, h, weight, moe.w_router.weight, moe.w_gate.weight,
+                              moe.w_up.weight, moe.w_down.weight)
     *lead, H = x.shape
+    if h.shape != x.shape or weight.numel() != H:
+        raise ValueError("moe_residual_rms_norm: h must have the shape of x and weight H elements")
+    E, I = moe.check_operands(x.dtype, H)
     x2 = x.reshape(-1, H).contiguous()
-    h2 = h.reshape(-1, H).contiguous()
+    h2 = h.reshape(-1, H).to(x.dtype).contiguous()
     T = x2.shape[0]
-    E = moe.w_router.weight.shape[0]
-    I = moe.w_gate.weight.shape[1]
     ws = moe._workspace(T, H, I, E, dev)
     (wr, sr, br), (wg, sg, bg), (wu, su, bu), (wd, sd, bd) = moe._operands()
     w = weight.to(x.dtype).contiguous()

@@ -178,6 +178,7 @@ class Moe:
         # the regime of the expert products; "auto" follows the routed batch size
         self.regime = "auto"
         self._ws = None
+        self._retired_ws = []
 
     def _operands(self):
         return [(_i32(w.weight), w.scales.contiguous(), w.biases.contiguous())
@@ -189,32 +190,48 @@ class Moe:
         _lib.check(lib.nvm_moe_workspace_size(T, H, I, E, self.num_experts_per_tok,
                                               ctypes.byref(size)))
         if self._ws is None or self._ws.numel() < size.value or self._ws.device != dev:
+            # A HIP graph captured earlier may still refer to the old buffer:
+            # it stays alive with the block (each replacement is larger, so
+            # the retired buffers total less than the current one).
+            if self._ws is not None:
+                self._retired_ws.append(self._ws)
             self._ws = _workspace(size.value, dev)
         return self._ws
 
-    def forward(self, x: torch.Tensor, return_routing: bool = False):
-        lib = _lib.load()
-        dev = _lib.require_device(x, self.w_router.weight, self.w_gate.weight,
-                                  self.w_up.weight, self.w_down.weight)
+    def check_operands(self, act: torch.dtype, H: int):
+        """Validate the four weight sets against activations of dtype ``act``
+        and hidden size ``H`` (the library takes one group size and bit width
+        for all of them); returns ``(E, I)``."""
         for name, w in (("router", self.w_router), ("gate", self.w_gate), ("up", self.w_up),
                         ("down", self.w_down)):
-            if w.scales.dtype != x.dtype or w.biases.dtype != x.dtype:
+            if w.scales.dtype != act or w.biases.dtype != act:
                 raise ValueError(f"Moe: {name} scales/biases must have the activation dtype")
         gs = self.w_gate.group_size
         bits = self.w_gate.bits
         for w in (self.w_router, self.w_up, self.w_down):
             if w.group_size != gs or w.bits != bits:
                 raise ValueError("Moe: all weights must share group_size and bits")
-        *lead, H = x.shape
-        x2 = x.reshape(-1, H).contiguous()
-        T = x2.shape[0]
         E = self.w_router.weight.shape[0]
         I = self.w_gate.weight.shape[1]
-        k = self.num_experts_per_tok
+        if self.w_router.weight.shape != (E, H // 8):
+            raise ValueError("Moe: router weight must be [E, H/8]")
         if self.w_gate.weight.shape != (E, I, H // 8) or self.w_up.weight.shape != (E, I, H // 8):
             raise ValueError("Moe: gate/up weights must be [E, I, H/8]")
         if self.w_down.weight.shape != (E, H, I // 8):
             raise ValueError("Moe: down weight must be [E, H, I/8]")
+        return E, I
+
+    def forward(self, x: torch.Tensor, return_routing: bool = False):
+        lib = _lib.load()
+        dev = _lib.require_device(x, self.w_router.weight, self.w_gate.weight,
+                                  self.w_up.weight, self.w_down.weight)
+        *lead, H = x.shape
+        E, I = self.check_operands(x.dtype, H)
+        gs = self.w_gate.group_size
+        bits = self.w_gate.bits
+        x2 = x.reshape(-1, H).contiguous()
+        T = x2.shape[0]
+        k = self.num_experts_per_tok
         prep = self._operands()
         ws = self._workspace(T, H, I, E, dev)
         y = torch.empty_like(x2)

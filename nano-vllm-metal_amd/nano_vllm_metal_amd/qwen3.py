@@ -98,8 +98,15 @@ class DenseMLP:
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         g = quantized_linear(x, self.w_gate)
         u = quantized_linear(x, self.w_up)
-        h = (F.silu(g.float()) * u.float()).to(x.dtype)
-        return quantized_linear(h, self.w_down)
+        return quantized_linear(silu(g) * u, self.w_down)
+
+
+def silu(x: torch.Tensor) -> torch.Tensor:
+    """``silu`` of layers/activation.py:21-24 as the same element-wise ops on
+    tensors of the activation dtype, each result rounded to that dtype."""
+    sig = 1 / (1 + torch.exp(-torch.abs(x)))
+    sig = torch.where(x < 0, 1 - sig, sig)
+    return x * sig
 
 
 @dataclass

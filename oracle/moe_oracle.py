@@ -26,7 +26,8 @@ Reference functions restated here (paths relative to the reference's
 * ``dispatch`` — the stable ``argsort`` of ``layers/moe.py:16-20``.
 * ``grouped_expert_linear`` — ``layers/moe.py:8-34``.
 * ``moe_forward`` — ``Moe.__call__``, ``layers/moe.py:69-86``, with ``silu``
-  from ``layers/activation.py:21-24``.
+  from ``layers/activation.py:21-24`` (``silu_act``: its five ops, each
+  rounded to act).
 
 Rounding specification.  Every place where the reference materialises an
 activation-dtype ("act", fp16 or bf16) tensor, the oracle rounds the exact
@@ -36,7 +37,8 @@ mathematical value (computed in float64) to act with round-to-nearest-even:
 * probs  = rnd(softmax(logits)) (softmax of the act logits, in float64)
 * top-k  = the k largest probs; ties go to the lower expert index
 * scores = probs[ids]; with renormalisation rnd(s_j / rnd(sum_j s_j))
-* gate, up = rnd(x . W^T); h = rnd(silu(gate) * up); down = rnd(h . Wd^T)
+* gate, up = rnd(x . W^T); h = rnd(silu_act(gate) * up) with silu_act the
+  reference's stable form rounded after each of its ops; down = rnd(h . Wd^T)
 * y = rnd(sum_j rnd(down_j * score_j))
 
 Parity status (what pins each function; see tests/test_oracle.py):
@@ -286,9 +288,39 @@ def grouped_expert_linear(x, wq, scales, biases, group_size: int, expert_ids, ac
 
 
 def silu(v):
-    """x * sigmoid(x) in float64 (activation.py:21-24 restated exactly)."""
+    """x * sigmoid(x) in float64, unrounded (the mathematical function)."""
     v = np.asarray(v, np.float64)
     return v / (1.0 + np.exp(-v))
+
+
+def silu_act(g, act: str) -> np.ndarray:
+    """``silu`` of activation.py:21-24 on an act tensor, op by op.
+
+    The reference evaluates the stable form as separate activation-dtype
+    ops, each materialising a rounded act tensor:
+
+      e  = exp(-|g|)            (rounded)
+      d  = 1 + e                (rounded)
+      s  = 1 / d                (rounded)
+      sg = where(g < 0, 1 - s, s)   (1 - s rounded)
+      silu = g * sg             (rounded)
+
+    Every intermediate here is computed in float64 and rounded once to act.
+    For d, 1 - s and g * sg the float64 value is exact (act operands), and
+    1 / d is never a rounding tie (d has at most 11 significant bits and is
+    not a power of two unless the quotient is exact), so this equals MLX's
+    float32-then-act evaluation of each op; exp itself is correctly rounded
+    here, MLX's own exp is not pinned.  Consequences of the rounding points:
+    for |g| past 8 ln 2 (bf16) or 11 ln 2 (fp16) the rounded 1 + e is 1 and a
+    negative g gives exactly 0; for negative g near -3 the rounded 1 - s
+    carries a relative error of a few percent against the exact sigmoid.
+    """
+    g = np.asarray(g, np.float64)
+    e = round_act(np.exp(-np.abs(g)), act)
+    d = round_act(1.0 + e, act)
+    s = round_act(1.0 / d, act)
+    sg = np.where(g < 0, round_act(1.0 - s, act), s)
+    return round_act(g * sg, act)
 
 
 def moe_forward(x, weights: dict, top_k: int, norm_topk_prob: bool, act: str, group_size: int):
@@ -314,7 +346,7 @@ def moe_forward(x, weights: dict, top_k: int, norm_topk_prob: bool, act: str, gr
         wd = dequantize(weights["down"][0][e], weights["down"][1][e], weights["down"][2][e], group_size)
         g = round_act(xe @ wg.T, act)
         u = round_act(xe @ wu.T, act)
-        h = round_act(silu(g) * u, act)
+        h = round_act(silu_act(g, act) * u, act)
         down[pairs] = round_act(h @ wd.T, act)
     contrib = round_act(down.reshape(T, top_k, H) * scores[..., None], act)
     y = round_act(contrib.sum(axis=1), act)
@@ -356,15 +388,25 @@ def random_packed(rng, shape, group_size: int, act: str, w_std: float = 0.02):
     normal group spans about 4.8 sigma), signed scales of that range over 15
     steps and biases centring the codes, all act-representable.  Much cheaper
     than quantising a float tensor at the 30B/235B expert shapes, and the same
-    layout."""
+    layout.
+
+    Each code comes from one uniform byte through an inverse-CDF table; two
+    bytes (one uniform 16-bit draw) give the byte holding codes 2i (low
+    nibble) and 2i + 1, and four such bytes, little-endian, are one packed
+    word, so code 8w + j lands in bits [4j, 4j+4) of word w."""
     *lead, n_out, n_in = shape
-    # inverse-CDF table: a uniform byte picks the code of the normal quantile
-    # at its bin centre
+    assert n_in % 8 == 0
     nd = statistics.NormalDist()
     table = np.array([min(15.0, max(0.0, round(7.5 + nd.inv_cdf((i + 0.5) / 256) * 15.0 / 4.8)))
-                      for i in range(256)], dtype=np.uint32)
-    q = table[rng.integers(0, 256, size=(*lead, n_out, n_in), dtype=np.uint8)]
-    wq = pack_nibbles(q)
+                      for i in range(256)], dtype=np.uint8)
+    pair = (table[np.arange(65536) & 0xFF] | (table[np.arange(65536) >> 8] << 4)).astype(np.uint8)
+    wq = np.empty((*lead, n_out, n_in // 8), dtype=np.uint32)
+    flat = wq.reshape(-1, n_in // 8)
+    step = max(1, (1 << 24) // n_in)  # rows per batch (bounded temporaries)
+    for r in range(0, flat.shape[0], step):
+        rows = flat[r:r + step]
+        draws = rng.integers(0, 65536, size=(rows.shape[0], n_in // 2), dtype=np.uint16)
+        rows[...] = pair[draws].view("<u4")
     gshape = (*lead, n_out, n_in // group_size)
     mag = w_std * 4.8 / 15.0 * (1.0 + 0.1 * rng.standard_normal(gshape))
     sign = np.where(rng.random(gshape) < 0.5, -1.0, 1.0)

@@ -17,7 +17,8 @@
  *   5. per routed pair, the scalar dequant-dot loop of
  *      metal/src/quantized_matmul.cpp:117-145 (float accumulation,
  *      w = float(q)*float(scale) + float(bias)) for gate and up, rounded to
- *      act; h = rnd(silu(gate) * up); the same loop for down, rounded to act
+ *      act; h = rnd(silu(gate) * up) with silu's ops each rounded to act
+ *      (layers/activation.py:21-24); the same loop for down, rounded to act
  *      (layers/moe.py:81-85, layers/activation.py:21-24);
  *   6. y = rnd(sum_j rnd(down_j * score_j)) in float (layers/moe.py:86).
  * Step 5 is parallelised over routed pairs with OpenMP.
@@ -80,6 +81,16 @@ static double round_to(double v, int prec, int emin) {
 
 static double round_act(double v, int dt) {
   return dt == DT_BF16 ? round_to(v, 8, -126) : round_to(v, 11, -14);
+}
+
+/* silu of layers/activation.py:21-24 on an act value g, each of its ops
+ * (exp(-|g|), 1 + e, 1 / d, where(g < 0, 1 - s, s), g * sg) rounded to act. */
+static double silu_act(double g, int dt) {
+  const double e = round_act(exp(-fabs(g)), dt);
+  const double d = round_act(1.0 + e, dt);
+  const double s = round_act(1.0 / d, dt);
+  const double sg = g < 0.0 ? round_act(1.0 - s, dt) : s;
+  return round_act(g * sg, dt);
 }
 
 /* bit pattern of an act-representable value */
@@ -239,7 +250,7 @@ int moe_ref_forward(const uint16_t *x, int64_t T, int64_t H, int64_t I, int64_t 
           const int64_t row = (int64_t)e * I + r;
           const double g = round_act(qdot_row(xr, wg + row * hw, sg + row * hg, bg + row * hg, H, gs, dt), dt);
           const double u = round_act(qdot_row(xr, wu + row * hw, su + row * hg, bu + row * hg, H, gs, dt), dt);
-          h[r] = act_bits(round_act((float)(g / (1.0 + exp(-g))) * (float)u, dt), dt);
+          h[r] = act_bits(round_act(silu_act(g, dt) * u, dt), dt);
         }
         for (int64_t c = 0; c < H; ++c) {
           const int64_t row = (int64_t)e * H + c;

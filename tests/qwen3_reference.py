@@ -23,6 +23,14 @@ def _lin(x, w, dt):
     return (x.float() @ _deq(w).T).to(dt)
 
 
+def _silu(x):
+    """layers/activation.py:21-24 on act tensors: each op's result is a
+    rounded act tensor, as in the reference (the stable exp(-|x|) form)."""
+    sig = 1 / (1 + torch.exp(-torch.abs(x)))
+    sig = torch.where(x < 0, 1 - sig, sig)
+    return x * sig
+
+
 def _rms(x, w, eps):
     xf = x.float()
     return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()).to(x.dtype)
@@ -39,12 +47,22 @@ def _rope(x, pos, theta):
     return torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], -1).to(x.dtype)
 
 
-def _moe(x, moe, dt):
+def _moe(x, moe, dt, margins=None):
     E = moe.w_router.weight.shape[0]
-    logits = _lin(x, moe.w_router, dt)
-    probs = torch.softmax(logits.float(), -1).to(dt)
+    # router logits and softmax as the oracle defines them: exact sums rounded
+    # once (float64 here), then the k largest probabilities with ties to the
+    # lower expert index (a stable descending sort)
+    logits = (x.double() @ _deq(moe.w_router).double().T).to(dt)
+    probs = torch.softmax(logits.double(), -1).to(dt)
     k = moe.num_experts_per_tok
-    sc, ids = torch.topk(probs.float(), k, dim=-1)
+    sc, ids = torch.sort(probs.float(), dim=-1, descending=True, stable=True)
+    if margins is not None and k < E:
+        # gap between the k-th and (k+1)-th probability in units of the act
+        # ulp of the k-th: 0 is a tie broken by expert index, 1 is one ulp
+        ulp = torch.pow(2.0, torch.floor(torch.log2(sc[:, k - 1])) -
+                        (7 if dt == torch.bfloat16 else 10))
+        margins.append(((sc[:, k - 1] - sc[:, k]) / ulp).cpu())
+    sc, ids = sc[:, :k], ids[:, :k]
     sc = sc.to(dt)
     if moe.norm_topk_prob:
         sc = (sc.float() / sc.float().sum(-1, keepdim=True).to(dt).float()).to(dt)
@@ -56,7 +74,7 @@ def _moe(x, moe, dt):
             e = int(ids[t, j])
             g = (x[t].float() @ wg[e].T).to(dt)
             u = (x[t].float() @ wu[e].T).to(dt)
-            h = (torch.nn.functional.silu(g.float()) * u.float()).to(dt)
+            h = _silu(g) * u
             d = (h.float() @ wd[e].T).to(dt)
             acc.append((d.float() * sc[t, j].float()).to(dt))
         y[t] = torch.stack([a.float() for a in acc]).sum(0)
@@ -64,8 +82,12 @@ def _moe(x, moe, dt):
     return y.to(dt)
 
 
-def reference_logits(model, tokens) -> torch.Tensor:
-    """``tokens [L]`` -> logits ``[L, vocab]`` (float32) of every position."""
+def reference_logits(model, tokens, margins=None) -> torch.Tensor:
+    """``tokens [L]`` -> logits ``[L, vocab]`` (float32) of every position.
+
+    With a list ``margins``, each MoE layer appends the per-token gap between
+    its k-th and (k+1)-th routing probability in act ulps (near-ties, where a
+    one-ulp difference in the layer input can change the chosen experts)."""
     from nano_vllm_metal_amd.moe import Moe
 
     c = model.config
@@ -92,11 +114,11 @@ def reference_logits(model, tokens) -> torch.Tensor:
         h = h + _lin(o, layer.wo, dt)
         x = _rms(h, layer.post_norm, c.rms_norm_eps)
         if isinstance(layer.mlp, Moe):
-            h = h + _moe(x, layer.mlp, dt)
+            h = h + _moe(x, layer.mlp, dt, margins)
         else:
             m = layer.mlp
             g, u = _lin(x, m.w_gate, dt), _lin(x, m.w_up, dt)
-            h = h + _lin((torch.nn.functional.silu(g.float()) * u.float()).to(dt), m.w_down, dt)
+            h = h + _lin(_silu(g) * u, m.w_down, dt)
     h = _rms(h, model.norm, c.rms_norm_eps)
     head = model.lm_head if model.lm_head is not None else model.embed_w
     return _lin(h, head, dt).float()

@@ -97,6 +97,17 @@ def test_forward_empty_batch_is_a_no_op():
     assert _forward(lib, T=0) == 0
 
 
+def test_operands_beyond_32bit_offsets_are_refused():
+    """The kernels address x and the weights through 32-bit buffer offsets:
+    larger operands are refused instead of being read as zeros."""
+    L, lib = _lib()
+    T = 600_000  # 600000 x 2048 bf16 = 2.46 GB
+    r = lib.nvm_moe_route(1, T, 2048, 1, 1, 1, 128, 64, 4, 8, 0, 1, None, 1, 1, 1, 1 << 40, None)
+    assert r == L.NVM_ERR_UNSUPPORTED and "2 GiB" in _err(lib)
+    r = lib.nvm_quantized_matmul(1, 1, 64, 4, 1, 1, 1, 1, T, 2048, 128, 1, None)
+    assert r == L.NVM_ERR_UNSUPPORTED and "2 GiB" in _err(lib)
+
+
 def test_quantized_matmul_validation():
     L, lib = _lib()
     # the reference requires transpose_b (quantized_matmul.cpp:56-58)

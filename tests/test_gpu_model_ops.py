@@ -46,9 +46,14 @@ def test_residual_rms_norm(T, H, dt):
     _near(x3, _rms(h, w, 1e-6), dt, "norm")
 
 
-@pytest.mark.parametrize("Hq,Hkv,D,dt", [(32, 4, 128, torch.bfloat16), (8, 2, 64, torch.float16),
-                                         (4, 4, 128, torch.bfloat16)])
-def test_qk_norm_rope_store(Hq, Hkv, D, dt):
+@pytest.mark.parametrize("Hq,Hkv,D,dt,wide", [(32, 4, 128, torch.bfloat16, False),
+                                              (8, 2, 64, torch.float16, False),
+                                              (4, 4, 128, torch.bfloat16, False),
+                                              (32, 4, 128, torch.bfloat16, True)])
+def test_qk_norm_rope_store(Hq, Hkv, D, dt, wide):
+    """wide: int64 positions, page ids and slots and float32 norm weights,
+    which the wrapper converts (each converted tensor must stay alive, and
+    distinct, until the call is enqueued)."""
     from nano_vllm_metal_amd.fused import qk_norm_rope_store
     from nano_vllm_metal_amd.qwen3 import RoPE
 
@@ -65,8 +70,13 @@ def test_qk_norm_rope_store(Hq, Hkv, D, dt):
     page_ids[4] = -1  # not stored
     kp = torch.zeros(P, Hkv, ps, D, dtype=dt, device=DEV)
     vp = torch.zeros_like(kp)
-    q, k, v = qk_norm_rope_store(qkv, Hq, Hkv, D, qn, kn, 1e-6, pos, rope.cos, rope.sin, page_ids,
-                                 slots, kp, vp, want_kv=True)
+    if wide:
+        q, k, v = qk_norm_rope_store(qkv, Hq, Hkv, D, qn.float(), kn.float(), 1e-6, pos.long(),
+                                     rope.cos, rope.sin, page_ids.long(), slots.long(), kp, vp,
+                                     want_kv=True)
+    else:
+        q, k, v = qk_norm_rope_store(qkv, Hq, Hkv, D, qn, kn, 1e-6, pos, rope.cos, rope.sin,
+                                     page_ids, slots, kp, vp, want_kv=True)
     x = qkv.view(T, Hq + 2 * Hkv, D)
     rq = _rope(_rms(x[:, :Hq], qn, 1e-6), pos.long(), 1e6)
     rk = _rope(_rms(x[:, Hq:Hq + Hkv], kn, 1e-6), pos.long(), 1e6)

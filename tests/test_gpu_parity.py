@@ -130,8 +130,8 @@ def test_quantized_matmul_matches_oracle(M, N, K, act, gs):
 # would be smaller than the chip) or the GEMM, accumulating in float32 like
 # quantized_matmul.metal:25-44.  The
 # GEMV's sums equal the unrounded dequantised products; the GEMM rounds each
-# dequantised weight to the activation dtype before its MFMA, as MLX's qmm
-# does (the reference's NVM_QMATMUL_BACKEND=mlx path, layers/linear.py:109-117).
+# dequantised weight to fp16 (single rounding of q*s + b) before its fp16
+# MFMA, 2^-12 relative, below the output rounding of either activation dtype.
 # Both are held to the tolerance against the exactly rounded oracle (outputs
 # are of unit scale, so the mean error is taken relative to the largest
 # output), and most elements must equal the exactly rounded result of their
@@ -162,7 +162,7 @@ def test_quantized_matmul_dense_products(M, N, K, act, gs, path):
     ref = O.quantized_matmul(a, wq, s, b, gs, act)
     assert_moe_close(out, ref, act, f"quantized_matmul {M}x{N}x{K}", mae_rel=True)
     if path == "gemm":
-        wd = O.round_act(O.dequantize(wq, s, b, gs), act)
+        wd = O.round_act(O.dequantize(wq, s, b, gs), "float16")
         ref = O.round_act(np.asarray(a, np.float64) @ wd.T, act)
     same = np.mean(to_np(out) == ref)
     assert same > 0.9, f"{path}: {same:.3f} of the outputs equal the rounded exact result"
@@ -296,7 +296,8 @@ def test_moe_30b_decode(T):
 def test_moe_235b_decode():
     """H4096 I1536: gate/up through the eight-group slice GEMV (KS 8), down
     through six-group slices in four k-slices."""
-    x, w = _moe_case(300, 32, 4096, 128, 1536, "bfloat16")
+    w = _packed_weights(300, 4096, 128, 1536, "bfloat16")
+    x = O.round_act(np.random.default_rng(303).standard_normal((32, 4096)), "bfloat16")
     _check_moe(x, w, 8, True, "bfloat16", 64, "decode")
 
 
@@ -360,10 +361,100 @@ def test_moe_skewed_routing(regime):
     _check_moe(x, w, 4, True, "bfloat16", 64, regime)
 
 
-def test_moe_30b_prefill_sampled_rows():
-    """T=512 through the prefill GEMM, every row checked; T=4096 rows sampled."""
+def test_moe_30b_prefill_512_all_rows():
+    """T=512 at the 30B shape through the prefill GEMM, every row checked."""
     x, w = _moe_case(200, 512, 2048, 128, 768, "bfloat16")
     _check_moe(x, w, 8, True, "bfloat16", 64, "prefill")
+
+
+# Large prefill batches (test_moe.py:93-131 pattern: ids compared exactly,
+# outputs within tolerance).  Routing and the dispatch permutation are checked
+# for every token; the block output on sampled rows: every row of the first
+# and last 128-row tile of the most popular expert (its first and last GEMM
+# m-tiles) and a random sample of the rest.
+_WEIGHTS = {}
+
+
+def _packed_weights(seed, H, E, I, act, gs=64):
+    key = (seed, H, E, I, act, gs)
+    if key not in _WEIGHTS:
+        # (30B: 0.3 GB packed, 235B: 1.2 GB; the tests of a shape share them)
+        _WEIGHTS[key] = O.make_packed_inputs(seed, 1, H, E, I, act, gs)[1]
+    return _WEIGHTS[key]
+
+
+def _zipf_router(seed, H, E, act, s=1.1, gs=64):
+    """Zipf(s) expert popularity: with one 64-wide activation group held at 1.0,
+    the first group of router row e holds log(p_e) / 64 (p_e ~ e^-s), so that
+    group adds log-popularity offsets to the logits.  A token picks an expert
+    at most once, so the most popular experts saturate near one pick per token
+    (the capped Zipf of the 30B-A3B prefill workload)."""
+    rng = np.random.default_rng(seed)
+    wr = O.round_act(rng.standard_normal((E, H)) * 0.02, act)
+    p = np.arange(1, E + 1, dtype=np.float64) ** -s
+    wr[:, :64] = O.round_act(np.log(p / p.sum())[:, None] / 64.0, act)
+    return O.quantize(wr, gs, 4, act)
+
+
+def _prefill_rows(ids, E, T, seed, n_random=48, tile=128):
+    counts = np.bincount(ids.reshape(-1), minlength=E)
+    hot = int(np.argmax(counts))
+    toks = np.nonzero((ids == hot).any(axis=1))[0]  # ascending: its slot order
+    last = len(toks) - ((len(toks) - 1) % tile + 1)
+    rng = np.random.default_rng(seed)
+    rows = np.concatenate([toks[:tile], toks[last:], rng.integers(0, T, n_random)])
+    return np.unique(rows), counts
+
+
+def _check_prefill(x, w, k, act, gs, seed):
+    from nano_vllm_metal_amd import route_and_dispatch
+
+    T = x.shape[0]
+    E = w["router"][0].shape[0]
+    _, _, ids_ref, sc_ref = O.route_topk(x, *w["router"], gs, k, True, act)
+    off_ref, srt_ref = O.dispatch(ids_ref, E)
+    xt = to_act(x, act, DEV)
+    moe = make_moe(w, act, gs, k, True, DEV)
+    y, ids, scores = moe.forward(xt, return_routing=True)
+    ids2, _, off, srt = route_and_dispatch(xt, moe.w_router, k, True)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy(), ids_ref), "ids differ"
+    assert np.array_equal(to_np(scores), sc_ref), "scores differ"
+    assert np.array_equal(ids2.cpu().numpy(), ids_ref), "route_and_dispatch ids differ"
+    assert np.array_equal(off.cpu().numpy(), off_ref), "expert offsets differ"
+    assert np.array_equal(srt.cpu().numpy(), srt_ref), "dispatch permutation differs"
+    rows, counts = _prefill_rows(ids_ref, E, T, seed)
+    y_ref, _, _ = O.moe_forward(x[rows], w, k, True, act, gs)
+    stats = assert_moe_close(to_np(y)[rows], y_ref, act, f"prefill T={T}")
+    print(f"prefill T={T}: {len(rows)} rows checked, expert load max/mean "
+          f"{counts.max() / counts.mean():.1f}, {stats}", flush=True)
+    return counts
+
+
+@pytest.mark.parametrize("routing", ["uniform", "zipf"])
+def test_moe_30b_prefill_4096(routing):
+    """The 30B-A3B layer at 4096 tokens (the prefill headline workload),
+    uniform and Zipf(1.1) routing; with Zipf the favourite expert fills
+    about 32 m-tiles of the GEMM."""
+    H, E, I, act, gs, T = 2048, 128, 768, "bfloat16", 64, 4096
+    w = dict(_packed_weights(210, H, E, I, act))
+    rng = np.random.default_rng(211)
+    x = O.round_act(rng.standard_normal((T, H)), act)
+    if routing == "zipf":
+        x[:, :64] = 1.0
+        w["router"] = _zipf_router(212, H, E, act)
+    counts = _check_prefill(x, w, 8, act, gs, 213)
+    if routing == "zipf":
+        assert counts.max() >= 10 * counts.mean(), counts.max() / counts.mean()
+
+
+def test_moe_235b_prefill_2048():
+    """The 235B-A22B layer (hidden 4096, intermediate 1536) at 2048 tokens."""
+    H, E, I, act, gs, T = 4096, 128, 1536, "bfloat16", 64, 2048
+    w = _packed_weights(300, H, E, I, act)
+    rng = np.random.default_rng(301)
+    x = O.round_act(rng.standard_normal((T, H)), act)
+    _check_prefill(x, w, 8, act, gs, 302)
 
 
 @pytest.mark.parametrize("T", [32, 200])

@@ -14,6 +14,11 @@ off-by-one in the dispatch offsets) fails it:
   one-hot logits, renormalised scores summing to one;
 * dispatch: brute-force loops, bijection/monotonicity/bincount invariants and
   hypothesis property tests;
+* SwiGLU activation: the reference's stable silu form (activation.py:21-24)
+  evaluated by torch on the CPU in the activation dtype (a different engine
+  whose per-op results are rounded tensors, as MLX's are), plus closed forms
+  (the collapse to exactly 0 for large negative inputs, silu(g) = g for large
+  positive ones) and its measured distance from the exact function;
 * MoE block: a per-token dense loop written independently of moe_forward,
   k = 1 with renormalisation, identical experts;
 * the C restatement (oracle/moe_ref.c) against the numpy oracle.
@@ -33,6 +38,27 @@ from hypothesis import strategies as st
 from oracle import moe_oracle as O
 
 ACTS = ["float16", "bfloat16"]
+
+
+def _silu_torch_act(g, act):
+    """activation.py:21-24 evaluated by torch on the CPU with act tensors:
+    every op of the expression returns a tensor rounded to the act dtype."""
+    import torch
+
+    dt = {"float16": torch.float16, "bfloat16": torch.bfloat16}[act]
+    x = torch.from_numpy(np.ascontiguousarray(g, dtype=np.float32)).to(dt)
+    sig = 1 / (1 + torch.exp(-torch.abs(x)))
+    sig = torch.where(x < 0, 1 - sig, sig)
+    return (x * sig).double().numpy()
+
+
+def _all_act_values(act, lo, hi):
+    """Every act-representable value in [lo, hi]."""
+    b = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+    with np.errstate(invalid="ignore"):
+        v = O.from_bits(b, act)
+    v = v[np.isfinite(v)]
+    return np.unique(v[(v >= lo) & (v <= hi)])
 
 
 # ---------------------------------------------------------------- rounding
@@ -250,6 +276,79 @@ def test_dispatch_properties(ids, E):
         assert np.all(np.diff(srt[off[e]:off[e + 1]]) > 0)
 
 
+# ---------------------------------------------------------------- packed generator
+
+
+def test_random_packed_layout_and_codes():
+    """Codes of the packed-domain generator: code 8w + j of a row sits in bits
+    [4j, 4j + 4) of word w, each drawn from one uniform byte through the
+    inverse-CDF table (byte i -> round(7.5 + Phi^-1((i + .5) / 256) * 15 / 4.8))."""
+    import statistics
+
+    nd = statistics.NormalDist()
+    table = np.array([min(15, max(0, round(7.5 + nd.inv_cdf((i + 0.5) / 256) * 15 / 4.8)))
+                      for i in range(256)])
+    wq, s, b = O.random_packed(np.random.default_rng(5), (3, 7, 128), 64, "bfloat16")
+    draws = np.random.default_rng(5).integers(0, 65536, size=(21, 64), dtype=np.uint16)
+    codes = np.stack([table[draws & 0xFF], table[draws >> 8]], axis=-1).reshape(3, 7, 128)
+    assert np.array_equal(O.unpack_nibbles(wq), codes)
+    assert s.shape == b.shape == (3, 7, 2)
+    assert np.array_equal(O.round_act(s, "bfloat16"), s) and np.all(s != 0)
+
+
+# ---------------------------------------------------------------- SwiGLU activation
+
+
+@pytest.mark.parametrize("act", ACTS)
+def test_silu_act_matches_per_op_act_evaluation(act):
+    """Every act value in [-16, 16]: the oracle's op-by-op silu equals the
+    reference expression evaluated with torch act tensors, except where the
+    two exp implementations round a value lying within float32 error of an
+    act rounding tie."""
+    g = _all_act_values(act, -16.0, 16.0)
+    got = O.silu_act(g, act)
+    ref = _silu_torch_act(g, act)
+    diff = got != ref
+    assert diff.mean() < 2e-3, (act, int(diff.sum()), g[diff][:10])
+    # a mismatch is one act ulp at most
+    ulp = np.abs(ref) * 2.0 ** -(7 if act == "bfloat16" else 10)
+    assert np.all(np.abs(got - ref)[diff] <= ulp[diff] + 1e-30)
+
+
+@pytest.mark.parametrize("act,edge", [("bfloat16", 8), ("float16", 11)])
+def test_silu_act_closed_forms(act, edge):
+    """1 + exp(-|g|) rounds to 1 once exp(-|g|) is below half an act ulp of 1
+    (|g| > edge * ln 2): the reference's sigmoid is then exactly 1 or 0, so
+    silu(g) = g for positive g and exactly 0 for negative g."""
+    g = _all_act_values(act, -60.0, 60.0)
+    far = np.abs(g) > edge * math.log(2.0) + 0.05
+    y = O.silu_act(g, act)
+    assert np.all(y[far & (g > 0)] == g[far & (g > 0)])
+    assert np.all(y[far & (g < 0)] == 0.0)
+    assert O.silu_act(np.array([0.0]), act)[0] == 0.0
+    # the exact function is not zero there: the rounding points matter
+    assert np.all(O.silu(g[far & (g < 0) & (g > -20)]) < 0)
+
+
+@pytest.mark.parametrize("act", ACTS)
+def test_silu_act_distance_from_exact(act):
+    """Positive inputs stay within two act ulps of the exact silu; negative
+    ones carry the error of the rounded 1 - s, largest near g = -3 (several
+    percent in bfloat16), which a single-rounding silu would not show."""
+    g = _all_act_values(act, -8.0, 8.0)
+    y = O.silu_act(g, act)
+    ex = O.silu(g)
+    pos = g > 2.0 ** -13  # (below, silu(g) ~ g/2 is subnormal in float16)
+    ulp = 2.0 ** -(7 if act == "bfloat16" else 10)
+    assert np.all(np.abs(y - ex)[pos] <= 2 * ulp * np.abs(ex)[pos])
+    band = (g > -4) & (g < -2)
+    rel = np.abs(y - ex)[band] / np.abs(ex)[band]
+    if act == "bfloat16":
+        assert rel.max() > 0.01
+    single = O.round_act(ex, act)
+    assert np.any(single[g < 0] != y[g < 0])
+
+
 # ---------------------------------------------------------------- MoE block
 
 
@@ -265,7 +364,7 @@ def _dense_reference(x, w, k, norm, act, gs):
             e = ids[t, j]
             g = O.round_act(O.dequantize(w["gate"][0][e], w["gate"][1][e], w["gate"][2][e], gs) @ x[t], act)
             u = O.round_act(O.dequantize(w["up"][0][e], w["up"][1][e], w["up"][2][e], gs) @ x[t], act)
-            h = O.round_act(g / (1 + np.exp(-g)) * u, act)
+            h = O.round_act(_silu_torch_act(g, act) * u, act)
             d = O.round_act(O.dequantize(w["down"][0][e], w["down"][1][e], w["down"][2][e], gs) @ h, act)
             terms.append(O.round_act(d * scores[t, j], act))
         y[t] = O.round_act(np.sum(terms, axis=0), act)
@@ -290,7 +389,7 @@ def test_moe_top1_renorm_is_expert_output():
         e = ids[t, 0]
         g = O.grouped_expert_linear(x[t:t + 1], *w["gate"], 64, np.array([e]), act)
         u = O.grouped_expert_linear(x[t:t + 1], *w["up"], 64, np.array([e]), act)
-        h = O.round_act(O.silu(g) * u, act)
+        h = O.round_act(_silu_torch_act(g, act) * u, act)
         d = O.grouped_expert_linear(h, *w["down"], 64, np.array([e]), act)
         assert np.array_equal(y[t], d[0])
 
