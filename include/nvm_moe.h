@@ -197,6 +197,30 @@ int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, i
                     void *y, int32_t *ids_out, void *scores_out, int regime,
                     void *workspace, size_t workspace_bytes, nvm_stream_t stream);
 
+/*
+ * nvm_moe_forward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference: it is
+ * nvm_moe_forward with its workspace taken from a static device array of
+ * nvm_moe_scratch_bytes() bytes (32 MiB) that every GPU the library runs on
+ * holds until the process ends.  Calls needing more workspace than that
+ * (nvm_moe_workspace_size) return NVM_ERR_UNSUPPORTED; at the 30B-A3B shape
+ * (hidden 2048, 128 experts, top-8, intermediate 768) that is beyond about
+ * 540 tokens.  The call allocates nothing (no
+ * hipMalloc, no library allocation).  All calls on one GPU share the array:
+ * calls that overlap in time on one GPU (other streams, other threads) race.
+ * Nothing in the array needs to start at zero (the routing kernels reset
+ * the one counter they use).  The current device must be the stream's.
+ */
+int nvm_moe_scratch_bytes(size_t *bytes);
+int nvm_moe_forward_noalloc(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int top_k,
+                            int norm_topk_prob, int group_size, int bits, int dtype,
+                            const uint32_t *wr, const void *sr, const void *br,
+                            const uint32_t *wg, const void *sg, const void *bg,
+                            const uint32_t *wu, const void *su, const void *bu,
+                            const uint32_t *wd, const void *sd, const void *bd, void *y,
+                            int32_t *ids_out, void *scores_out, int regime, nvm_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

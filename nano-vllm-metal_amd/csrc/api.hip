@@ -3,6 +3,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
 
 #include "internal.h"
@@ -199,6 +200,34 @@ int moe_stages(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int to
                const uint32_t *wd, const void *sd, const void *bd, int32_t *ids_out,
                void *scores_out, int regime, void *workspace, size_t workspace_bytes,
                nvm_stream_t stream, MoeWs &ws, uint16_t *&scores);
+
+// Workspace of nvm_moe_forward_noalloc: a file-scope device array, one copy
+// per GPU, held until the process ends.  Host code never uses the array's
+// name as an address: each device's copy is located once with
+// hipGetSymbolAddress and that pointer is what the kernels receive.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch`, located on first use.
+int scratch_for_current_device(void **out) {
+  int dev = -1;
+  NVM_TRY_HIP(hipGetDevice(&dev));
+  NVM_SUPPORTED(dev >= 0 && dev < kMaxDevices, "moe_noalloc: device %d beyond %d", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    NVM_TRY_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    NVM_REQUIRE(p != nullptr, "moe_noalloc: no device address for the scratch array");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return NVM_OK;
+}
 
 }  // namespace
 
@@ -506,6 +535,33 @@ int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, i
     return r;
   if (T == 0) return NVM_OK;
   return nvm_moe_combine(ws.down, scores, T, top_k, H, dtype, y, stream);
+}
+
+int nvm_moe_scratch_bytes(size_t *bytes) {
+  NVM_REQUIRE(bytes, "moe_scratch_bytes: null output");
+  *bytes = kScratchBytes;
+  return NVM_OK;
+}
+
+int nvm_moe_forward_noalloc(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int top_k,
+                            int norm_topk_prob, int group_size, int bits, int dtype,
+                            const uint32_t *wr, const void *sr, const void *br,
+                            const uint32_t *wg, const void *sg, const void *bg,
+                            const uint32_t *wu, const void *su, const void *bu,
+                            const uint32_t *wd, const void *sd, const void *bd, void *y,
+                            int32_t *ids_out, void *scores_out, int regime, nvm_stream_t stream) {
+  NVM_REQUIRE(T >= 0 && H > 0 && I > 0 && E > 0 && top_k > 0, "moe_noalloc: bad shape");
+  if (T == 0) return NVM_OK;
+  const size_t need = carve_moe(nullptr, T, H, I, E, top_k).bytes;
+  NVM_SUPPORTED(need <= kScratchBytes,
+                "moe_noalloc: %lld tokens need %zu bytes of workspace, more than the %zu-byte "
+                "static scratch; use nvm_moe_forward with a workspace",
+                (long long)T, need, kScratchBytes);
+  void *ws = nullptr;
+  if (int r = scratch_for_current_device(&ws)) return r;
+  return nvm_moe_forward(x, T, H, I, E, top_k, norm_topk_prob, group_size, bits, dtype, wr, sr,
+                         br, wg, sg, bg, wu, su, bu, wd, sd, bd, y, ids_out, scores_out, regime,
+                         ws, kScratchBytes, stream);
 }
 
 int nvm_moe_forward_residual_norm(const void *x, int64_t T, int64_t H, int64_t I, int64_t E,

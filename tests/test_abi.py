@@ -97,6 +97,24 @@ def test_forward_empty_batch_is_a_no_op():
     assert _forward(lib, T=0) == 0
 
 
+def test_noalloc_entry_point_validation():
+    """nvm_moe_forward_noalloc: an empty batch is a no-op, and a batch whose
+    workspace exceeds the static array is refused before any device work."""
+    L, lib = _lib()
+    cap = ctypes.c_size_t()
+    assert lib.nvm_moe_scratch_bytes(ctypes.byref(cap)) == 0 and cap.value == 32 << 20
+    p = [1] * 12
+
+    def call(T):
+        return lib.nvm_moe_forward_noalloc(1, T, 2048, 768, 128, 8, 1, 64, 4, 1, *p, 1, None,
+                                           None, 0, None)
+
+    assert call(0) == 0
+    assert call(2048) == L.NVM_ERR_UNSUPPORTED and "static scratch" in _err(lib)
+    assert lib.nvm_moe_forward_noalloc(1, -1, 2048, 768, 128, 8, 1, 64, 4, 1, *p, 1, None, None,
+                                       0, None) == L.NVM_ERR_INVALID
+
+
 def test_operands_beyond_32bit_offsets_are_refused():
     """The kernels address x and the weights through 32-bit buffer offsets:
     larger operands are refused instead of being read as zeros."""
