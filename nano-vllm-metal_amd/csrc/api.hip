@@ -3,6 +3,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 
@@ -121,7 +122,8 @@ MoeWs carve_moe(void *base, int64_t T, int64_t H, int64_t I, int64_t E, int k) {
   Carve c(base);
   MoeWs w;
   const int64_t N = T * k;
-  w.partial = c.take<double>((size_t)nvm::route_splits(T, H, E) * T * E);
+  const int splits = std::max(nvm::route_splits(T, H, E), nvm::decode_route_splits(T, H, E));
+  w.partial = c.take<double>((size_t)splits * T * E);
   w.ids = c.take<int32_t>(N);
   w.scores = c.take<uint16_t>(N);
   w.offsets = c.take<int32_t>(E + 1);
@@ -616,13 +618,47 @@ int moe_stages(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int to
   scores = scores_out ? (uint16_t *)scores_out : ws.scores;
   const int64_t N = T * top_k;
   hipStream_t st = (hipStream_t)stream;
-  if (int r = run_route_dispatch(dtype, x, T, H, wr, sr, br, E, group_size, top_k, norm_topk_prob,
-                                 nullptr, ids, scores, ws.offsets, ws.sorted, ws.partial,
-                                 ws.counts, ws.done, st))
-    return r;
-  if (int r = nvm_moe_expert_gateup(x, T, H, I, E, top_k, group_size, bits, dtype, wg, sg, bg,
-                                    wu, su, bu, ws.offsets, ws.sorted, ws.h, regime, stream))
-    return r;
+  if (nvm::fused_route_supports(T, E, top_k) && use_decode(regime, N, E, H)) {
+    // Decode batches: one launch of float64 partial logits, then the gate/up
+    // product finalises the routing and sorts the pairs in every block's
+    // prologue (block 0 stores ids, scores, offsets and the sorted pairs).
+    NVM_TRY_HIP(nvm::launch_route_partial_decode(dtype, x, T, H, wr, sr, br, E, group_size,
+                                                 ws.partial, st));
+    nvm::GroupedArgs g{};
+    g.act = (const uint16_t *)x;
+    g.act_ld = H;
+    g.act_rows = T;
+    g.a_div = top_k;
+    g.offsets = ws.offsets;
+    g.w0 = wg;
+    g.s0 = (const uint16_t *)sg;
+    g.b0 = (const uint16_t *)bg;
+    g.w1 = wu;
+    g.s1 = (const uint16_t *)su;
+    g.b1 = (const uint16_t *)bu;
+    g.R = (int)I;
+    g.K = (int)H;
+    g.gs = group_size;
+    g.E = (int)E;
+    g.out = ws.h;
+    g.out_ld = I;
+    g.route_part = ws.partial;
+    g.route_splits = nvm::decode_route_splits(T, H, E);
+    g.route_norm = norm_topk_prob;
+    g.r_ids = ids;
+    g.r_scores = scores;
+    g.r_offsets = ws.offsets;
+    g.r_sorted = ws.sorted;
+    if (int r = run_products(dtype, true, true, g, N, st)) return r;
+  } else {
+    if (int r = run_route_dispatch(dtype, x, T, H, wr, sr, br, E, group_size, top_k,
+                                   norm_topk_prob, nullptr, ids, scores, ws.offsets, ws.sorted,
+                                   ws.partial, ws.counts, ws.done, st))
+      return r;
+    if (int r = nvm_moe_expert_gateup(x, T, H, I, E, top_k, group_size, bits, dtype, wg, sg, bg,
+                                      wu, su, bu, ws.offsets, ws.sorted, ws.h, regime, stream))
+      return r;
+  }
   return nvm_moe_expert_down(ws.h, N, H, I, E, group_size, bits, dtype, wd, sd, bd, ws.offsets,
                              ws.sorted, ws.down, regime, stream);
 }

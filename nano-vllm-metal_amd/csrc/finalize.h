@@ -1,0 +1,131 @@
+// Routing finalise of decode batches, as a device building block: from the
+// float64 partial logits of the router, the rest of route_topk
+// (layers/moe.py:37-49) for four tokens per wavefront.
+//
+// The arithmetic is route_finalize_kernel's: the partials of a logit are
+// added in split order and the sum is rounded once to the activation dtype;
+// the softmax of those act logits runs in float64 and each probability is
+// rounded once; top-k takes (probability desc, expert index asc); with
+// norm_topk_prob the scores are rnd(p / rnd(sum of the k probabilities)).
+// A token occupies one 16-lane row of the wavefront, so every reduction is a
+// four-step DPP butterfly inside the row (quad_perm [1,0,3,2], quad_perm
+// [2,3,0,1], row_half_mirror, row_mirror), after which all 16 lanes hold the
+// same value (each step combines a lane with a partner that computes the
+// same pair).
+#pragma once
+
+#include "common.h"
+
+namespace nvm {
+
+constexpr int kRowExperts = 128;  // experts per 16-lane row: 8 per lane
+constexpr int kRowTopK = 16;      // slots per token (one lane each)
+
+template <class Op>
+__device__ __forceinline__ double row_reduce_f64(double v, Op op) {
+  v = op(v, dpp_f64<0xB1>(v));
+  v = op(v, dpp_f64<0x4E>(v));
+  v = op(v, dpp_f64<0x141>(v));
+  return op(v, dpp_f64<0x140>(v));
+}
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));
+  v = max(v, dpp_u32<0x4E>(v));
+  v = max(v, dpp_u32<0x141>(v));
+  return max(v, dpp_u32<0x140>(v));
+}
+
+// Tokens t0 .. t0+3 (row r of the wavefront holds token t0 + r; rows past T
+// compute and store nothing).  part is [T][E][splits] float64; E <= 128,
+// k <= 16.  Slot i of token t goes to s_ids[t*k + i] and s_sc[t*k + i] (act
+// bits).  Every lane of the wavefront must call it.
+template <int DT>
+__device__ __forceinline__ void finalize_rows(const double *__restrict__ part, int splits, int t0,
+                                              int T, int E, int k, int norm, int *s_ids,
+                                              uint16_t *s_sc) {
+  using A = Act<DT>;
+  constexpr int P = A::kPrec, EMIN = A::kEmin;
+  const int lane = threadIdx.x & 63, c = lane & 15;
+  const int t = t0 + (lane >> 4);
+  const bool tok = t < T;
+  // all loads of the lane in flight together; absent tokens/experts read zeros
+  const rsrc_t pr = make_rsrc(part, (uint32_t)((int64_t)T * E * splits * 8));
+  double sum[8];
+  if (splits == 2) {
+    u32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e = c + 16 * j;
+      v[j] = bload16(pr, tok && e < E ? ((t * E + e) * 2) * 8 : kMaskedOffset, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      sum[j] = (0.0 + __builtin_bit_cast(double, u32x2{v[j].x, v[j].y})) +
+               __builtin_bit_cast(double, u32x2{v[j].z, v[j].w});
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum[j] = 0.0;
+    for (int z = 0; z < splits; ++z) {
+      u32x2 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = c + 16 * j;
+        v[j] = bload8(pr, tok && e < E ? ((t * E + e) * splits + z) * 8 : kMaskedOffset, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sum[j] += __builtin_bit_cast(double, v[j]);
+    }
+  }
+  double lg[8];
+  double m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    lg[j] = c + 16 * j < E ? round_f64_to(sum[j], P, EMIN) : -INFINITY;
+    m = fmax(m, lg[j]);
+  }
+  m = row_reduce_f64(m, [](double a, double b) { return fmax(a, b); });
+  double p[8];
+  double s = 0.0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    p[j] = c + 16 * j < E ? exp(lg[j] - m) : 0.0;
+    s += p[j];
+  }
+  s = row_reduce_f64(s, [](double a, double b) { return a + b; });
+  uint32_t key[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int e = c + 16 * j;
+    // probabilities are >= +0, so their bit patterns order like their values;
+    // the low half prefers the lower expert index on ties
+    key[j] = e < E ? ((uint32_t)act_from_f64<DT>(p[j] / s) << 16) | (uint32_t)(0xFFFF - e) : 0u;
+  }
+  int my_id = 0;
+  double my_p = 0.0, psum = 0.0;
+  for (int i = 0; i < k; ++i) {
+    uint32_t best = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) best = max(best, key[j]);
+    best = row_max_u32(best);
+    const int e = 0xFFFF - (int)(best & 0xFFFFu);
+    const double pv = (double)A::to_f32(best >> 16);
+    psum += pv;  // at most k act values: exact in float64
+    if (c == i) {
+      my_id = e;
+      my_p = pv;
+    }
+    if ((e & 15) == c) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j == (e >> 4)) key[j] = 0u;
+    }
+  }
+  if (tok && c < k) {
+    double sc = my_p;
+    if (norm) sc = my_p / round_f64_to(psum, P, EMIN);
+    s_ids[t * k + c] = my_id;
+    s_sc[t * k + c] = act_from_f64<DT>(sc);
+  }
+}
+
+}  // namespace nvm

@@ -43,7 +43,9 @@
 #include <algorithm>
 
 #include "common.h"
+#include "finalize.h"
 #include "internal.h"
+#include "sort.h"
 
 namespace nvm {
 
@@ -150,6 +152,11 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
   constexpr int UPB = !DUAL && DEPTH % 2 == 0 ? 2 : 1, NBUF = 2 * UPB;
   __shared__ int s_orow[NBUF][kChunk];  // output rows of the unit's routed rows
   __shared__ float s_red[NBUF][kMaxNW][NM][4][64];
+  // routing finalised here (route_part): ids, scores and the sorted pairs
+  __shared__ int s_rids[DUAL ? kFusedPairs : 1];
+  __shared__ uint16_t s_rsc[DUAL ? kFusedPairs : 1];
+  __shared__ int s_sorted[DUAL ? kFusedPairs : 1];
+  __shared__ int s_sortws[DUAL ? (kMaxNW + 1) * kRowExperts : 1];
 
   hoist_args(a.act, a.act_ld, a.act_rows, a.a_map, a.a_div, a.offsets, a.w0, a.s0, a.b0, a.w1,
              a.s1, a.b1, a.R, a.K, a.gs, a.E, a.out, a.o_map, a.out_ld, KS, NT);
@@ -158,24 +165,49 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
   const int col = lane & 15, G = lane >> 4;
   const int E = a.E, R = a.R, KW = a.K >> 3, GPR = a.K / a.gs;
   const int gsh = a.gs == 128 ? 1 : 0;
+  // routing finalised in this prologue (uniform)
+  const bool fused = DUAL && a.route_part != nullptr;
 
+  if (fused) {
+    // every block finalises every token (four per wavefront) and sorts the
+    // pairs into expert order in LDS: the offsets land in s_off
+    const int T = (int)a.act_rows, k = a.a_div, n = T * k;
+    for (int t0 = 4 * wv; t0 < T; t0 += 4 * NW)
+      finalize_rows<DT>(a.route_part, a.route_splits, t0, T, E, k, a.route_norm, s_rids, s_rsc);
+    __syncthreads();
+    int nbits = 0;
+    while ((1 << nbits) < E) ++nbits;
+    block_sort([&](int p) { return s_rids[p]; }, n, E, nbits, s_sortws, s_off, s_sorted);
+    __syncthreads();
+    if (blockIdx.x == 0) {
+      // the routing for the stages after this one (down product, combine)
+      for (int i = tid; i < n; i += blockDim.x) {
+        a.r_ids[i] = s_rids[i];
+        a.r_scores[i] = s_rsc[i];
+        a.r_sorted[i] = s_sorted[i];
+      }
+      for (int i = tid; i <= E; i += blockDim.x) a.r_offsets[i] = s_off[i];
+    }
+  }
   if (wv == 0) {
     // every offset in flight at once (one round trip, not one per 64
     // experts), then the chunk counts from LDS
     // (no offsets: one expert over all act_rows rows, the dense product)
     constexpr int kOffRegs = kMaxExperts / 64 + 1;
-    int ov[kOffRegs];
-    if (a.offsets) {
-      const rsrc_t off_r = make_rsrc(a.offsets, (uint32_t)(E + 1) * 4);
+    if (!fused) {
+      int ov[kOffRegs];
+      if (a.offsets) {
+        const rsrc_t off_r = make_rsrc(a.offsets, (uint32_t)(E + 1) * 4);
+#pragma unroll
+        for (int j = 0; j < kOffRegs; ++j)
+          if (64 * j <= E) ov[j] = (int)bload4(off_r, (64 * j + lane) * 4, 0);
+      } else {
+        ov[0] = lane == 1 ? (int)a.act_rows : 0;
+      }
 #pragma unroll
       for (int j = 0; j < kOffRegs; ++j)
-        if (64 * j <= E) ov[j] = (int)bload4(off_r, (64 * j + lane) * 4, 0);
-    } else {
-      ov[0] = lane == 1 ? (int)a.act_rows : 0;
+        if (64 * j <= E && 64 * j + lane <= E) s_off[64 * j + lane] = ov[j];
     }
-#pragma unroll
-    for (int j = 0; j < kOffRegs; ++j)
-      if (64 * j <= E && 64 * j + lane <= E) s_off[64 * j + lane] = ov[j];
     __builtin_amdgcn_wave_barrier();
     int carry = 0;
     for (int e0 = 0; e0 < E; e0 += 64) {
@@ -287,7 +319,7 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
     int arow = -1;
     if (col < cnt) {
       const int sl = slot0 + col;
-      arow = a.a_map ? a.a_map[sl] / a.a_div : sl;
+      arow = fused ? s_sorted[sl] / a.a_div : a.a_map ? a.a_map[sl] / a.a_div : sl;
       my_orow = a.o_map ? a.o_map[sl] : sl;
     }
     // step s of group pair h covers codes 128h + 64(s/2) + 32(G%2) + 16(G/2)

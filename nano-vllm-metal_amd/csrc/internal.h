@@ -31,7 +31,24 @@ struct GroupedArgs {
   uint16_t *out;
   const int32_t *o_map;
   int64_t out_ld;
+  // Routing finalised in the gate/up product's prologue (decode batches,
+  // fused_route_supports): with route_part set, every block finalises the
+  // act_rows tokens from these partial logits [act_rows][E][route_splits]
+  // (top-k = a_div, renormalised when route_norm) and sorts the pairs in LDS;
+  // offsets, a_map and o_map are then not read.  Block 0 writes the routing
+  // for the stages after it: r_ids/r_scores [act_rows * a_div], r_offsets
+  // [E + 1], r_sorted [act_rows * a_div].
+  const double *route_part;
+  int route_splits, route_norm;
+  int32_t *r_ids;
+  uint16_t *r_scores;
+  int32_t *r_offsets, *r_sorted;
 };
+
+// Decode batches whose routing the gate/up product can finalise: at most
+// kFusedPairs pairs, E <= 128 experts, top-k <= 16.
+constexpr int kFusedPairs = 1024;
+bool fused_route_supports(int64_t T, int64_t E, int k);
 
 // Router.  Partial float64 logits over hidden splits, then per-token finalise.
 // With final_act the logits are rounded and stored as act [T, E] directly.
@@ -44,6 +61,13 @@ hipError_t launch_route_partial(int dtype, const void *x, int64_t T, int64_t H, 
 hipError_t launch_route_finalize(int dtype, const double *partial, int splits, int64_t T,
                                  int64_t E, int k, int norm, void *probs, int32_t *ids,
                                  void *scores, hipStream_t st);
+
+// Decode batches of nvm_moe_forward (routed inside the gate/up product, see
+// fused_route_supports): partial logits [T][E][decode_route_splits] float64.
+int decode_route_splits(int64_t T, int64_t H, int64_t E);
+hipError_t launch_route_partial_decode(int dtype, const void *x, int64_t T, int64_t H,
+                                       const uint32_t *wr, const void *sr, const void *br,
+                                       int64_t E, int gs, double *partial, hipStream_t st);
 
 constexpr int kMaxExperts = 512;
 

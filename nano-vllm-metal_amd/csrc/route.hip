@@ -12,6 +12,7 @@
 // weight is within ~2^-40 relative of the exact sum, so the rounded logits,
 // and with them the top-k ids, do not depend on summation order.
 #include "common.h"
+#include "finalize.h"
 #include "internal.h"
 #include "sort.h"
 
@@ -32,32 +33,34 @@ typedef double f64x4 __attribute__((ext_vector_type(4)));
 // lane.  The D fragment of the float64 MFMA is row-interleaved: element i of
 // lane (c, G) is token t0+G+4i of expert e0+c.
 //
-// With `fin` (logits rounded straight to the activation dtype, no partial
-// buffer) the block's four wavefronts take the four hidden splits of one tile
-// and add their float64 partials in LDS, in split order, before rounding.
+// Items are (token tile, expert tile, output split z < splits).  With
+// wpb > 1 a block owns one item and its wpb wavefronts split the item's hidden
+// range further; their float64 partials meet in LDS and are added in
+// wavefront order.  With `fin` (logits rounded straight to the activation
+// dtype, no partial buffer) splits is 1.
 template <int DT, int EB, bool SB_VEC>
-__global__ __launch_bounds__(256) void route_mfma_kernel(
+__global__ __launch_bounds__(512) void route_mfma_kernel(
     const uint16_t *__restrict__ x, int T, int H, const uint32_t *__restrict__ wr,
     const uint16_t *__restrict__ sr, const uint16_t *__restrict__ br, int E, int gs, int KR,
-    int n_tt, int n_eb, int splits, double *__restrict__ part,
+    int n_tt, int n_eb, int splits, int wpb, double *__restrict__ part,
     uint16_t *__restrict__ fin, unsigned *__restrict__ done) {
   using A = Act<DT>;
   constexpr int NC = 8;  // 32-wide chunks per batch; all loads of a batch are in flight together
-  hoist_args(x, T, H, wr, sr, br, E, gs, KR, n_tt, n_eb, splits, part, fin, done);
+  hoist_args(x, T, H, wr, sr, br, E, gs, KR, n_tt, n_eb, splits, wpb, part, fin, done);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   // the finalising launch that follows counts its blocks from zero
   if (done && blockIdx.x == 0 && threadIdx.x == 0) *done = 0u;
-  // in-block splits: one tile per block (uniform exit, the block meets at a
-  // barrier); else one (tile, split) item per wavefront
-  const bool in_block = fin && splits > 1;
+  // in-block splits: one item per block (uniform exit, the block meets at a
+  // barrier); else one item per wavefront
+  const bool in_block = wpb > 1;
   const int item = in_block ? blockIdx.x : blockIdx.x * (blockDim.x >> 6) + wv;
-  if (item >= n_tt * n_eb * (in_block ? 1 : splits)) return;
+  if (item >= n_tt * n_eb * splits) return;
   const int tt = item % n_tt;
   const int eb = (item / n_tt) % n_eb;
-  const int z = in_block ? wv : item / (n_tt * n_eb);
+  const int z = item / (n_tt * n_eb);
   const int col = lane & 15, G = lane >> 4;
   const int t = tt * 16 + col;
-  const int k_begin = z * KR;
+  const int k_begin = (in_block ? z * wpb + wv : z) * KR;
   const int HW = H / 8, GPR = H / gs;
 
   const rsrc_t xr = make_rsrc(x, (uint32_t)((int64_t)T * H * 2));
@@ -144,7 +147,7 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(
 #pragma unroll
     for (int h = 1; h < CH; ++h) acc[b][0] += acc[b][h];
   if (in_block) {
-    // [split][tile b][element i][lane]
+    // [wavefront][tile b][element i][lane]
     extern __shared__ double s_part[];
 #pragma unroll
     for (int b = 0; b < EB; ++b)
@@ -157,7 +160,7 @@ __global__ __launch_bounds__(256) void route_mfma_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         double sum = s_part[((0 * EB + b) * 4 + i) * 64 + lane];
-        for (int zz = 1; zz < splits; ++zz) sum += s_part[((zz * EB + b) * 4 + i) * 64 + lane];
+        for (int w = 1; w < wpb; ++w) sum += s_part[((w * EB + b) * 4 + i) * 64 + lane];
         acc[b][0][i] = sum;
       }
   }
@@ -337,6 +340,7 @@ constexpr int kFinSplits = 4;  // hidden splits of a rounded-logits block (its w
 
 struct RoutePlan {
   int eb, n_tt, n_eb, splits;
+  int wpb = 1;  // wavefronts per item (in-block hidden splits)
 };
 
 // Work split of the router: expert tiles per wavefront and hidden splits
@@ -359,29 +363,49 @@ RoutePlan route_plan(int64_t T, int64_t H, int64_t E) {
   return p;
 }
 
+// Decode batches whose routing the gate/up product finalises (its prologue
+// reads every partial of every token, so few partials per logit): one block
+// per (token tile, expert tile, output split), whose wpb wavefronts split the
+// hidden range again in whole 128-column blocks; 16 sub-splits in all where
+// H allows, at most 8 per block.
+RoutePlan decode_route_plan(int64_t T, int64_t H, int64_t E) {
+  RoutePlan p;
+  p.eb = 1;
+  p.n_tt = (int)((T + 15) / 16);
+  p.n_eb = (int)((E + 15) / 16);
+  int n = 1;
+  const int64_t blocks128 = H % 128 == 0 ? H / 128 : 1;
+  while (n * 2 <= kMaxSplits && blocks128 % (n * 2) == 0) n *= 2;
+  p.wpb = n < 8 ? n : 8;
+  p.splits = n / p.wpb;
+  return p;
+}
+
 template <int DT, int EB>
 hipError_t launch_mfma_t(const void *x, int64_t T, int64_t H, const uint32_t *wr, const void *sr,
                          const void *br, int64_t E, int gs, const RoutePlan &p, double *partial,
                          void *fin, unsigned *done, hipStream_t st) {
-  const bool in_block = fin && p.splits > 1;
+  const bool in_block = p.wpb > 1;
   const int64_t items = (int64_t)p.n_tt * p.n_eb * p.splits;
-  dim3 grid((unsigned)(in_block ? (int64_t)p.n_tt * p.n_eb : (items + 3) / 4));
-  const size_t lds = in_block ? sizeof(double) * kFinSplits * EB * 4 * 64 : 0;
+  dim3 grid((unsigned)(in_block ? items : (items + 3) / 4));
+  dim3 block(in_block ? 64 * p.wpb : 256);
+  const size_t lds = in_block ? sizeof(double) * p.wpb * EB * 4 * 64 : 0;
+  const int64_t KR = H / (p.splits * p.wpb);
   // 8-byte scale loads need 4 groups (group 64) or 2 groups (group 128) of
   // whole dwords at every 256-column batch start
   const int64_t gpr = H / gs;
   const int sb_vec =
-      (H / p.splits) % 256 == 0 && ((gs == 64 && gpr % 4 == 0) || (gs == 128 && gpr % 2 == 0));
+      KR % 256 == 0 && ((gs == 64 && gpr % 4 == 0) || (gs == 128 && gpr % 2 == 0));
   if (sb_vec)
-    hipLaunchKernelGGL((route_mfma_kernel<DT, EB, true>), grid, dim3(256), lds, st,
+    hipLaunchKernelGGL((route_mfma_kernel<DT, EB, true>), grid, block, lds, st,
                        (const uint16_t *)x, (int)T, (int)H, wr, (const uint16_t *)sr,
-                       (const uint16_t *)br, (int)E, gs, (int)(H / p.splits), p.n_tt, p.n_eb,
-                       p.splits, partial, (uint16_t *)fin, done);
+                       (const uint16_t *)br, (int)E, gs, (int)KR, p.n_tt, p.n_eb, p.splits, p.wpb,
+                       partial, (uint16_t *)fin, done);
   else
-    hipLaunchKernelGGL((route_mfma_kernel<DT, EB, false>), grid, dim3(256), lds, st,
+    hipLaunchKernelGGL((route_mfma_kernel<DT, EB, false>), grid, block, lds, st,
                        (const uint16_t *)x, (int)T, (int)H, wr, (const uint16_t *)sr,
-                       (const uint16_t *)br, (int)E, gs, (int)(H / p.splits), p.n_tt, p.n_eb,
-                       p.splits, partial, (uint16_t *)fin, done);
+                       (const uint16_t *)br, (int)E, gs, (int)KR, p.n_tt, p.n_eb, p.splits, p.wpb,
+                       partial, (uint16_t *)fin, done);
   return hipGetLastError();
 }
 
@@ -397,6 +421,19 @@ hipError_t launch_route_t(const void *x, int64_t T, int64_t H, const uint32_t *w
 
 int route_splits(int64_t T, int64_t H, int64_t E) { return route_plan(T, H, E).splits; }
 
+int decode_route_splits(int64_t T, int64_t H, int64_t E) {
+  return decode_route_plan(T, H, E).splits;
+}
+
+hipError_t launch_route_partial_decode(int dtype, const void *x, int64_t T, int64_t H,
+                                       const uint32_t *wr, const void *sr, const void *br,
+                                       int64_t E, int gs, double *partial, hipStream_t st) {
+  const RoutePlan p = decode_route_plan(T, H, E);
+  return dtype == DT_BF16
+             ? launch_mfma_t<DT_BF16, 1>(x, T, H, wr, sr, br, E, gs, p, partial, nullptr, nullptr, st)
+             : launch_mfma_t<DT_F16, 1>(x, T, H, wr, sr, br, E, gs, p, partial, nullptr, nullptr, st);
+}
+
 hipError_t launch_route_partial(int dtype, const void *x, int64_t T, int64_t H,
                                 const uint32_t *wr, const void *sr, const void *br, int64_t E,
                                 int gs, bool final_act, double *partial, void *fin,
@@ -404,13 +441,21 @@ hipError_t launch_route_partial(int dtype, const void *x, int64_t T, int64_t H,
   RoutePlan p = route_plan(T, H, E);
   // rounded logits: the four wavefronts of a block split the hidden range
   // when it is whole 128-column blocks per split
-  if (final_act) p.splits = H % (128 * kFinSplits) == 0 ? kFinSplits : 1;
+  if (final_act) {
+    p.splits = 1;
+    p.wpb = H % (128 * kFinSplits) == 0 ? kFinSplits : 1;
+  }
   return dtype == DT_BF16
              ? launch_route_t<DT_BF16>(x, T, H, wr, sr, br, E, gs, p, partial, fin, done, st)
              : launch_route_t<DT_F16>(x, T, H, wr, sr, br, E, gs, p, partial, fin, done, st);
 }
 
 bool route_fused_dispatch(int64_t T, int k) { return T <= kFusedRouteTokens && T * k <= kSortChunk; }
+
+bool fused_route_supports(int64_t T, int64_t E, int k) {
+  return T >= 1 && T <= kFusedRouteTokens && T * k <= kFusedPairs && E <= kRowExperts &&
+         k <= kRowTopK;
+}
 
 namespace {
 

@@ -57,11 +57,15 @@ def _moe(x, moe, dt, margins=None):
     k = moe.num_experts_per_tok
     sc, ids = torch.sort(probs.float(), dim=-1, descending=True, stable=True)
     if margins is not None and k < E:
-        # gap between the k-th and (k+1)-th probability in units of the act
-        # ulp of the k-th: 0 is a tie broken by expert index, 1 is one ulp
-        ulp = torch.pow(2.0, torch.floor(torch.log2(sc[:, k - 1])) -
-                        (7 if dt == torch.bfloat16 else 10))
-        margins.append(((sc[:, k - 1] - sc[:, k]) / ulp).cpu())
+        # Gap between the logits of the k-th and (k+1)-th expert in units of
+        # the act ulp of the larger: each logit is a rounded act value, so a
+        # tiny change of the layer input moves it by at most one ulp, and a
+        # gap of two ulps or less can change the chosen experts.
+        lk = logits.double().gather(-1, ids[:, k - 1:k])[:, 0]
+        lk1 = logits.double().gather(-1, ids[:, k:k + 1])[:, 0]
+        top = torch.maximum(lk.abs(), lk1.abs()).clamp_min(2.0 ** -100)
+        ulp = torch.pow(2.0, torch.floor(torch.log2(top)) - (7 if dt == torch.bfloat16 else 10))
+        margins.append(((lk - lk1) / ulp).cpu())
     sc, ids = sc[:, :k], ids[:, :k]
     sc = sc.to(dt)
     if moe.norm_topk_prob:
@@ -86,8 +90,8 @@ def reference_logits(model, tokens, margins=None) -> torch.Tensor:
     """``tokens [L]`` -> logits ``[L, vocab]`` (float32) of every position.
 
     With a list ``margins``, each MoE layer appends the per-token gap between
-    its k-th and (k+1)-th routing probability in act ulps (near-ties, where a
-    one-ulp difference in the layer input can change the chosen experts)."""
+    the logits of its k-th and (k+1)-th expert in act ulps (near-ties, where
+    a one-ulp difference in the layer input can change the chosen experts)."""
     from nano_vllm_metal_amd.moe import Moe
 
     c = model.config

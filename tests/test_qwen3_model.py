@@ -289,11 +289,13 @@ def test_generate_at_30b_a3b_dimensions():
     may differ by a few such ulps.  Every generated token must be the
     reference's greedy choice within 2 ulps.  Prefill logits must agree within
     4 ulps per position, except where 128-way routing sits on a near-tie: the
-    act-rounded probabilities can tie, or lie one ulp apart, at the top-k
-    boundary, and a one-ulp difference in the layer input then picks another
-    expert (ties go to the lower index in both).  Such positions are allowed
-    only where the reference shows a near-tie (<= 1 ulp) in some layer, and
-    at most three of them."""
+    router logits are act-rounded values, a one-ulp difference in a layer's
+    input can move a logit by one act ulp (and its probability by about two
+    probability ulps), so where the k-th and (k+1)-th experts' logits lie
+    within two ulps the model and the reference may pick different experts
+    (ties go to the lower index in both).  Such positions are allowed only
+    where the reference shows that near-tie in some layer, and at most three
+    of them."""
     from nano_vllm_metal_amd import LLM, Qwen3Model, SamplingParams, qwen3_30b_a3b_config
     from qwen3_reference import reference_logits
 
@@ -324,9 +326,9 @@ def test_generate_at_30b_a3b_dimensions():
     near = torch.stack(margins).min(0).values
     print("30B-dims prefill: per-position max logit difference (row ulps):",
           [round(float(e), 2) for e in err], flush=True)
-    print("30B-dims prefill: smallest routing margin per position (prob ulps):",
+    print("30B-dims prefill: smallest routing logit margin per position (ulps):",
           [round(float(v), 2) for v in near], flush=True)
     bad = err > 4.0
     assert int(bad.sum()) <= 3, f"{int(bad.sum())} positions beyond 4 ulps"
-    assert bool((near[bad] <= 1.0).all()), "a position beyond 4 ulps without a routing near-tie"
+    assert bool((near[bad] <= 2.0).all()), "a position beyond 4 ulps without a routing near-tie"
     assert float(err.median()) <= 2.0
