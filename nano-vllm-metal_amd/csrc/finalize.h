@@ -15,6 +15,7 @@
 #pragma once
 
 #include "common.h"
+#include "sort.h"
 
 namespace nvm {
 
@@ -37,12 +38,13 @@ __device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
 
 // Tokens t0 .. t0+3 (row r of the wavefront holds token t0 + r; rows past T
 // compute and store nothing).  part is [T][E][splits] float64; E <= 128,
-// k <= 16.  Slot i of token t goes to s_ids[t*k + i] and s_sc[t*k + i] (act
-// bits).  Every lane of the wavefront must call it.
+// k <= 16, T <= 64.  Slot i of token t goes to s_ids[t*k + i] and
+// s_sc[t*k + i] (act bits), and bit t is set in s_mask[expert] (LDS, zeroed
+// by the caller).  Every lane of the wavefront must call it.
 template <int DT>
 __device__ __forceinline__ void finalize_rows(const double *__restrict__ part, int splits, int t0,
                                               int T, int E, int k, int norm, int *s_ids,
-                                              uint16_t *s_sc) {
+                                              uint16_t *s_sc, uint64_t *s_mask) {
   using A = Act<DT>;
   constexpr int P = A::kPrec, EMIN = A::kEmin;
   const int lane = threadIdx.x & 63, c = lane & 15;
@@ -125,7 +127,57 @@ __device__ __forceinline__ void finalize_rows(const double *__restrict__ part, i
     if (norm) sc = my_p / round_f64_to(psum, P, EMIN);
     s_ids[t * k + c] = my_id;
     s_sc[t * k + c] = act_from_f64<DT>(sc);
+    // (an OR commutes: the mask does not depend on the order of the lanes)
+    __hip_atomic_fetch_or(&s_mask[my_id], 1ull << t, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_WORKGROUP);
   }
+}
+
+// The routing of a decode batch (T <= 64 tokens, E <= 128 experts, k <= 16)
+// finalised and sorted inside one block, from the router's partial logits:
+// the result of route_finalize followed by the dispatch sort
+// (layers/moe.py:37-49, 16-17).  A token's k experts are distinct, so the
+// pairs of expert e are one per token that chose it, in token order: with
+// the token set of every expert as a 64-bit mask, the stable rank of pair
+// (t, j) is the number of tokens below t in its expert's mask.
+// Fills s_ids/s_sc [T*k], s_off [E+1] (slot offsets), s_cb [E+1] (exclusive
+// prefix of ceil(count / chunk_rows)) and s_sorted [T*k].  All threads of
+// the block must call it; it ends with a barrier.
+template <int DT>
+__device__ __forceinline__ void route_in_block(const double *__restrict__ part, int splits, int T, int E, int k,
+                               int norm, int chunk_rows, int *s_ids, uint16_t *s_sc,
+                               uint64_t *s_mask, int *s_off, int *s_cb, int *s_sorted) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
+  for (int e = tid; e < E; e += blockDim.x) s_mask[e] = 0ull;
+  __syncthreads();
+  for (int t0 = 4 * wv; t0 < T; t0 += 4 * NW)
+    finalize_rows<DT>(part, splits, t0, T, E, k, norm, s_ids, s_sc, s_mask);
+  __syncthreads();
+  if (wv == 0) {
+    int carry = 0, ccarry = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + lane;
+      const int n = e < E ? __popcll(s_mask[e]) : 0;
+      const int nc = (n + chunk_rows - 1) / chunk_rows;
+      const int inc = wave_incl_scan(n, lane), cinc = wave_incl_scan(nc, lane);
+      if (e < E) {
+        s_off[e] = carry + inc - n;
+        s_cb[e] = ccarry + cinc - nc;
+      }
+      carry += __shfl(inc, 63);
+      ccarry += __shfl(cinc, 63);
+    }
+    if (lane == 0) {
+      s_off[E] = carry;
+      s_cb[E] = ccarry;
+    }
+  }
+  __syncthreads();
+  for (int p = tid; p < T * k; p += blockDim.x) {
+    const int e = s_ids[p], t = p / k;
+    s_sorted[s_off[e] + __popcll(s_mask[e] & ((1ull << t) - 1ull))] = p;
+  }
+  __syncthreads();
 }
 
 }  // namespace nvm

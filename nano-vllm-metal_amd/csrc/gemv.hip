@@ -156,7 +156,7 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
   __shared__ int s_rids[DUAL ? kFusedPairs : 1];
   __shared__ uint16_t s_rsc[DUAL ? kFusedPairs : 1];
   __shared__ int s_sorted[DUAL ? kFusedPairs : 1];
-  __shared__ int s_sortws[DUAL ? (kMaxNW + 1) * kRowExperts : 1];
+  __shared__ uint64_t s_mask[DUAL ? kRowExperts : 1];  // token set of each expert
 
   hoist_args(a.act, a.act_ld, a.act_rows, a.a_map, a.a_div, a.offsets, a.w0, a.s0, a.b0, a.w1,
              a.s1, a.b1, a.R, a.K, a.gs, a.E, a.out, a.o_map, a.out_ld, KS, NT);
@@ -170,15 +170,11 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
 
   if (fused) {
     // every block finalises every token (four per wavefront) and sorts the
-    // pairs into expert order in LDS: the offsets land in s_off
+    // pairs into expert order in LDS: offsets and chunk bases land in s_off
+    // and s_cb
     const int T = (int)a.act_rows, k = a.a_div, n = T * k;
-    for (int t0 = 4 * wv; t0 < T; t0 += 4 * NW)
-      finalize_rows<DT>(a.route_part, a.route_splits, t0, T, E, k, a.route_norm, s_rids, s_rsc);
-    __syncthreads();
-    int nbits = 0;
-    while ((1 << nbits) < E) ++nbits;
-    block_sort([&](int p) { return s_rids[p]; }, n, E, nbits, s_sortws, s_off, s_sorted);
-    __syncthreads();
+    route_in_block<DT>(a.route_part, a.route_splits, T, E, k, a.route_norm, kChunk, s_rids, s_rsc,
+                       s_mask, s_off, s_cb, s_sorted);
     if (blockIdx.x == 0) {
       // the routing for the stages after this one (down product, combine)
       for (int i = tid; i < n; i += blockDim.x) {
@@ -188,26 +184,23 @@ __global__ __launch_bounds__(64 * kMaxNW, kWavesPerSimd) void gemv_kernel(
       }
       for (int i = tid; i <= E; i += blockDim.x) a.r_offsets[i] = s_off[i];
     }
-  }
-  if (wv == 0) {
+  } else if (wv == 0) {
     // every offset in flight at once (one round trip, not one per 64
     // experts), then the chunk counts from LDS
     // (no offsets: one expert over all act_rows rows, the dense product)
     constexpr int kOffRegs = kMaxExperts / 64 + 1;
-    if (!fused) {
-      int ov[kOffRegs];
-      if (a.offsets) {
-        const rsrc_t off_r = make_rsrc(a.offsets, (uint32_t)(E + 1) * 4);
-#pragma unroll
-        for (int j = 0; j < kOffRegs; ++j)
-          if (64 * j <= E) ov[j] = (int)bload4(off_r, (64 * j + lane) * 4, 0);
-      } else {
-        ov[0] = lane == 1 ? (int)a.act_rows : 0;
-      }
+    int ov[kOffRegs];
+    if (a.offsets) {
+      const rsrc_t off_r = make_rsrc(a.offsets, (uint32_t)(E + 1) * 4);
 #pragma unroll
       for (int j = 0; j < kOffRegs; ++j)
-        if (64 * j <= E && 64 * j + lane <= E) s_off[64 * j + lane] = ov[j];
+        if (64 * j <= E) ov[j] = (int)bload4(off_r, (64 * j + lane) * 4, 0);
+    } else {
+      ov[0] = lane == 1 ? (int)a.act_rows : 0;
     }
+#pragma unroll
+    for (int j = 0; j < kOffRegs; ++j)
+      if (64 * j <= E && 64 * j + lane <= E) s_off[64 * j + lane] = ov[j];
     __builtin_amdgcn_wave_barrier();
     int carry = 0;
     for (int e0 = 0; e0 < E; e0 += 64) {
@@ -636,6 +629,7 @@ bool gemv_supports(int K) {
 }
 
 hipError_t launch_gemv(int dtype, bool dual, const GroupedArgs &a, hipStream_t st) {
+  if (gemv3_supports(a.K, a.R, a.E, a.gs)) return launch_gemv3(dtype, dual, a, st);
   GemvShape s;
   if (!gemv_shape(a.K, a.R, s)) return hipErrorInvalidValue;
   if (dtype == DT_BF16)

@@ -1,0 +1,512 @@
+// Decode-regime grouped W4A16 expert products for the common reduction
+// widths (K = 256 NS, NS in {3, 6, 8, 16}: 768, 1536, 2048, 4096).
+//
+// Replaces `mx.gather_qmm` inside grouped_expert_linear (layers/moe.py:21-32)
+// for decode-sized batches, fused with SwiGLU (layers/moe.py:84,
+// layers/activation.py:21-24, op by op: silu_act) for the gate/up pair.  The
+// arithmetic is gemv.hip's (exact M+q codes on v_mfma_f32_16x16x32, groups
+// folded as s * sum x(M+q) + (b - M s) * sum x); what differs is the shape of
+// the work, chosen so that every instruction of the inner loop is weight
+// streaming or its arithmetic:
+//
+// * A work unit is (chunk of up to 16 routed rows of one expert, tile of
+//   weight rows) over the whole reduction dimension, owned by one wavefront:
+//   no partial sums cross wavefronts and the epilogue reads the MFMA
+//   accumulators.  Gate/up units are 16 rows of both matrices; down units
+//   are two 16-row tiles of the one matrix (the same bytes per unit).
+// * The unit's NS steps of 256 reduction columns are unrolled at compile
+//   time, and a register ring of D slots (D | NS) streams the weights, scales
+//   and biases D steps ahead, across unit boundaries (the next unit's
+//   addresses are known when its first slots are requested).  Every slot
+//   issues the same loads (a missing unit reads through masked offsets:
+//   zeros, no traffic), so the compiler's wait counts keep D - 1 slots in
+//   flight.  Step, ring slot and LDS offsets are compile-time constants: the
+//   loop body holds no index arithmetic.
+// * The routed rows are staged in LDS once per block, already in the lane
+//   order of the MFMA A operand, with their 64-wide group sums (the bias
+//   MFMA's A operand).  A block's contiguous unit range spans few chunks;
+//   they are staged together when they fit ("phase"), else in several
+//   phases.  Lanes past a chunk's row count read its last row: an A row
+//   only reaches the same C row, which the epilogue does not store.
+// * A persistent grid (one block of 8 wavefronts per CU) deals the unit list
+//   evenly: block b owns units [bU/n, (b+1)U/n), its wavefronts take them in
+//   turn.
+#include <algorithm>
+
+#include "common.h"
+#include "finalize.h"
+#include "internal.h"
+#include "sort.h"
+
+namespace nvm {
+
+namespace {
+
+constexpr int kW = 8;           // wavefronts per block
+constexpr int kRows = 16;       // routed rows per chunk (MFMA rows)
+constexpr int kMaxRounds = 64;  // chunks per staging phase
+// dynamic LDS for the staged chunks; with the static LDS of the fused-routing
+// gate/up kernel (about 17 KB) within the 160 KB of a CU
+constexpr int kActLds = 136 * 1024;
+// offset of a masked row: with the 4 KB of step offsets added it stays below
+// 2^31 and at or beyond the end of every tensor (gemv3_supports)
+constexpr int kMasked = 0x7FFF0000;
+
+// Bytes per staged routed row: the A operands (2K) and the group sums (K/16),
+// padded to an odd multiple of 16 bytes, so that the 16 rows one lane group
+// reads in an MFMA step fall in distinct 16-byte bank groups.
+constexpr int row_bytes(int K) { return ((2 * K + K / 16 + 31) / 32) * 32 + 16; }
+
+// Exchange of the lower half-wave's words 2-3 with the upper half-wave's
+// words 0-1: afterwards words 0-1 of every lane belong to the first group of
+// the pair and words 2-3 to the second (see gemv.hip).
+__device__ __forceinline__ u32x4 swap_pairs3(u32x4 w) {
+  const auto a = __builtin_amdgcn_permlane32_swap(w.x, w.z, false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(w.y, w.w, false, false);
+  return u32x4{a[0], b[0], a[1], b[1]};
+}
+
+// Position of an A operand inside a staged row: for MFMA step st (0..3) of
+// group pair h (0..1) of slot s, lane group G reads the 16 bytes at
+// (((s * 2 + h) * 4 + st) * 4 + G) * 16.
+__device__ __forceinline__ constexpr int a_offset(int s, int h, int st, int G) {
+  return (((s * 2 + h) * 4 + st) * 4 + G) * 16;
+}
+
+// Value j (0..3) of a step's scale or bias window (four 16-bit values).
+__device__ __forceinline__ uint32_t sb_val(const u32x2 &v, int j) {
+  const uint32_t d = (j & 2) ? v.y : v.x;
+  return (j & 1) ? (d >> 16) : (d & 0xFFFFu);
+}
+
+template <int DT, bool DUAL, int NS>
+__global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, int RT) {
+  using A = Act<DT>;
+  constexpr int D = NS % 4 == 0 ? 4 : 3;  // ring slots
+  static_assert(NS % D == 0, "the ring must divide the steps of a unit");
+  constexpr int K = 256 * NS, KW = K / 8, G64 = K / 64;
+  constexpr int ROWB = row_bytes(K);
+  constexpr int NM = 2;                    // gate and up, or two row tiles
+  constexpr int RU = DUAL ? kRows : 2 * kRows;  // weight rows per unit
+  // 16-byte windows per lane of a weight row's scales (or biases): lane
+  // group G holds groups 8G..8G+7 of window j, 32j + 8G.. of the row
+  constexpr int SBW = (G64 + 31) / 32;
+  // staged rows per phase
+  constexpr int kMaxStagedRows = kActLds / ROWB;
+  static_assert(kMaxStagedRows >= kRows, "one chunk must fit the staging LDS");
+
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ int s_off[kMaxExperts + 1];  // slot offsets of the experts
+  __shared__ int s_cb[kMaxExperts + 1];   // first chunk index of each expert
+  __shared__ int s_round[kMaxRounds][4];  // expert, first slot, rows, first staged row
+  __shared__ int s_nph, s_nrows;          // chunks and staged rows of the current phase
+  __shared__ int s_orow[DUAL ? 1 : kMaxRounds][kRows];  // output rows (single product)
+  // routing finalised here (route_part): ids, scores and the sorted pairs
+  __shared__ int s_rids[DUAL ? kFusedPairs : 1];
+  __shared__ uint16_t s_rsc[DUAL ? kFusedPairs : 1];
+  __shared__ int s_sorted[DUAL ? kFusedPairs : 1];
+  __shared__ uint64_t s_mask[DUAL ? kRowExperts : 1];  // token set of each expert
+
+  hoist_args(a.act, a.act_ld, a.act_rows, a.a_map, a.a_div, a.offsets, a.w0, a.s0, a.b0, a.w1,
+             a.s1, a.b1, a.R, a.gs, a.E, a.out, a.o_map, a.out_ld, RT);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, G = lane >> 4;
+  const int E = a.E, R = a.R;
+  const bool fused = DUAL && a.route_part != nullptr;
+
+  // ---- routing: finalised and sorted here, or the offsets of dispatch
+  if (fused) {
+    const int T = (int)a.act_rows, k = a.a_div, n = T * k;
+    route_in_block<DT>(a.route_part, a.route_splits, T, E, k, a.route_norm, kRows, s_rids, s_rsc,
+                       s_mask, s_off, s_cb, s_sorted);
+    if (blockIdx.x == 0) {
+      // the routing for the stages after this one (down product, combine)
+      for (int i = tid; i < n; i += 64 * kW) {
+        a.r_ids[i] = s_rids[i];
+        a.r_scores[i] = s_rsc[i];
+        a.r_sorted[i] = s_sorted[i];
+      }
+      for (int i = tid; i <= E; i += 64 * kW) a.r_offsets[i] = s_off[i];
+    }
+  } else {
+    // (no offsets: one expert over all act_rows rows, the dense product)
+    for (int i = tid; i <= E; i += 64 * kW)
+      s_off[i] = a.offsets ? a.offsets[i] : (i == 0 ? 0 : (int)a.act_rows);
+    __syncthreads();
+    if (wv == 0) {
+      // chunk bases: exclusive prefix over experts of ceil(rows / 16)
+      int carry = 0;
+      for (int e0 = 0; e0 < E; e0 += 64) {
+        const int e = e0 + lane;
+        const int n = e < E ? (s_off[e + 1] - s_off[e] + kRows - 1) / kRows : 0;
+        const int inc = wave_incl_scan(n, lane);
+        if (e < E) s_cb[e] = carry + inc - n;
+        carry += __shfl(inc, 63);
+      }
+      if (lane == 0) s_cb[E] = carry;
+    }
+    __syncthreads();
+  }
+
+  // ---- the block's share of units [u0, u1); unit u = (chunk u / RT, tile u % RT)
+  const int U = s_cb[E] * RT;
+  int u0, u1;
+  if ((int64_t)U * gridDim.x < (1ll << 31)) {
+    u0 = (int)((unsigned)(blockIdx.x * U) / gridDim.x);
+    u1 = (int)((unsigned)((blockIdx.x + 1) * U) / gridDim.x);
+  } else {
+    u0 = (int)((int64_t)blockIdx.x * U / gridDim.x);
+    u1 = (int)((int64_t)(blockIdx.x + 1) * U / gridDim.x);
+  }
+  if (u1 <= u0) return;  // uniform over the block, before any further barrier
+  const int c_last = (u1 - 1) / RT;
+
+  // whole-tensor descriptors: every expert's rows are reached through 32-bit
+  // offsets (the host keeps E * R * K / 2 below 2 GiB)
+  const int64_t ER = (int64_t)E * R;
+  const rsrc_t w_r[NM] = {make_rsrc(a.w0, (uint32_t)(ER * KW * 4)),
+                          make_rsrc(DUAL ? a.w1 : a.w0, (uint32_t)(ER * KW * 4))};
+  const rsrc_t s_r[NM] = {make_rsrc(a.s0, (uint32_t)(ER * G64 * 2)),
+                          make_rsrc(DUAL ? a.s1 : a.s0, (uint32_t)(ER * G64 * 2))};
+  const rsrc_t b_r[NM] = {make_rsrc(a.b0, (uint32_t)(ER * G64 * 2)),
+                          make_rsrc(DUAL ? a.b1 : a.b0, (uint32_t)(ER * G64 * 2))};
+  const rsrc_t act_r = make_rsrc(a.act, (uint32_t)(a.act_rows * a.act_ld * 2));
+
+  const uint32_t nib_mask = sgpr_const(0x000F000Fu << A::kCodeShift);
+  const uint32_t magic = vgpr_const(A::kMagic2);
+
+  // ring: the weights, two 16-byte loads per matrix and step
+  u32x4 wq[D][NM][2];
+  // per-lane byte offsets of a unit's rows: weights and scale/bias rows
+  struct Addr {
+    int w[NM], sb[NM];
+  };
+  auto issue = [&](int d, int s, const Addr &ad) {
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      wq[d][m][0] = bload16(w_r[m], ad.w[m] + s * 128, 0);
+      wq[d][m][1] = bload16(w_r[m], ad.w[m] + s * 128 + 64, 0);
+    }
+  };
+  // A unit's scales and biases come in whole: one 16-byte load per lane,
+  // matrix and window (each row's values are read once, by its four lane
+  // groups, in full 64-byte segments), one unit ahead of their use.  (Read
+  // per step, the 8-byte values every lane group repeats would take as many
+  // memory requests as the weights.)  Step s reads its four groups from lane
+  // group (s % 8) / 2 of window s / 8 with ds_bpermute.
+  typedef u32x4 SbUnit[NM][SBW];
+  SbUnit su_cur, bu_cur, su_nxt, bu_nxt;
+  auto sb_issue = [&](SbUnit &su, SbUnit &bu, const Addr &ad) {
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int j = 0; j < SBW; ++j) {
+        su[m][j] = bload16(s_r[m], ad.sb[m] + 16 * G + 64 * j, 0);
+        bu[m][j] = bload16(b_r[m], ad.sb[m] + 16 * G + 64 * j, 0);
+      }
+  };
+
+  // the staged rows' activation rows (and, single product, output rows)
+  auto act_row = [&](int sl) {
+    return fused ? s_sorted[sl] / a.a_div : a.a_map ? a.a_map[sl] / a.a_div : sl;
+  };
+  // staging item (staged row gr, 64-wide group g): its 128 bytes, requested
+  // into registers, then written in A-operand order with the group sum.  The
+  // rows of the phase's n chunks are staged one after another.
+  auto stage_load = [&](int item, int tot, int n, u32x4 (&v)[8]) {
+    const bool ok = item < tot;
+    const int gr = ok ? item / G64 : 0, g = item - gr * G64;
+    int r = 0;
+    while (r + 1 < n && s_round[r + 1][3] <= gr) ++r;
+    const int arow = act_row(s_round[r][1] + gr - s_round[r][3]);
+    const int ao = ok ? (int)((int64_t)arow * a.act_ld * 2) + g * 128 : kMasked;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = bload16(act_r, ao + 16 * i, 0);
+  };
+  auto stage_store = [&](int item, int tot, const u32x4 (&v)[8]) {
+    if (item >= tot) return;
+    const int gr = item / G64, g = item - gr * G64;
+    uint8_t *row = smem + gr * ROWB;
+    const int s = g >> 2, h = (g >> 1) & 1, q = g & 1;
+    float gs = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) gs = A::dot2(v[i][j], A::kOne2, gs);
+      // codes 8i..8i+7 of the group go to lane group
+      // Gi = ((i >> 2) & 1) | (((i >> 1) & 1) << 1), MFMA step 2q + (i & 1)
+      const int Gi = ((i >> 2) & 1) | (((i >> 1) & 1) << 1);
+      *(u32x4 *)(row + a_offset(s, h, 2 * q + (i & 1), Gi)) = pair_order(v[i]);
+    }
+    *(float *)(row + 2 * K + 4 * g) = gs;
+  };
+
+  for (int cb = u0 / RT; cb <= c_last;) {
+    // ---- phase: chunks cb .. cb + n - 1, as many as fit the LDS (at least
+    // one); their rows are staged one after another
+    if (wv == 0) {
+      // the chunks cb .. cb + 63 (within the block's range) from the experts
+      // holding them: expert e owns chunks s_cb[e] .. s_cb[e + 1] - 1
+      const int c_end = min(c_last + 1, cb + kMaxRounds);
+      for (int e0 = 0; e0 < E; e0 += 64) {
+        const int e = e0 + lane;
+        if (e < E) {
+          const int c0 = max(s_cb[e], cb), c1 = min(s_cb[e + 1], c_end);
+          for (int ci = c0; ci < c1; ++ci) {
+            const int slot0 = s_off[e] + (ci - s_cb[e]) * kRows;
+            s_round[ci - cb][0] = e;
+            s_round[ci - cb][1] = slot0;
+            s_round[ci - cb][2] = min(kRows, s_off[e + 1] - slot0);
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      const int ci = cb + lane;
+      const int cnt = ci < c_end ? s_round[lane][2] : 0;
+      const int incl = wave_incl_scan(cnt, lane);
+      const bool fits = ci < c_end && (lane == 0 || incl <= kMaxStagedRows);
+      const int n = __popcll(__ballot(fits));
+      if (fits) s_round[lane][3] = incl - cnt;  // first staged row
+      // (every lane takes part in the shuffle: it reads lane n - 1)
+      const int rows = __shfl(incl, n - 1);
+      if (lane == 0) {
+        s_nph = n;
+        s_nrows = rows;
+      }
+    }
+    __syncthreads();
+    const int n = s_nph, tot = s_nrows * G64;
+    if constexpr (!DUAL) {
+      // output rows of the phase's routed rows (single product)
+      for (int i = tid; i < n * kRows; i += 64 * kW) {
+        const int r = i / kRows, c = i - r * kRows;
+        const int sl = s_round[r][1] + c;
+        s_orow[r][c] = c < s_round[r][2] ? (a.o_map ? a.o_map[sl] : sl) : 0;
+      }
+    }
+
+    // ---- this wavefront's units of the phase: a contiguous range [p0, p1).
+    // The wavefronts w and w + 4 of a block share a SIMD: they take ranges
+    // 2w and 2w + 1 of the eight, so that every SIMD gets a quarter of the
+    // units (to one unit).
+    const int ua = max(u0, cb * RT), ub = min(u1, (cb + n) * RT);
+    const int P = ub - ua;
+    auto range_start = [&](int ri) { return ua + (int)((unsigned)(ri * P) / kW); };
+    const int ri = (wv & 3) * 2 + (wv >> 2);
+    const int p0 = range_start(ri), p1 = range_start(ri + 1);
+    // unit u: row offsets of its rows (uniform except the lane's rows; a unit
+    // past the range is masked)
+    auto setup = [&](int u, Addr &ad) {
+      const bool ok = u < p1;
+      const int uu = ok ? u : ua;
+      const int ci = uu / RT, rt = uu - ci * RT;
+      const int e = __builtin_amdgcn_readfirstlane(s_round[ci - cb][0]);
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        const int row = rt * RU + (DUAL ? 0 : kRows * m) + col;
+        const bool rok = ok && row < R;
+        const int er = e * R + row;
+        ad.w[m] = rok ? er * (KW * 4) + 16 * G : kMasked;
+        ad.sb[m] = rok ? er * (G64 * 2) : kMasked;
+      }
+    };
+
+    // Staging, a barrier, then the ring's first D slots.  (Requested before
+    // the staging reads return, the weight misses would hold them up: the
+    // staging would wait behind the ring's whole first burst.)
+    {
+      u32x4 v0[8], v1[8];
+      stage_load(tid, tot, n, v0);
+      stage_load(tid + 64 * kW, tot, n, v1);
+      stage_store(tid, tot, v0);
+      stage_store(tid + 64 * kW, tot, v1);
+      for (int item = tid + 128 * kW; item < tot; item += 64 * kW) {
+        stage_load(item, tot, n, v0);
+        stage_store(item, tot, v0);
+      }
+    }
+    __syncthreads();
+    Addr cur, nxt;
+    setup(p0, cur);
+    setup(p0 + 1, nxt);
+    sb_issue(su_cur, bu_cur, cur);
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue(d, d, cur);
+
+    // unit u's epilogue: lane (c, G) holds routed rows 4G..4G+3 of weight row c
+    auto epilogue = [&](int u, const f32x4 (&o)[NM]) {
+      const int ci = u / RT, r = ci - cb, rt = u - ci * RT;
+      const int slot0 = __builtin_amdgcn_readfirstlane(s_round[r][1]);
+      const int cnt = __builtin_amdgcn_readfirstlane(s_round[r][2]);
+#pragma unroll
+      for (int m = 0; m < (DUAL ? 1 : NM); ++m) {
+        const int row = rt * RU + (DUAL ? 0 : kRows * m) + col;
+        if (row < R) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int t = 4 * G + v;
+            if (t < cnt) {
+              if constexpr (DUAL) {
+                // reference rounding points: gate and up outputs are act
+                // tensors, silu's ops each round (silu_act), and silu(gate) *
+                // up rounds once more (its float32 product is exact)
+                const float gv = round_act<DT>(o[0][v]);
+                const float uv = round_act<DT>(o[1][v]);
+                a.out[(int64_t)(slot0 + t) * a.out_ld + row] = A::from_f32(silu_act<DT>(gv) * uv);
+              } else {
+                a.out[(int64_t)s_orow[r][t] * a.out_ld + row] = A::from_f32(o[m][v]);
+              }
+            }
+          }
+        }
+      }
+    };
+
+    for (int u = p0; u < p1; ++u) {
+      const int ci = u / RT, r = ci - cb;
+      const int cnt = __builtin_amdgcn_readfirstlane(s_round[r][2]);
+      const uint8_t *arow =
+          smem + (__builtin_amdgcn_readfirstlane(s_round[r][3]) + min(col, cnt - 1)) * ROWB;
+      const uint8_t *ab = arow + G * 16;
+      const float *gsum = (const float *)(arow + 2 * K);
+      // the next unit's scales and biases, ahead of its first ring slots
+      sb_issue(su_nxt, bu_nxt, nxt);
+      f32x4 o[NM];
+#pragma unroll
+      for (int m = 0; m < NM; ++m) o[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int d = s % D;
+        // the step's scale and bias windows (groups 4s..4s+3) from lane group
+        // (s % 8) / 2: dwords 2 (s % 2) and 2 (s % 2) + 1 of window s / 8
+        u32x2 sv[NM], bv[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          const int j = s / 8, Gp = (s % 8) / 2, w0 = 2 * (s % 2);
+          const int src = (Gp * 16 + col) * 4;
+          sv[m] = u32x2{(uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)su_cur[m][j][w0]),
+                        (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)su_cur[m][j][w0 + 1])};
+          bv[m] = u32x2{(uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)bu_cur[m][j][w0]),
+                        (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)bu_cur[m][j][w0 + 1])};
+        }
+        // A operands of the step's eight MFMA steps and the group sums of its
+        // four groups, requested before the expansion
+        u32x4 af[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int st = 0; st < 4; ++st) af[h][st] = *(const u32x4 *)(ab + a_offset(s, h, st, 0));
+        const float xb = gsum[4 * s + G];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          u32x4 bop[NM][4];
+#pragma unroll
+          for (int m = 0; m < NM; ++m) {
+            const u32x4 w = swap_pairs3(wq[d][m][h]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              bop[m][j] = nibble_pairs_v<A::kCodeShift>(w[j], nib_mask, magic);
+          }
+          f32x4 acc[NM][2];
+#pragma unroll
+          for (int step2 = 0; step2 < 2; ++step2)
+#pragma unroll
+            for (int m = 0; m < NM; ++m)
+#pragma unroll
+              for (int q = 0; q < 2; ++q)
+                acc[m][q] = A::mfma16(af[h][2 * q + step2], bop[m][2 * q + step2],
+                                      step2 ? acc[m][q] : f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+          for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              const float sc = A::to_f32(sb_val(sv[m], 2 * h + q));
+#pragma unroll
+              for (int v = 0; v < 4; ++v) o[m][v] = fmaf(sc, acc[m][q][v], o[m][v]);
+            }
+        }
+        // bias terms of the step's four groups: lane (c, G) supplies the group
+        // sum of routed row c and (b - M s) of weight row c, group 4s + G
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          const float scv = A::to_f32(sb_val(sv[m], G));
+          const float bvv = A::to_f32(sb_val(bv[m], G));
+          o[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xb, fmaf(-A::kMagic, scv, bvv), o[m], 0, 0,
+                                                      0);
+        }
+        // refill the slot D steps ahead: this unit, or the next one.  The
+        // scheduling barrier keeps each step's requests in that step (the
+        // scheduler would otherwise sink them towards their use and drain
+        // the ring).
+        if (s + D < NS) issue(d, s + D, cur);
+        else issue(d, s + D - NS, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      epilogue(u, o);
+      cur = nxt;
+      setup(u + 2, nxt);
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int j = 0; j < SBW; ++j) {
+          su_cur[m][j] = su_nxt[m][j];
+          bu_cur[m][j] = bu_nxt[m][j];
+        }
+    }
+
+    // every wavefront is done with the staged rows
+    __syncthreads();
+    cb += n;
+  }
+}
+
+}  // namespace
+
+bool gemv3_supports(int K, int R, int E, int gs) {
+  const int NS = K / 256;
+  if (K % 256 || gs != 64 || R <= 0 || E <= 0 || E > kMaxExperts) return false;
+  if (NS != 3 && NS != 6 && NS != 8 && NS != 16) return false;
+  // one chunk of 16 rows fits the staging LDS; 32-bit weight offsets
+  if (kRows * row_bytes(K) > kActLds) return false;
+  return (int64_t)E * R * (K / 2) <= kMasked;
+}
+
+template <int DT, bool DUAL, int NS>
+hipError_t launch_v3(const GroupedArgs &a, hipStream_t st) {
+  const int RU = DUAL ? kRows : 2 * kRows;
+  const int RT = (a.R + RU - 1) / RU;
+  // more than 64 KB of dynamic LDS (once per device; a failure here shows up
+  // as a failed launch below)
+  static bool attr_set[64] = {false};
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !attr_set[dev]) {
+    (void)hipFuncSetAttribute((const void *)&gemv3_kernel<DT, DUAL, NS>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kActLds);
+    attr_set[dev] = true;
+  }
+  hipLaunchKernelGGL((gemv3_kernel<DT, DUAL, NS>), dim3(cu_count()), dim3(64 * kW), kActLds, st,
+                     a, RT);
+  return hipGetLastError();
+}
+
+template <int DT, bool DUAL>
+hipError_t launch_v3_ns(const GroupedArgs &a, hipStream_t st) {
+  switch (a.K / 256) {
+    case 3: return launch_v3<DT, DUAL, 3>(a, st);
+    case 6: return launch_v3<DT, DUAL, 6>(a, st);
+    case 8: return launch_v3<DT, DUAL, 8>(a, st);
+    case 16: return launch_v3<DT, DUAL, 16>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gemv3(int dtype, bool dual, const GroupedArgs &a, hipStream_t st) {
+  if (!gemv3_supports(a.K, a.R, a.E, a.gs)) return hipErrorInvalidValue;
+  if (dtype == DT_BF16)
+    return dual ? launch_v3_ns<DT_BF16, true>(a, st) : launch_v3_ns<DT_BF16, false>(a, st);
+  return dual ? launch_v3_ns<DT_F16, true>(a, st) : launch_v3_ns<DT_F16, false>(a, st);
+}
+
+}  // namespace nvm

@@ -95,6 +95,10 @@ hipError_t launch_dispatch(const int32_t *ids, int64_t n, int64_t E, int32_t *of
 bool gemv_supports(int K);
 int cu_count();  // compute units of the current device
 hipError_t launch_gemv(int dtype, bool dual, const GroupedArgs &a, hipStream_t st);
+// The one-wavefront-per-unit decode products (gemv3.hip): group size 64,
+// K in {768, 1536, 2048, 4096}; launch_gemv takes them when supported.
+bool gemv3_supports(int K, int R, int E, int gs);
+hipError_t launch_gemv3(int dtype, bool dual, const GroupedArgs &a, hipStream_t st);
 constexpr int kGemmBM = 128;   // prefill tile rows (routed pairs)
 constexpr int kGemmBN = 128;   // prefill tile columns per weight matrix
 hipError_t launch_gemm(int dtype, bool dual, const GroupedArgs &a, int64_t max_m_tiles,

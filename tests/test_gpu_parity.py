@@ -293,6 +293,23 @@ def test_moe_30b_decode(T):
     _check_moe(x, w, 8, True, "bfloat16", 64, "auto")
 
 
+@pytest.mark.parametrize("H,I,T_full", [(2048, 768, 64), (4096, 1536, 32)])
+def test_moe_decode_is_batch_invariant(H, I, T_full):
+    """A token's output does not depend on the batch around it: the decode
+    products deal their units (and halves of units) to wavefronts by the
+    batch's routing, but sum every output in one fixed order."""
+    w = _packed_weights(110 if H == 2048 else 300, H, 128, I, "bfloat16")
+    x = O.round_act(np.random.default_rng(111).standard_normal((T_full, H)), "bfloat16")
+    moe = make_moe(w, "bfloat16", 64, 8, True, DEV)
+    moe.regime = "decode"
+    xs = to_act(x, "bfloat16", DEV)
+    full = moe.forward(xs)
+    for T in (1, 5, T_full // 2):
+        part = moe.forward(xs[:T].contiguous())
+        torch.cuda.synchronize()
+        assert torch.equal(part, full[:T]), f"T={T} differs from the first rows of T={T_full}"
+
+
 def test_moe_235b_decode():
     """H4096 I1536: gate/up through the eight-group slice GEMV (KS 8), down
     through six-group slices in four k-slices."""

@@ -250,7 +250,9 @@ def test_graph_decode_matches_eager_logits():
 @pytest.mark.gpu
 def test_generate_sampling_stays_in_filtered_set():
     """Temperature sampling with top-k: every sampled token is among the k
-    most likely of its step (checked by replaying the step), lengths hold."""
+    most likely of its step (checked by replaying the step), lengths hold.
+    bf16 logits tie often; the filter keeps every token whose logit reaches
+    the k-th largest, so a tied token counts as inside."""
     from nano_vllm_metal_amd import LLM, SamplingParams
 
     m = _model(6)
@@ -263,8 +265,9 @@ def test_generate_sampling_stays_in_filtered_set():
         cache.add(0)
         logits = m.forward(torch.tensor([p], device=DEV), cache, [0])
         for t in o.token_ids:
-            top = torch.topk(logits[0].float(), 3).indices.tolist()
-            assert t in top, (t, top)
+            vals = logits[0].float()
+            kth = torch.topk(vals, 3).values[-1]
+            assert vals[t] >= kth, (t, float(vals[t]), torch.topk(vals, 4))
             logits = m.forward(torch.tensor([[t]], device=DEV), cache, [0])
 
 
