@@ -312,9 +312,10 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
       }
     };
 
-    // Staging, a barrier, then the ring's first D slots.  (Requested before
-    // the staging reads return, the weight misses would hold them up: the
-    // staging would wait behind the ring's whole first burst.)
+    // Staging, a barrier, then the ring's first D slots, the first slot of
+    // every wavefront before the others.  (Requested before the staging reads
+    // return, the weight misses would hold them up: the staging would wait
+    // behind the ring's whole first burst.)
     {
       u32x4 v0[8], v1[8];
       stage_load(tid, tot, n, v0);
@@ -331,8 +332,10 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
     setup(p0, cur);
     setup(p0 + 1, nxt);
     sb_issue(su_cur, bu_cur, cur);
+    issue(0, 0, cur);
+    __builtin_amdgcn_s_barrier();
 #pragma unroll
-    for (int d = 0; d < D; ++d) issue(d, d, cur);
+    for (int d = 1; d < D; ++d) issue(d, d, cur);
 
     // unit u's epilogue: lane (c, G) holds routed rows 4G..4G+3 of weight row c
     auto epilogue = [&](int u, const f32x4 (&o)[NM]) {

@@ -38,6 +38,8 @@ typedef double f64x4 __attribute__((ext_vector_type(4)));
 // range further; their float64 partials meet in LDS and are added in
 // wavefront order.  With `fin` (logits rounded straight to the activation
 // dtype, no partial buffer) splits is 1.
+constexpr int kMaxBlockSplits = 8;  // wavefronts of an in-block hidden split
+
 template <int DT, int EB, bool SB_VEC>
 __global__ __launch_bounds__(512) void route_mfma_kernel(
     const uint16_t *__restrict__ x, int T, int H, const uint32_t *__restrict__ wr,
@@ -146,38 +148,43 @@ __global__ __launch_bounds__(512) void route_mfma_kernel(
   for (int b = 0; b < EB; ++b)
 #pragma unroll
     for (int h = 1; h < CH; ++h) acc[b][0] += acc[b][h];
+  auto store = [&](int b, int i, double v) {
+    const int e = (eb * EB + b) * 16 + col;
+    const int tok = tt * 16 + G + 4 * i;
+    if (!e_ok[b] || tok >= T) return;
+    if (fin)
+      fin[(int64_t)tok * E + e] = act_from_f64<DT>(v);
+    else
+      part[((int64_t)tok * E + e) * splits + z] = v;
+  };
   if (in_block) {
-    // [wavefront][tile b][element i][lane]
+    // [wavefront][tile b][element i][lane]; the EB * 4 (tile, element) sums
+    // are dealt over the block's wavefronts, each adding its wpb (<= 8)
+    // partials in wavefront order
     extern __shared__ double s_part[];
 #pragma unroll
     for (int b = 0; b < EB; ++b)
 #pragma unroll
       for (int i = 0; i < 4; ++i) s_part[((wv * EB + b) * 4 + i) * 64 + lane] = acc[b][0][i];
     __syncthreads();
-    if (wv != 0) return;
+    for (int j = wv; j < EB * 4; j += wpb) {
+      const int b = j >> 2, i = j & 3;
+      double v[kMaxBlockSplits];
 #pragma unroll
-    for (int b = 0; b < EB; ++b)
+      for (int w = 0; w < kMaxBlockSplits; ++w)
+        v[w] = w < wpb ? s_part[((w * EB + b) * 4 + i) * 64 + lane] : 0.0;
+      double sum = v[0];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        double sum = s_part[((0 * EB + b) * 4 + i) * 64 + lane];
-        for (int w = 1; w < wpb; ++w) sum += s_part[((w * EB + b) * 4 + i) * 64 + lane];
-        acc[b][0][i] = sum;
-      }
-  }
-#pragma unroll
-  for (int b = 0; b < EB; ++b) {
-    const int e = (eb * EB + b) * 16 + col;
-    if (!e_ok[b]) continue;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int tok = tt * 16 + G + 4 * i;
-      if (tok >= T) continue;
-      if (fin)
-        fin[(int64_t)tok * E + e] = act_from_f64<DT>(acc[b][0][i]);
-      else
-        part[((int64_t)tok * E + e) * splits + z] = acc[b][0][i];
+      for (int w = 1; w < kMaxBlockSplits; ++w)
+        if (w < wpb) sum += v[w];
+      store(b, i, sum);
     }
+    return;
   }
+#pragma unroll
+  for (int b = 0; b < EB; ++b)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store(b, i, acc[b][0][i]);
 }
 
 constexpr int kMaxExpertSlots = 8;  // experts per lane: E <= 512
@@ -376,7 +383,7 @@ RoutePlan decode_route_plan(int64_t T, int64_t H, int64_t E) {
   int n = 1;
   const int64_t blocks128 = H % 128 == 0 ? H / 128 : 1;
   while (n * 2 <= kMaxSplits && blocks128 % (n * 2) == 0) n *= 2;
-  p.wpb = n < 8 ? n : 8;
+  p.wpb = n < kMaxBlockSplits ? n : kMaxBlockSplits;
   p.splits = n / p.wpb;
   return p;
 }
@@ -391,11 +398,13 @@ hipError_t launch_mfma_t(const void *x, int64_t T, int64_t H, const uint32_t *wr
   dim3 block(in_block ? 64 * p.wpb : 256);
   const size_t lds = in_block ? sizeof(double) * p.wpb * EB * 4 * 64 : 0;
   const int64_t KR = H / (p.splits * p.wpb);
-  // 8-byte scale loads need 4 groups (group 64) or 2 groups (group 128) of
-  // whole dwords at every 256-column batch start
+  // 8-byte scale loads (the four values from the batch's first group on)
+  // need that group's value to start a dword in every row: an even group
+  // index at every batch start (a batch of fewer than four groups reads
+  // values past its range and leaves them unused; past the tensor's end the
+  // load reads zeros)
   const int64_t gpr = H / gs;
-  const int sb_vec =
-      KR % 256 == 0 && ((gs == 64 && gpr % 4 == 0) || (gs == 128 && gpr % 2 == 0));
+  const int sb_vec = gpr % 2 == 0 && KR % (2 * gs) == 0;
   if (sb_vec)
     hipLaunchKernelGGL((route_mfma_kernel<DT, EB, true>), grid, block, lds, st,
                        (const uint16_t *)x, (int)T, (int)H, wr, (const uint16_t *)sr,
