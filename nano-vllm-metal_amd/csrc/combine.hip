@@ -59,13 +59,15 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t *__restrict
 
 hipError_t launch_combine(int dtype, const void *down, const void *scores, int64_t T, int k,
                           int64_t H, void *y, hipStream_t st) {
+  // one wavefront per block: a decode batch (32 tokens x 2048) spreads over
+  // 128 CUs instead of 32 (the kernel is one round trip of latency per thread)
   const int64_t work = T * (H / 8);
-  dim3 grid((unsigned)((work + 255) / 256));
+  dim3 grid((unsigned)((work + 63) / 64));
   if (dtype == DT_BF16)
-    hipLaunchKernelGGL(combine_kernel<DT_BF16>, grid, dim3(256), 0, st, (const uint16_t *)down,
+    hipLaunchKernelGGL(combine_kernel<DT_BF16>, grid, dim3(64), 0, st, (const uint16_t *)down,
                        (const uint16_t *)scores, T, k, H, (uint16_t *)y);
   else
-    hipLaunchKernelGGL(combine_kernel<DT_F16>, grid, dim3(256), 0, st, (const uint16_t *)down,
+    hipLaunchKernelGGL(combine_kernel<DT_F16>, grid, dim3(64), 0, st, (const uint16_t *)down,
                        (const uint16_t *)scores, T, k, H, (uint16_t *)y);
   return hipGetLastError();
 }
