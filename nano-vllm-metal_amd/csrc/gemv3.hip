@@ -79,7 +79,9 @@ __device__ __forceinline__ uint32_t sb_val(const u32x2 &v, int j) {
   return (j & 1) ? (d >> 16) : (d & 0xFFFFu);
 }
 
-template <int DT, bool DUAL, int NS>
+// FUSED: the gate/up product that finalises the routing in its prologue
+// (a distinct instance, so that profiles tell the two apart).
+template <int DT, bool DUAL, int NS, bool FUSED>
 __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, int RT) {
   using A = Act<DT>;
   constexpr int D = NS % 4 == 0 ? 4 : 3;  // ring slots
@@ -101,11 +103,12 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
   __shared__ int s_round[kMaxRounds][4];  // expert, first slot, rows, first staged row
   __shared__ int s_nph, s_nrows;          // chunks and staged rows of the current phase
   __shared__ int s_orow[DUAL ? 1 : kMaxRounds][kRows];  // output rows (single product)
+  static_assert(!FUSED || DUAL, "only the gate/up product finalises the routing");
   // routing finalised here (route_part): ids, scores and the sorted pairs
-  __shared__ int s_rids[DUAL ? kFusedPairs : 1];
-  __shared__ uint16_t s_rsc[DUAL ? kFusedPairs : 1];
-  __shared__ int s_sorted[DUAL ? kFusedPairs : 1];
-  __shared__ uint64_t s_mask[DUAL ? kRowExperts : 1];  // token set of each expert
+  __shared__ int s_rids[FUSED ? kFusedPairs : 1];
+  __shared__ uint16_t s_rsc[FUSED ? kFusedPairs : 1];
+  __shared__ int s_sorted[FUSED ? kFusedPairs : 1];
+  __shared__ uint64_t s_mask[FUSED ? kRowExperts : 1];  // token set of each expert
 
   hoist_args(a.act, a.act_ld, a.act_rows, a.a_map, a.a_div, a.offsets, a.w0, a.s0, a.b0, a.w1,
              a.s1, a.b1, a.R, a.gs, a.E, a.out, a.o_map, a.out_ld, RT);
@@ -113,10 +116,10 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, G = lane >> 4;
   const int E = a.E, R = a.R;
-  const bool fused = DUAL && a.route_part != nullptr;
+  constexpr bool fused = FUSED;
 
   // ---- routing: finalised and sorted here, or the offsets of dispatch
-  if (fused) {
+  if constexpr (fused) {
     const int T = (int)a.act_rows, k = a.a_div, n = T * k;
     route_in_block<DT>(a.route_part, a.route_splits, T, E, k, a.route_norm, kRows, s_rids, s_rsc,
                        s_mask, s_off, s_cb, s_sorted);
@@ -476,7 +479,7 @@ bool gemv3_supports(int K, int R, int E, int gs) {
   return (int64_t)E * R * (K / 2) <= kMasked;
 }
 
-template <int DT, bool DUAL, int NS>
+template <int DT, bool DUAL, int NS, bool FUSED>
 hipError_t launch_v3(const GroupedArgs &a, hipStream_t st) {
   const int RU = DUAL ? kRows : 2 * kRows;
   const int RT = (a.R + RU - 1) / RU;
@@ -485,22 +488,30 @@ hipError_t launch_v3(const GroupedArgs &a, hipStream_t st) {
   static bool attr_set[64] = {false};
   int dev = 0;
   if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !attr_set[dev]) {
-    (void)hipFuncSetAttribute((const void *)&gemv3_kernel<DT, DUAL, NS>,
+    (void)hipFuncSetAttribute((const void *)&gemv3_kernel<DT, DUAL, NS, FUSED>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, kActLds);
     attr_set[dev] = true;
   }
-  hipLaunchKernelGGL((gemv3_kernel<DT, DUAL, NS>), dim3(cu_count()), dim3(64 * kW), kActLds, st,
-                     a, RT);
+  hipLaunchKernelGGL((gemv3_kernel<DT, DUAL, NS, FUSED>), dim3(cu_count()), dim3(64 * kW), kActLds,
+                     st, a, RT);
   return hipGetLastError();
+}
+
+template <int DT, bool DUAL, int NS>
+hipError_t launch_v3_f(const GroupedArgs &a, hipStream_t st) {
+  if constexpr (DUAL) {
+    if (a.route_part) return launch_v3<DT, true, NS, true>(a, st);
+  }
+  return launch_v3<DT, DUAL, NS, false>(a, st);
 }
 
 template <int DT, bool DUAL>
 hipError_t launch_v3_ns(const GroupedArgs &a, hipStream_t st) {
   switch (a.K / 256) {
-    case 3: return launch_v3<DT, DUAL, 3>(a, st);
-    case 6: return launch_v3<DT, DUAL, 6>(a, st);
-    case 8: return launch_v3<DT, DUAL, 8>(a, st);
-    case 16: return launch_v3<DT, DUAL, 16>(a, st);
+    case 3: return launch_v3_f<DT, DUAL, 3>(a, st);
+    case 6: return launch_v3_f<DT, DUAL, 6>(a, st);
+    case 8: return launch_v3_f<DT, DUAL, 8>(a, st);
+    case 16: return launch_v3_f<DT, DUAL, 16>(a, st);
     default: return hipErrorInvalidValue;
   }
 }
