@@ -507,6 +507,21 @@ def attention_bench(dev):
         out[f"B{B}_ctx{ctx}"] = {"us": us, "kv_bytes": kv_bytes, "gbs": kv_bytes / us / 1e3,
                                  "frac_hbm": kv_bytes / us / 1e3 / HBM_PEAK_GBS}
         del q, kp, vp, bt
+    # the initial-prefill causal attention at the e2e shape: 8 requests x 1024
+    # tokens (flops of the visible half: 2 products of 2 L^2/2 D per head)
+    from nano_vllm_metal_amd.attention import causal_attention
+
+    B, L = 8, 1024
+    g = torch.Generator(device=dev).manual_seed(11)
+    q = torch.randn(B, L, Hq, D, device=dev, generator=g).to(torch.bfloat16).float()
+    k = torch.randn(B, L, Hkv, D, device=dev, generator=g).to(torch.bfloat16).float()
+    v = torch.randn(B, L, Hkv, D, device=dev, generator=g).to(torch.bfloat16).float()
+    us = _graph_us(lambda: causal_attention(q, k, v, D ** -0.5, torch.bfloat16,
+                                            out_dtype=torch.bfloat16))
+    flops = 2.0 * B * Hq * L * (L + 1) * D * 2 / 2
+    out[f"prefill_causal_B{B}_L{L}"] = {"us": us, "tflops": flops / us / 1e6,
+                                        "frac_mfma": flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS}
+    del q, k, v
     return out
 
 

@@ -65,6 +65,28 @@ int nvm_paged_attention(const float *q, int64_t N, int64_t L, int64_t D, const v
                         int num_kv_heads, int num_heads, int out_dtype, void *out,
                         void *workspace, size_t workspace_bytes, nvm_stream_t stream);
 
+/*
+ * Causal attention of an initial prefill: every request attends over its own
+ * new tokens only.  Replaces the float32
+ * `mx.fast.scaled_dot_product_attention(q, k, v, scale, mask="causal")` of
+ * the model's initial prefill (models/qwen3.py:134-141).
+ *
+ *   q    [B * L, num_heads, D] float32
+ *   k, v [B * L, num_kv_heads, D] float32
+ *   out  [B * L, num_heads, D] of out_dtype (NVM_KV_F32, NVM_KV_BF16 or
+ *        NVM_KV_F16: the float32 result rounded once)
+ *
+ * Token row b * L + i is position i of request b; query row i sees key rows
+ * j <= i of its request, query head h reads kv head h / (num_heads /
+ * num_kv_heads).  q, k and v must hold values of the activation dtype `dtype`
+ * (NVM_DTYPE_BF16 or NVM_DTYPE_F16; the model's q/k norm and RoPE round
+ * them): the products are then exact, the sums float32.  D of 64 or 128 and
+ * 1, 2, 4, 8 or 16 query heads per kv head (else NVM_ERR_UNSUPPORTED).
+ */
+int nvm_causal_attention(const float *q, const float *k, const float *v, int64_t B, int64_t L,
+                         int num_heads, int num_kv_heads, int64_t D, float scale, int dtype,
+                         int out_dtype, void *out, nvm_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

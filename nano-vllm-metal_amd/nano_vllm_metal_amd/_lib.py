@@ -55,6 +55,7 @@ SIGNATURES = {
                                            ctypes.POINTER(_SZ)],
     "nvm_paged_attention": [_P, _I64, _I64, _I64, _P, _P, _I64, _I64, _I, _P, _P, _P, _I64, _I64,
                             _P, ctypes.c_float, _I, _I, _I, _I, _P, _P, _SZ, _P],
+    "nvm_causal_attention": [_P, _P, _P, _I64, _I64, _I, _I, _I64, ctypes.c_float, _I, _I, _P, _P],
     "nvm_residual_rms_norm": [_P, _P, _P, _I64, _I64, ctypes.c_float, _I, _P, _P, _P],
     "nvm_qk_norm_rope_store": [_P, _I64, _I, _I, _I64, _P, _P, ctypes.c_float, _P, _P, _P, _I64,
                                _P, _P, _P, _P, _I64, _I64, _I, _P, _P, _P, _P],

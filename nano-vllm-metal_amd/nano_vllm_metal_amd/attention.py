@@ -83,3 +83,43 @@ def paged_attention(query: torch.Tensor, key_pages: torch.Tensor, value_pages: t
         out.data_ptr(), ws.data_ptr(),
         size.value, _lib.stream_of(dev)))
     return out.reshape(B, Hq, L, D)
+
+
+def causal_attention_supports(num_heads: int, num_kv_heads: int, head_dim: int) -> bool:
+    """Shapes of the causal prefill kernel: head dim 64 or 128 and 1, 2, 4, 8
+    or 16 query heads per kv head."""
+    r = num_heads // num_kv_heads if num_kv_heads > 0 else 0
+    return head_dim in (64, 128) and num_heads % max(num_kv_heads, 1) == 0 and r in (1, 2, 4, 8, 16)
+
+
+def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
+                     act_dtype: torch.dtype, out_dtype: torch.dtype = torch.float32
+                     ) -> torch.Tensor:
+    """Causal attention of an initial prefill, the float32
+    ``scaled_dot_product_attention(q, k, v, scale, mask="causal")`` of
+    ``models/qwen3.py:134-141``: ``q [B, L, num_heads, D]``, ``k, v
+    [B, L, num_kv_heads, D]`` float32 holding ``act_dtype`` values (bf16 or
+    f16, as the q/k norm and RoPE step leaves them); query i sees keys j <= i
+    of its own request.  Returns ``[B, L, num_heads, D]`` of ``out_dtype``
+    (float32, or that result rounded once to bf16/f16)."""
+    lib = _lib.load()
+    if q.dim() != 4 or k.dim() != 4 or v.shape != k.shape:
+        raise ValueError("causal_attention: q [B, L, Hq, D], k and v [B, L, Hkv, D]")
+    B, L, Hq, D = q.shape
+    if k.shape[0] != B or k.shape[1] != L or k.shape[3] != D:
+        raise ValueError("causal_attention: q, k and v must share batch, length and head dim")
+    Hkv = k.shape[2]
+    if Hq % Hkv:
+        raise ValueError("causal_attention: num_heads must be divisible by num_kv_heads")
+    if out_dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise ValueError(f"causal_attention: unsupported out_dtype {out_dtype}")
+    dev = _lib.require_device(q, k, v)
+    qc = q.to(torch.float32).contiguous()
+    kc = k.to(torch.float32).contiguous()
+    vc = v.to(torch.float32).contiguous()
+    out = torch.empty((B, L, Hq, D), dtype=out_dtype, device=dev)
+    _lib.check(lib.nvm_causal_attention(
+        qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), B, L, Hq, Hkv, D, float(scale),
+        _lib.dtype_code(act_dtype), _lib.KV_DTYPE_CODES[out_dtype], out.data_ptr(),
+        _lib.stream_of(dev)))
+    return out

@@ -30,9 +30,8 @@ from pathlib import Path
 from typing import List, Optional, Sequence
 
 import torch
-import torch.nn.functional as F
 
-from .attention import paged_attention
+from .attention import causal_attention, causal_attention_supports, paged_attention
 from .fused import moe_residual_rms_norm, qk_norm_rope_store, residual_rms_norm
 from .kv_cache import PagedKVCache
 from .linear import QuantizedWeights, dequantize, quantized_linear
@@ -186,19 +185,20 @@ class Qwen3Model:
                                      step.positions, self.rope.cos, self.rope.sin, step.page_ids,
                                      step.slots, cache.key_pages[li], cache.value_pages[li],
                                      want_kv=step.initial)
-        q = q.view(B, L, Hq, D).transpose(1, 2)
         scale = D ** -0.5
-        if step.initial:
+        if step.initial and causal_attention_supports(Hq, Hkv, D):
             # every request starts from an empty cache: causal attention over
-            # the new tokens only (models/qwen3.py:134-141)
-            kf = k.view(B, L, Hkv, D).transpose(1, 2).repeat_interleave(Hq // Hkv, dim=1)
-            vf = v.view(B, L, Hkv, D).transpose(1, 2).repeat_interleave(Hq // Hkv, dim=1)
-            o = F.scaled_dot_product_attention(q, kf, vf, is_causal=True, scale=scale)
+            # the new tokens only (models/qwen3.py:134-141); the grouped query
+            # heads share each key/value read
+            o = causal_attention(q.view(B, L, Hq, D), k.view(B, L, Hkv, D), v.view(B, L, Hkv, D),
+                                 scale, self.dtype, out_dtype=x.dtype)
+            o = o.reshape(B, L, Hq * D)
         else:
-            o = paged_attention(q, cache.key_pages[li], cache.value_pages[li], step.block_table,
-                                step.lens, cache.page_size, scale=scale, mask="causal",
-                                out_dtype=x.dtype)
-        o = o.to(x.dtype).transpose(1, 2).reshape(B, L, Hq * D)
+            # (the k/v of an initial step are in the pages as well)
+            o = paged_attention(q.view(B, L, Hq, D).transpose(1, 2), cache.key_pages[li],
+                                cache.value_pages[li], step.block_table, step.lens,
+                                cache.page_size, scale=scale, mask="causal", out_dtype=x.dtype)
+            o = o.transpose(1, 2).reshape(B, L, Hq * D)
         return quantized_linear(o, layer.wo)
 
     # ---------------------------------------------------------------- forward

@@ -200,3 +200,75 @@ def test_output_in_activation_dtype(odt):
         f = paged_attention(q, kp, vp, bt, lens, 16, mask="causal")
         h = paged_attention(q, kp, vp, bt, lens, 16, mask="causal", out_dtype=odt)
         assert h.dtype == odt and torch.equal(h, f.to(odt)), (B, L, ctx)
+
+
+# ------------------------------------------------------------ causal prefill
+
+
+def _causal_case(seed, B, L, Hq, Hkv, D, act):
+    """q [B, L, Hq, D], k, v [B, L, Hkv, D] holding act-dtype values (as the
+    model's q/k norm and RoPE leave them), with the f64 oracle per request."""
+    rng = np.random.default_rng(seed)
+    dt = torch.bfloat16 if act == "bfloat16" else torch.float16
+    q = torch.from_numpy(rng.standard_normal((B, L, Hq, D)).astype(np.float32)).to(dt).float()
+    k = torch.from_numpy(rng.standard_normal((B, L, Hkv, D)).astype(np.float32)).to(dt).float()
+    v = torch.from_numpy(rng.standard_normal((B, L, Hkv, D)).astype(np.float32)).to(dt).float()
+    return q, k, v, dt
+
+
+def _causal_ref(q, k, v, b, h, scale):
+    R = q.shape[2] // k.shape[2]
+    return AO.dense_attention(q[b, :, h].numpy(), k[b, :, h // R].numpy(), v[b, :, h // R].numpy(),
+                              scale, True)
+
+
+@pytest.mark.parametrize("B,L,Hq,Hkv,D,act", [
+    (2, 37, 8, 2, 64, "bfloat16"),     # ragged last query block, R=4
+    (1, 130, 4, 4, 128, "float16"),    # R=1: 16 positions per wavefront
+    (3, 64, 16, 1, 128, "bfloat16"),   # R=16: one position per wavefront
+    (1, 1, 8, 1, 64, "bfloat16"),      # a one-token prompt
+])
+def test_causal_attention_matches_oracle(B, L, Hq, Hkv, D, act):
+    from nano_vllm_metal_amd.attention import causal_attention
+
+    q, k, v, dt = _causal_case(7 + L, B, L, Hq, Hkv, D, act)
+    scale = D ** -0.5
+    out = causal_attention(q.to(DEV), k.to(DEV), v.to(DEV), scale, dt).cpu()
+    for b in range(B):
+        for h in range(Hq):
+            ref = _causal_ref(q, k, v, b, h, scale)
+            np.testing.assert_allclose(out[b, :, h].numpy(), ref, rtol=1e-4, atol=2e-5,
+                                       err_msg=f"b={b} h={h}")
+
+
+def test_causal_attention_30b_heads_8x1024():
+    """The 30B-A3B attention shape of the end-to-end prefill: 8 requests x
+    1024 tokens, 32 query heads over 4 kv heads of dim 128; two requests
+    checked against the oracle head by head, every output finite, and the
+    bf16 output the float32 one rounded once."""
+    from nano_vllm_metal_amd.attention import causal_attention
+
+    B, L, Hq, Hkv, D = 8, 1024, 32, 4, 128
+    q, k, v, dt = _causal_case(1234, B, L, Hq, Hkv, D, "bfloat16")
+    scale = D ** -0.5
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    out = causal_attention(qd, kd, vd, scale, dt)
+    out_bf = causal_attention(qd, kd, vd, scale, dt, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    assert torch.equal(out.to(torch.bfloat16), out_bf)
+    out = out.cpu()
+    for b in (0, 7):
+        for h in range(Hq):
+            ref = _causal_ref(q, k, v, b, h, scale)
+            np.testing.assert_allclose(out[b, :, h].numpy(), ref, rtol=1e-4, atol=2e-5,
+                                       err_msg=f"b={b} h={h}")
+
+
+def test_causal_attention_rejects_unsupported_shapes():
+    from nano_vllm_metal_amd.attention import causal_attention
+
+    q = torch.zeros((1, 4, 6, 96), device=DEV)
+    k = torch.zeros((1, 4, 2, 96), device=DEV)
+    with pytest.raises(ValueError, match="head dim"):
+        causal_attention(q, k, k, 0.1, torch.bfloat16)
