@@ -36,6 +36,7 @@ sys.path.insert(0, str(ROOT / "nano-vllm-metal_amd"))
 
 HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
 MFMA_BF16_PEAK_TFLOPS = 2500.0   # dense bf16 MFMA
+MI355X_XCDS, MI355X_SIMDS = 8, 1024  # 256 CUs of 4 SIMDs in 8 XCDs
 METRIC = "MoE-layer tokens/s + HBM GB/s, 30B-A3B shape, decode B=32 / prefill 4K"
 SHAPE = dict(H=2048, E=128, I=768, k=8, gs=64)
 # Qwen3-235B-A22B's MoE layer (also reported: decode B=32, prefill 2048)
@@ -793,6 +794,31 @@ def rocprof_summary(root: Path, write_traffic: bool) -> str:
             b = kib * 1024.0 * factors[cname]
             traffic.setdefault(k, {})[cname.lower() + "_bytes"] = b
             lines.append(f"  {k:16s} n={len(vals):5d} {kib:12.1f} KiB -> {b / 1e6:9.2f} MB per launch")
+    # the other counters: per key, the median per dispatch; the MFMA busy
+    # fraction where SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE come from one
+    # run (GRBM_GUI_ACTIVE counts the dispatch's cycles once per XCD,
+    # SQ_VALU_MFMA_BUSY_CYCLES sums the busy cycles of every SIMD)
+    other = sorted(c for c in counters if c not in ("FETCH_SIZE", "WRITE_SIZE"))
+    keys = sorted({k for c in other for k in counters[c] if k != "copy"})
+    if keys:
+        lines.append("counters (rocprofv3 --pmc; per key: median per dispatch):")
+    for k in keys:
+        vals = {c: statistics.median(counters[c][k]) for c in other if counters[c].get(k)}
+        n = max(len(counters[c][k]) for c in other if counters[c].get(k))
+        lines.append(f"  {k} (n={n}):")
+        for c, v in vals.items():
+            lines.append(f"    {c:28s} {v:16.0f}")
+        waves = vals.get("SQ_WAVES")
+        if waves:
+            for c in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS"):
+                if c in vals:
+                    lines.append(f"    per wavefront {c:14s} {vals[c] / waves:10.1f}")
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in vals and vals.get("GRBM_GUI_ACTIVE"):
+            cycles = vals["GRBM_GUI_ACTIVE"] / MI355X_XCDS
+            busy = vals["SQ_VALU_MFMA_BUSY_CYCLES"] / (cycles * MI355X_SIMDS)
+            lines.append(f"    MFMA busy {100 * busy:.1f}% = SQ_VALU_MFMA_BUSY_CYCLES / "
+                         f"(GRBM_GUI_ACTIVE / {MI355X_XCDS} XCDs x {MI355X_SIMDS} SIMDs); "
+                         f"{cycles:.0f} cycles per dispatch")
     for k, rec in traffic.items():
         if "fetch_size_bytes" in rec and "write_size_bytes" in rec:
             rec["hbm_bytes_per_launch"] = rec["fetch_size_bytes"] + rec["write_size_bytes"]

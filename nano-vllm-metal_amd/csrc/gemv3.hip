@@ -315,14 +315,20 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
       }
     };
 
-    // Staging, a barrier, then the ring's first D slots, the first slot of
-    // every wavefront before the others.  (Requested before the staging reads
-    // return, the weight misses would hold them up: the staging would wait
-    // behind the ring's whole first burst.)
+    // The first two staging reads, then the first unit's scale/bias window and
+    // ring slot 0 (queued behind those reads, so they do not delay them), the
+    // staging stores and a barrier, then ring slots 1..D-1.  (All D slots
+    // requested ahead of the stores measure no better: later staging reads
+    // would wait behind the ring's whole first burst.)
+    Addr cur, nxt;
+    setup(p0, cur);
+    setup(p0 + 1, nxt);
     {
       u32x4 v0[8], v1[8];
       stage_load(tid, tot, n, v0);
       stage_load(tid + 64 * kW, tot, n, v1);
+      sb_issue(su_cur, bu_cur, cur);
+      issue(0, 0, cur);
       stage_store(tid, tot, v0);
       stage_store(tid + 64 * kW, tot, v1);
       for (int item = tid + 128 * kW; item < tot; item += 64 * kW) {
@@ -331,12 +337,6 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
       }
     }
     __syncthreads();
-    Addr cur, nxt;
-    setup(p0, cur);
-    setup(p0 + 1, nxt);
-    sb_issue(su_cur, bu_cur, cur);
-    issue(0, 0, cur);
-    __builtin_amdgcn_s_barrier();
 #pragma unroll
     for (int d = 1; d < D; ++d) issue(d, d, cur);
 
