@@ -629,9 +629,22 @@ bool gemv_supports(int K) {
 }
 
 hipError_t launch_gemv(int dtype, bool dual, const GroupedArgs &a, hipStream_t st) {
-  if (gemv3_supports(a.K, a.R, a.E, a.gs)) return launch_gemv3(dtype, dual, a, st);
+  // The expert products run on gemv3.  A dense product (one expert, no
+  // offsets) does only when its unit list (16-row chunks x weight-row tiles
+  // of 16 for gate/up, 32 otherwise) gives every wavefront of the grid at
+  // least four units, as the lm head at 32 rows does.  With fewer units this
+  // kernel's split of the reduction over a block's wavefronts keeps more
+  // loads in flight: q_proj (2048 -> 4096) at one row takes 5.7 us here and
+  // 9.4 us on gemv3.
   GemvShape s;
-  if (!gemv_shape(a.K, a.R, s)) return hipErrorInvalidValue;
+  const bool old_ok = gemv_shape(a.K, a.R, s);
+  if (gemv3_supports(a.K, a.R, a.E, a.gs)) {
+    const int RU = dual ? 16 : 32;
+    const int64_t units = (a.act_rows + 15) / 16 * ((a.R + RU - 1) / RU);
+    if (a.offsets || !old_ok || units >= 4 * 8 * (int64_t)cu_count())
+      return launch_gemv3(dtype, dual, a, st);
+  }
+  if (!old_ok) return hipErrorInvalidValue;
   if (dtype == DT_BF16)
     return dual ? launch_t<DT_BF16, true>(a, s, st) : launch_t<DT_BF16, false>(a, s, st);
   return dual ? launch_t<DT_F16, true>(a, s, st) : launch_t<DT_F16, false>(a, s, st);

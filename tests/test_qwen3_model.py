@@ -290,7 +290,9 @@ def test_generate_at_30b_a3b_dimensions():
     largest logit (about 7 here, ulp 2^-5): model and reference round the same
     bf16 tensors at the same points but sum in different orders, so logits
     may differ by a few such ulps.  Every generated token must be the
-    reference's greedy choice within 2 ulps.  Prefill logits must agree within
+    reference's greedy choice within 4 ulps: two logits each off by up to 2
+    ulps (the median bar of the prefill check below) may swap a near-tie of
+    up to 4 ulps.  Prefill logits must agree within
     4 ulps per position, except where 128-way routing sits on a near-tie: the
     router logits are act-rounded values, a one-ulp difference in a layer's
     input can move a logit by one act ulp (and its probability by about two
@@ -318,7 +320,7 @@ def test_generate_at_30b_a3b_dimensions():
             worst = max(worst, float((ref[pos].max() - ref[pos, t]) / ulp[pos]))
     print(f"30B-dims generate: worst reference logit gap of a chosen token {worst:.3g} ulps",
           flush=True)
-    assert worst <= 2.0
+    assert worst <= 4.0
 
     cache = m.create_kv_cache(8, page_size=16)
     cache.add(0)
