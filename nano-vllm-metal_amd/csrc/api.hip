@@ -192,6 +192,60 @@ int run_products(int dtype, bool decode, bool dual, nvm::GroupedArgs &g, int64_t
   return NVM_OK;
 }
 
+// Arguments of the gate/up product: sorted slot n reads token row
+// sorted[n] / top_k of x and writes row n of h [pairs, I].
+nvm::GroupedArgs gateup_args(const void *x, int64_t T, int64_t H, int64_t I, int64_t E,
+                             int top_k, int group_size, const uint32_t *wg, const void *sg,
+                             const void *bg, const uint32_t *wu, const void *su, const void *bu,
+                             const int32_t *offsets, const int32_t *sorted, void *h) {
+  nvm::GroupedArgs g{};
+  g.act = (const uint16_t *)x;
+  g.act_ld = H;
+  g.act_rows = T;
+  g.a_map = sorted;
+  g.a_div = top_k;
+  g.offsets = offsets;
+  g.w0 = wg;
+  g.s0 = (const uint16_t *)sg;
+  g.b0 = (const uint16_t *)bg;
+  g.w1 = wu;
+  g.s1 = (const uint16_t *)su;
+  g.b1 = (const uint16_t *)bu;
+  g.R = (int)I;
+  g.K = (int)H;
+  g.gs = group_size;
+  g.E = (int)E;
+  g.out = (uint16_t *)h;
+  g.o_map = nullptr;
+  g.out_ld = I;
+  return g;
+}
+
+// Arguments of the down product: sorted slot n reads row n of h and writes
+// row sorted[n] (the flat pair index) of down [pairs, H].
+nvm::GroupedArgs down_args(const void *h, int64_t n_pairs, int64_t H, int64_t I, int64_t E,
+                           int group_size, const uint32_t *wd, const void *sd, const void *bd,
+                           const int32_t *offsets, const int32_t *sorted, void *down) {
+  nvm::GroupedArgs d{};
+  d.act = (const uint16_t *)h;
+  d.act_ld = I;
+  d.act_rows = n_pairs;
+  d.a_map = nullptr;
+  d.a_div = 1;
+  d.offsets = offsets;
+  d.w0 = wd;
+  d.s0 = (const uint16_t *)sd;
+  d.b0 = (const uint16_t *)bd;
+  d.R = (int)H;
+  d.K = (int)I;
+  d.gs = group_size;
+  d.E = (int)E;
+  d.out = (uint16_t *)down;
+  d.o_map = sorted;
+  d.out_ld = H;
+  return d;
+}
+
 // Routing, dispatch and both expert products of the block (everything but
 // the combine), on the caller's workspace; `scores` is where the routing
 // scores went.
@@ -455,26 +509,8 @@ int nvm_moe_expert_gateup(const void *x, int64_t T, int64_t H, int64_t I, int64_
   NVM_REQUIRE(x && wg && sg && bg && wu && su && bu && expert_offsets && sorted_pairs && h,
               "expert_gateup: null pointer");
   if (T == 0) return NVM_OK;
-  nvm::GroupedArgs g{};
-  g.act = (const uint16_t *)x;
-  g.act_ld = H;
-  g.act_rows = T;
-  g.a_map = sorted_pairs;
-  g.a_div = top_k;
-  g.offsets = expert_offsets;
-  g.w0 = wg;
-  g.s0 = (const uint16_t *)sg;
-  g.b0 = (const uint16_t *)bg;
-  g.w1 = wu;
-  g.s1 = (const uint16_t *)su;
-  g.b1 = (const uint16_t *)bu;
-  g.R = (int)I;
-  g.K = (int)H;
-  g.gs = group_size;
-  g.E = (int)E;
-  g.out = (uint16_t *)h;
-  g.o_map = nullptr;
-  g.out_ld = I;
+  nvm::GroupedArgs g = gateup_args(x, T, H, I, E, top_k, group_size, wg, sg, bg, wu, su, bu,
+                                   expert_offsets, sorted_pairs, h);
   const int64_t N = T * top_k;
   return run_products(dtype, use_decode(regime, N, E, H), true, g, N, (hipStream_t)stream);
 }
@@ -489,23 +525,8 @@ int nvm_moe_expert_down(const void *h, int64_t n_pairs, int64_t H, int64_t I, in
   NVM_REQUIRE(h && wd && sd && bd && expert_offsets && sorted_pairs && down,
               "expert_down: null pointer");
   if (n_pairs == 0) return NVM_OK;
-  nvm::GroupedArgs d{};
-  d.act = (const uint16_t *)h;
-  d.act_ld = I;
-  d.act_rows = n_pairs;
-  d.a_map = nullptr;
-  d.a_div = 1;
-  d.offsets = expert_offsets;
-  d.w0 = wd;
-  d.s0 = (const uint16_t *)sd;
-  d.b0 = (const uint16_t *)bd;
-  d.R = (int)H;
-  d.K = (int)I;
-  d.gs = group_size;
-  d.E = (int)E;
-  d.out = (uint16_t *)down;
-  d.o_map = sorted_pairs;
-  d.out_ld = H;
+  nvm::GroupedArgs d = down_args(h, n_pairs, H, I, E, group_size, wd, sd, bd, expert_offsets,
+                                 sorted_pairs, down);
   return run_products(dtype, use_decode(regime, n_pairs, E, I), false, d, n_pairs,
                       (hipStream_t)stream);
 }
@@ -655,6 +676,24 @@ int moe_stages(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int to
                                    norm_topk_prob, nullptr, ids, scores, ws.offsets, ws.sorted,
                                    ws.partial, ws.counts, ws.done, st))
       return r;
+    if (int r = check_products(H, I, E, top_k, group_size, bits, dtype, regime)) return r;
+    if (dtype == NVM_DTYPE_BF16 && !use_decode(regime, N, E, H) && !use_decode(regime, N, E, I)) {
+      // Both products on the prefill GEMM, which computes in fp16: x is
+      // converted once (into the down buffer, which only the down product
+      // writes, later) and the gate/up epilogue stores h converted, instead
+      // of every tile of every block converting its rows again.  The values
+      // are the ones the GEMMs' staging would make.
+      NVM_TRY_HIP(nvm::launch_act_to_f16(x, T * H, ws.down, st));
+      nvm::GroupedArgs g = gateup_args(ws.down, T, H, I, E, top_k, group_size, wg, sg, bg, wu, su,
+                                       bu, ws.offsets, ws.sorted, ws.h);
+      g.act_h = 1;
+      g.out_h = 1;
+      if (int r = run_products(dtype, false, true, g, N, st)) return r;
+      nvm::GroupedArgs d = down_args(ws.h, N, H, I, E, group_size, wd, sd, bd, ws.offsets,
+                                     ws.sorted, ws.down);
+      d.act_h = 1;
+      return run_products(dtype, false, false, d, N, st);
+    }
     if (int r = nvm_moe_expert_gateup(x, T, H, I, E, top_k, group_size, bits, dtype, wg, sg, bg,
                                       wu, su, bu, ws.offsets, ws.sorted, ws.h, regime, stream))
       return r;

@@ -10,9 +10,13 @@
 //
 // A tile is 128 routed rows x 256 weight rows (gate/up: 128 columns of each
 // matrix; down: 256 columns).  Per 64-wide k-step the block stages the
-// gathered activation rows (bf16/fp16) and the *packed* int4 weight rows in
-// LDS, double-buffered, with the next k-step's global loads in flight during
-// the current k-step's MFMAs.  The four wavefronts split the tile along N: a
+// gathered activation rows (bf16/fp16), and per pair of k-steps the *packed*
+// int4 weight rows, in LDS, double-buffered, with the next global loads in
+// flight during the current k-step's MFMAs.  The kernel is bound by the
+// cache lines its loads touch, not by its arithmetic: a weight row's codes
+// for a k-step pair are half a 128-byte line (one k-step's were a quarter,
+// and the line was fetched again for every k-step), and the scales and
+// biases come in windows of four groups.  The four wavefronts split the tile along N: a
 // wavefront owns 2 x 32 weight rows (gate/up: the same 32 columns of both
 // matrices, so the SwiGLU pair lands in one lane) and all 128 routed rows
 // (4 x 2 tiles of v_mfma_f32_32x32x16).  Each weight word is dequantised once
@@ -45,11 +49,13 @@ constexpr int BM = kGemmBM;       // routed rows per tile
 constexpr int WROWS = 256;        // weight rows per tile
 constexpr int BK = 64;            // k per stage
 constexpr int A_PITCH = 144;      // bytes per staged activation row (128 + 16 pad)
-constexpr int B_PITCH = 48;       // bytes per staged weight row (32 + 16 pad)
+// bytes per staged weight row: the packed codes of two k-steps (64) + 16 pad
+constexpr int B_PITCH = 80;
 constexpr int A_STAGE = BM * A_PITCH;
 constexpr int B_STAGE = WROWS * B_PITCH;
-constexpr int STAGE = A_STAGE + B_STAGE;
-constexpr int kGemmLds = 2 * STAGE;
+// two activation stages (one k-step each) and two weight stages (a k-step
+// pair each): 76 KB, two blocks per CU
+constexpr int kGemmLds = 2 * A_STAGE + 2 * B_STAGE;
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
@@ -112,12 +118,19 @@ __device__ __forceinline__ uint32_t sb_pair_h(uint32_t bits) {
   return h | (h << 16);
 }
 
+// fp16 bits of x, rounded toward zero as v_cvt_pkrtz_f16_f32 rounds (the
+// conversion act_to_h applies to bf16 activations)
+__device__ __forceinline__ uint16_t f16_rtz(float x) {
+  return (uint16_t)(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x, x)) & 0xFFFFu);
+}
+
 __device__ __forceinline__ f32x16 mfma32_h(u32x4 a, u32x4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-template <int DT, bool DUAL>
+// AH: the activations arrive already in fp16 (GroupedArgs::act_h).
+template <int DT, bool DUAL, bool AH>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n_tiles) {
   using A = Act<DT>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -203,13 +216,16 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
     const int ar = s_arow[(tid >> 3) + 32 * c];
     a_voff[c] = ar >= 0 ? (int)(((int64_t)ar * a.act_ld) * 2) + 16 * (tid & 7) : kMaskedOffset;
   }
-  // packed weights: thread loads staged rows (tid >> 1) + 128c, half tid & 1
-  int b_voff[2];
+  // packed weights of a k-step pair (64 bytes of each row: half of a
+  // 128-byte line, where one k-step's 32 bytes were a quarter): thread loads
+  // staged rows (tid >> 2) + 64c, quarter tid & 3; rows 0..127 of a dual
+  // tile are gate rows, 128..255 up rows
+  int b_voff[4];
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int wrow = (tid >> 1) + 128 * c;
+  for (int c = 0; c < 4; ++c) {
+    const int wrow = (tid >> 2) + 64 * c;
     const int grow = DUAL ? n0 + (wrow & 127) : n0 + wrow;
-    b_voff[c] = grow < R ? grow * KW * 4 + 16 * (tid & 1) : kMaskedOffset;
+    b_voff[c] = grow < R ? grow * KW * 4 + 16 * (tid & 3) : kMaskedOffset;
   }
   // this lane's two weight rows (sub 0/1) for the scale/bias loads and reads
   int srow[2], lrow[2];
@@ -225,34 +241,69 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
   // register sets.  Every issue makes the same loads; k-steps past the end
   // read through masked offsets (zeros, no traffic), so the wait counts are
   // the same on every path.
+  // (the activations of one k-step; the packed weights of a k-step pair,
+  // requested with the pair's first k-step)
   struct Stage {
-    u32x4 a[4], b[2];
-    uint32_t s[2], z[2];
+    u32x4 a[4];
+  };
+  struct PairB {
+    u32x4 b[4];
   };
   auto issue = [&](Stage &g, int ks) {
     const bool ok = ks < nk;
-    const int k0 = ok ? ks * BK : 0;
-    const int sa = __builtin_amdgcn_readfirstlane(k0 * 2);
-    const int sb = __builtin_amdgcn_readfirstlane(k0 >> 1);
-    const int sg = __builtin_amdgcn_readfirstlane((k0 / a.gs) * 2);
+    const int sa = __builtin_amdgcn_readfirstlane(ok ? ks * BK * 2 : 0);
 #pragma unroll
     for (int c = 0; c < 4; ++c) g.a[c] = bload16(ra, ok ? a_voff[c] : kMaskedOffset, sa);
-    g.b[0] = bload16(rw0, ok ? b_voff[0] : kMaskedOffset, sb);
-    g.b[1] = bload16(rw1, ok ? b_voff[1] : kMaskedOffset, sb);
-    g.s[0] = bload2(rs0, ok ? srow[0] : kMaskedOffset, sg);
-    g.z[0] = bload2(rb0, ok ? srow[0] : kMaskedOffset, sg);
-    g.s[1] = bload2(rs1, ok ? srow[1] : kMaskedOffset, sg);
-    g.z[1] = bload2(rb1, ok ? srow[1] : kMaskedOffset, sg);
   };
-  auto store = [&](const Stage &g, int buf) {
-    uint8_t *As = smem + buf * STAGE;
-    uint8_t *Bs = As + A_STAGE;
+  auto issue_b = [&](PairB &g, int ks) {  // ks even: k-steps ks, ks + 1
+    const bool ok = ks < nk;
+    const int sb = __builtin_amdgcn_readfirstlane(ok ? ks * BK / 2 : 0);
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      *(u32x4 *)(As + ((tid >> 3) + 32 * c) * A_PITCH + 16 * (tid & 7)) = act_to_h<DT>(g.a[c]);
+      g.b[c] = bload16(c < 2 ? rw0 : rw1, ok ? b_voff[c] : kMaskedOffset, sb);
+  };
+  // Scales and biases of the lane's two weight rows come in windows of four
+  // groups: one 8-byte load per row and matrix every four groups.  (One
+  // 2-byte load per k-step made as many memory requests as the activation
+  // and weight loads together: each lane reads a different row.)  wcur holds
+  // the window of the current k-step's group, wnxt the next one, in flight.
+  u32x2 wcur[4];  // scale 0, bias 0, scale 1, bias 1
+  // (A window is one 8-byte load when a row's groups are a multiple of four:
+  // every window then starts on a dword and ends inside its row.  Otherwise
+  // it is packed from four 2-byte loads; groups past the row read zeros.)
+  const bool win8 = GPR % 4 == 0;
+  auto issue_w = [&](u32x2 (&w)[4], int wi) {
+    const int so = __builtin_amdgcn_readfirstlane(8 * wi);
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
-      *(u32x4 *)(Bs + ((tid >> 1) + 128 * c) * B_PITCH + 16 * (tid & 1)) = g.b[c];
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const rsrc_t r = t ? (s ? rb1 : rb0) : (s ? rs1 : rs0);
+        if (win8) {
+          w[2 * s + t] = bload8(r, 4 * wi < GPR ? srow[s] : kMaskedOffset, so);
+        } else {
+          uint32_t v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            v[q] = bload2(r, 4 * wi + q < GPR ? srow[s] : kMaskedOffset, so + 2 * q) & 0xFFFFu;
+          w[2 * s + t] = u32x2{v[0] | (v[1] << 16), v[2] | (v[3] << 16)};
+        }
+      }
+  };
+  int w_idx = 0;  // window of wcur
+  issue_w(wcur, 0);
+  auto store = [&](const Stage &g, int buf) {
+    uint8_t *As = smem + buf * A_STAGE;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      *(u32x4 *)(As + ((tid >> 3) + 32 * c) * A_PITCH + 16 * (tid & 7)) =
+          act_to_h<AH ? DT_F16 : DT>(g.a[c]);
+  };
+  auto store_b = [&](const PairB &g, int pbuf) {
+    uint8_t *Bs = smem + 2 * A_STAGE + pbuf * B_STAGE;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      *(u32x4 *)(Bs + ((tid >> 2) + 64 * c) * B_PITCH + 16 * (tid & 3)) = g.b[c];
   };
 
   f32x16 acc[2][4];
@@ -263,23 +314,29 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[s][i][r] = 0.f;
 
-  // this k-step's scale and bias of the lane's two weight rows, fp16 pairs
+  // k-step ks's scale and bias of the lane's two weight rows, fp16 pairs
+  // (k-step ks lies in group ks * 64 / gs; calls come in k-step order)
   uint32_t sc[2], bi[2];
-  auto take_sb = [&](const Stage &g) {
+  auto take_sb = [&](int ks) {
+    const int g = ks * BK / a.gs;
+    const int j = g & 3;
+    auto pick = [&](const u32x2 &w) { return ((j & 2) ? w.y : w.x) >> (16 * (j & 1)); };
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      sc[s] = sb_pair_h<DT>(g.s[s]);
-      bi[s] = sb_pair_h<DT>(g.z[s]);
+      sc[s] = sb_pair_h<DT>(pick(wcur[2 * s]));
+      bi[s] = sb_pair_h<DT>(pick(wcur[2 * s + 1]));
     }
+    // the window's last k-step: the next window, in the same registers
+    if (j == 3 && (ks + 1) * BK / a.gs != g) issue_w(wcur, ++w_idx);
   };
   // nibble-expansion constants in registers (one v_and_or_b32 per dword)
   const uint32_t nib_mask = sgpr_const(0x000F000Fu);
   const uint32_t magic = vgpr_const(0x64006400u);  // fp16 (1024, 1024)
   // Software-pipelined over the four 16-wide chunks: the A reads and the
   // dequantisation of chunk c + 1 are issued ahead of chunk c's MFMAs.
-  auto compute = [&](int buf) {
-    const uint8_t *As = smem + buf * STAGE;
-    const uint8_t *Bs = As + A_STAGE;
+  auto compute = [&](int ks) {
+    const uint8_t *As = smem + (ks & 1) * A_STAGE;
+    const uint8_t *Bs = smem + 2 * A_STAGE + ((ks >> 1) & 1) * B_STAGE + 32 * (ks & 1);
     u32x4 bw[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) bw[s] = *(const u32x4 *)(Bs + lrow[s] * B_PITCH + 16 * h);
@@ -315,31 +372,41 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
     }
   };
 
-  // k-step ks computes LDS buffer ks & 1 while the loads of ks + 2 are in
-  // flight in the register set that held ks; then ks + 1 (issued a k-step
-  // earlier) is stored into the other buffer.  Two k-steps per loop trip keep
-  // the register sets static.
+  // k-step ks computes activation stage ks & 1 and weight stage (ks / 2) & 1
+  // while the activation loads of ks + 2 (and, ks even, the weights of the
+  // pair ks + 2, ks + 3) are in flight in the register set that held ks;
+  // then ks + 1 (issued a k-step earlier) is stored into the other stage,
+  // and at the end of an odd k-step the next pair's weights.  Two k-steps per
+  // loop trip keep the register sets static.
   Stage g0, g1;
+  PairB gb;
   issue(g0, 0);
+  issue_b(gb, 0);
   issue(g1, 1);
   store(g0, 0);
-  take_sb(g0);
+  store_b(gb, 0);
+  take_sb(0);
   __syncthreads();
-  auto step = [&](int ks, Stage &gi, Stage &gs) {
-    issue(gi, ks + 2);
-    compute(ks & 1);
-    if (ks + 1 < nk) {
-      store(gs, (ks + 1) & 1);
-      take_sb(gs);
-    }
-    __syncthreads();
-  };
   int ks = 0;
   for (; ks + 1 < nk; ks += 2) {
-    step(ks, g0, g1);
-    step(ks + 1, g1, g0);
+    // even k-step
+    issue(g0, ks + 2);
+    issue_b(gb, ks + 2);
+    compute(ks);
+    store(g1, 1);
+    take_sb(ks + 1);
+    __syncthreads();
+    // odd k-step
+    issue(g1, ks + 3);
+    compute(ks + 1);
+    if (ks + 2 < nk) {
+      store(g0, 0);
+      store_b(gb, ((ks + 2) >> 1) & 1);
+      take_sb(ks + 2);
+    }
+    __syncthreads();
   }
-  if (ks < nk) step(ks, g0, g1);
+  if (ks < nk) compute(ks);  // an odd count: the last k-step, already staged
 
   // C fragment of v_mfma_f32_32x32x16: lane l, register 4*q+j holds row
   // 8*q + 4*(l/32) + j, column l%32
@@ -355,7 +422,9 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
         if (col < R) {
           const float gv = round_act<DT>(acc[0][i][r]);
           const float uv = round_act<DT>(acc[1][i][r]);
-          op[col] = A::from_f32(silu_act<DT>(gv) * uv);
+          const uint16_t o = A::from_f32(silu_act<DT>(gv) * uv);
+          // (out_h: the act value in the fp16 form of the down product's staging)
+          op[col] = DT == DT_BF16 && a.out_h ? f16_rtz(A::to_f32(o)) : o;
         }
       } else {
 #pragma unroll
@@ -368,25 +437,69 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
   }
 }
 
-template <int DT>
+// more than 64 KB of dynamic LDS: allowed once per device and instance (a
+// failure shows up as a failed launch)
+template <int DT, bool DUAL, bool AH>
+void allow_gemm_lds() {
+  static bool done[64] = {false};
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !done[dev]) {
+    (void)hipFuncSetAttribute((const void *)&gemm_kernel<DT, DUAL, AH>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
+    done[dev] = true;
+  }
+}
+
+template <int DT, bool AH>
 hipError_t launch_t(bool dual, const GroupedArgs &a, int64_t max_m_tiles, hipStream_t st) {
   const int cols = dual ? WROWS / 2 : WROWS;
   const int n_tiles = (a.R + cols - 1) / cols;
   const int64_t total = max_m_tiles * n_tiles;
   const unsigned grid = (unsigned)(8 * ((total + 7) / 8));
   if (dual)
-    hipLaunchKernelGGL((gemm_kernel<DT, true>), dim3(grid), dim3(256), kGemmLds, st, a, n_tiles);
+    allow_gemm_lds<DT, true, AH>();
   else
-    hipLaunchKernelGGL((gemm_kernel<DT, false>), dim3(grid), dim3(256), kGemmLds, st, a, n_tiles);
+    allow_gemm_lds<DT, false, AH>();
+  if (dual)
+    hipLaunchKernelGGL((gemm_kernel<DT, true, AH>), dim3(grid), dim3(256), kGemmLds, st, a,
+                       n_tiles);
+  else
+    hipLaunchKernelGGL((gemm_kernel<DT, false, AH>), dim3(grid), dim3(256), kGemmLds, st, a,
+                       n_tiles);
   return hipGetLastError();
+}
+
+// bf16 -> fp16 as act_to_h converts (pairs in natural order), eight values a
+// thread
+__global__ __launch_bounds__(256) void act_to_f16_kernel(const uint16_t *__restrict__ x,
+                                                        int64_t n8, uint16_t *__restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n8) return;
+  const u32x4 v = ldg16(x + 8 * i);
+  u32x4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    o[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(v[j] << 16),
+                                                                   __uint_as_float(v[j] & 0xFFFF0000u)));
+  *(u32x4 *)(out + 8 * i) = o;
 }
 
 }  // namespace
 
 hipError_t launch_gemm(int dtype, bool dual, const GroupedArgs &a, int64_t max_m_tiles,
                        hipStream_t st) {
-  return dtype == DT_BF16 ? launch_t<DT_BF16>(dual, a, max_m_tiles, st)
-                          : launch_t<DT_F16>(dual, a, max_m_tiles, st);
+  if (dtype != DT_BF16) return launch_t<DT_F16, false>(dual, a, max_m_tiles, st);
+  return a.act_h ? launch_t<DT_BF16, true>(dual, a, max_m_tiles, st)
+                 : launch_t<DT_BF16, false>(dual, a, max_m_tiles, st);
+}
+
+hipError_t launch_act_to_f16(const void *x, int64_t n, void *out, hipStream_t st) {
+  if (n % 8 || ((uintptr_t)x | (uintptr_t)out) % 16) return hipErrorInvalidValue;
+  const int64_t n8 = n / 8;
+  if (n8 == 0) return hipSuccess;
+  hipLaunchKernelGGL(act_to_f16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st,
+                     (const uint16_t *)x, n8, (uint16_t *)out);
+  return hipGetLastError();
 }
 
 }  // namespace nvm

@@ -149,6 +149,8 @@ def test_quantized_matmul_matches_oracle(M, N, K, act, gs):
     (65, 2048, 512, "bfloat16", 64, "gemv"),     # narrow output beyond 64 rows
     (300, 512, 96, "bfloat16", 64, "gemv"),
     (4096, 2048, 128, "float16", 128, "gemm"),
+    (600, 768, 1024, "bfloat16", 128, "gemm"),   # 6 groups a row: windows of 2-byte loads
+    (520, 192, 1024, "float16", 64, "gemm"),     # 3 k-steps: the last one after the pairs
 ])
 def test_quantized_matmul_dense_products(M, N, K, act, gs, path):
     from nano_vllm_metal_amd import quantized_matmul
