@@ -262,30 +262,36 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
     for (int c = 0; c < 4; ++c)
       g.b[c] = bload16(c < 2 ? rw0 : rw1, ok ? b_voff[c] : kMaskedOffset, sb);
   };
-  // Scales and biases of the lane's two weight rows come in windows of four
-  // groups: one 8-byte load per row and matrix every four groups.  (One
-  // 2-byte load per k-step made as many memory requests as the activation
-  // and weight loads together: each lane reads a different row.)  wcur holds
-  // the window of the current k-step's group, wnxt the next one, in flight.
+  // Scales and biases of the lane's two weight rows come in windows of eight
+  // groups split over the lane halves: half h holds groups 4h..4h+3 of the
+  // window, one 8-byte load per row and matrix every eight groups, and a
+  // k-step takes its group's value from the half that holds it with one
+  // v_permlane32_swap (lanes l and l + 32 own the same rows).  (One 2-byte
+  // load per k-step made as many memory requests as the activation and
+  // weight loads together: each lane reads a different row.)  The next window
+  // is requested, into the same registers, once the last group is taken.
   u32x2 wcur[4];  // scale 0, bias 0, scale 1, bias 1
-  // (A window is one 8-byte load when a row's groups are a multiple of four:
-  // every window then starts on a dword and ends inside its row.  Otherwise
-  // it is packed from four 2-byte loads; groups past the row read zeros.)
+  // (A half's four groups are one 8-byte load when a row's groups are a
+  // multiple of four: they then start on a dword and end inside their row.
+  // Otherwise they are packed from 2-byte loads; groups past the row read
+  // zeros.)
   const bool win8 = GPR % 4 == 0;
   auto issue_w = [&](u32x2 (&w)[4], int wi) {
-    const int so = __builtin_amdgcn_readfirstlane(8 * wi);
+    const int gh = 8 * wi + 4 * h;  // this half's first group
+    const int so = __builtin_amdgcn_readfirstlane(16 * wi);
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const rsrc_t r = t ? (s ? rb1 : rb0) : (s ? rs1 : rs0);
         if (win8) {
-          w[2 * s + t] = bload8(r, 4 * wi < GPR ? srow[s] : kMaskedOffset, so);
+          w[2 * s + t] = bload8(r, gh < GPR ? srow[s] + 8 * h : kMaskedOffset, so);
         } else {
           uint32_t v[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q)
-            v[q] = bload2(r, 4 * wi + q < GPR ? srow[s] : kMaskedOffset, so + 2 * q) & 0xFFFFu;
+            v[q] = bload2(r, gh + q < GPR ? srow[s] + 8 * h : kMaskedOffset, so + 2 * q) &
+                   0xFFFFu;
           w[2 * s + t] = u32x2{v[0] | (v[1] << 16), v[2] | (v[3] << 16)};
         }
       }
@@ -319,15 +325,21 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
   uint32_t sc[2], bi[2];
   auto take_sb = [&](int ks) {
     const int g = ks * BK / a.gs;
-    const int j = g & 3;
-    auto pick = [&](const u32x2 &w) { return ((j & 2) ? w.y : w.x) >> (16 * (j & 1)); };
+    const int j = g & 7;
+    // the word of group j in every lane: half (j >> 2)'s copy, both halves'
+    // after the swap
+    auto pick = [&](const u32x2 &w) {
+      const uint32_t x = (j & 2) ? w.y : w.x;
+      const auto pr = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+      return ((j & 4) ? pr[1] : pr[0]) >> (16 * (j & 1));
+    };
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       sc[s] = sb_pair_h<DT>(pick(wcur[2 * s]));
       bi[s] = sb_pair_h<DT>(pick(wcur[2 * s + 1]));
     }
     // the window's last k-step: the next window, in the same registers
-    if (j == 3 && (ks + 1) * BK / a.gs != g) issue_w(wcur, ++w_idx);
+    if (j == 7 && (ks + 1) * BK / a.gs != g) issue_w(wcur, ++w_idx);
   };
   // nibble-expansion constants in registers (one v_and_or_b32 per dword)
   const uint32_t nib_mask = sgpr_const(0x000F000Fu);
