@@ -682,8 +682,13 @@ KERNEL_KEYS = (
     ("decode_gateup_fused", r"gemv3_kernel<1, true, \d+, true>"),
     ("decode_gateup", r"gemv3_kernel<1, true, \d+, false>|gemv_kernel<1, true"),
     ("decode_down", r"gemv3_kernel<1, false|gemv_kernel<1, false"),
-    ("prefill_gateup", r"gemm_kernel<1, true"),
-    ("prefill_down", r"gemm_kernel<1, false"),
+    # prefill GEMMs of the forward (activations converted to fp16 once, by
+    # act_to_f16) and of the stage entry points (converting their own rows)
+    ("prefill_gateup", r"gemm_kernel<1, true, true>"),
+    ("prefill_down", r"gemm_kernel<1, false, true>"),
+    ("prefill_gateup_stage", r"gemm_kernel<1, true, false>"),
+    ("prefill_down_stage", r"gemm_kernel<1, false, false>"),
+    ("prefill_act_f16", r"act_to_f16_kernel"),
     ("route_partial", r"route_mfma_kernel<1"),
     ("route_finalize_dispatch", r"route_finalize_dispatch_kernel<1"),
     ("route_finalize", r"route_finalize_kernel<1"),
@@ -695,6 +700,7 @@ KERNEL_KEYS = (
 
 
 PROFILE_DECODE = ROOT / "profiles" / "decode_b32_kernel_trace.txt"
+PROFILE_PREFILL = ROOT / "profiles" / "prefill_4096_kernel_trace.txt"
 
 
 def read_rocprof_us(key, path=PROFILE_DECODE):
@@ -1012,11 +1018,21 @@ def main():
                 f"prefill {out['e2e']['prefill_tokens_per_s']:.0f} tok/s")
         u = out["prefill"]["uniform"]
         out["prefill_roofline"] = {
-            "kernel": "gemm_kernel<bf16, gate/up+SwiGLU> (nvm_moe_expert_gateup, prefill)",
+            "kernel": "gemm_kernel<bf16, gate/up+SwiGLU> (nvm_moe_expert_gateup, prefill; "
+                      "converts its staged bf16 rows to fp16 itself)",
             "bound": "mfma", "achieved": u["gateup_tflops"], "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": u["gateup_tflops"] / MFMA_BF16_PEAK_TFLOPS,
-            "traffic": read_traffic("prefill_gateup"),
+            "traffic": read_traffic("prefill_gateup_stage"),
         }
+        # the forward's gate/up GEMM (fp16 activations converted once), from
+        # the committed kernel trace of the same workload
+        avg, med = read_rocprof_us("prefill_gateup", PROFILE_PREFILL)
+        if med is not None:
+            fl = 2.0 * 4096 * SHAPE["k"] * SHAPE["H"] * 2 * SHAPE["I"]
+            out["prefill_roofline"]["forward_gateup"] = {
+                "rocprof_median_us": med, "tflops": fl / (med * 1e-6) / 1e12,
+                "frac": fl / (med * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                "rocprof_profile": str(PROFILE_PREFILL.relative_to(ROOT))}
     if not args.no_cpu:
         log(f"[bench] CPU baseline (~{args.cpu_seconds:.0f} s)")
         out["cpu_baseline"] = cpu_baseline(layers[0], args.batch, args.cpu_seconds, dev)

@@ -170,6 +170,33 @@ def test_quantized_matmul_dense_products(M, N, K, act, gs, path):
     assert same > 0.9, f"{path}: {same:.3f} of the outputs equal the rounded exact result"
 
 
+@pytest.mark.parametrize("act", ["float16", "bfloat16"])
+@pytest.mark.parametrize("gs", [64, 128])
+def test_torch_quantizer_on_gpu(act, gs):
+    """The MLX affine quantizer that builds every benchmark and test weight set,
+    run on the GPU: the same codes, scales and biases as on the CPU (each step
+    is an IEEE float32 operation or an exact one), and the oracle's quantizer
+    agrees as in the CPU test (float64 there; near-ties may round apart)."""
+    from nano_vllm_metal_amd import quantize
+
+    rng = np.random.default_rng(33 + gs)
+    w = O.round_act(rng.standard_normal((96, 8 * gs)) * 0.02, act)
+    dt = torch.float16 if act == "float16" else torch.bfloat16
+    wt = torch.from_numpy(w.astype(np.float32)).to(dt)
+    g_wq, g_s, g_b = quantize(wt.to(DEV), gs, 4)
+    c_wq, c_s, c_b = quantize(wt, gs, 4)
+    assert torch.equal(g_wq.cpu(), c_wq)
+    assert torch.equal(g_s.cpu().view(torch.int16), c_s.view(torch.int16))
+    assert torch.equal(g_b.cpu().view(torch.int16), c_b.view(torch.int16))
+    owq, os_, ob = O.quantize(w, gs, 4, act)
+    s_t = g_s.float().cpu().numpy().astype(np.float64)
+    b_t = g_b.float().cpu().numpy().astype(np.float64)
+    assert np.mean(s_t == os_) > 0.95 and np.mean(b_t == ob) > 0.95
+    same = np.repeat((s_t == os_) & (b_t == ob), gs, axis=1)
+    codes_g = O.unpack_nibbles(g_wq.cpu().numpy().view(np.uint32))
+    assert np.array_equal(codes_g[same], O.unpack_nibbles(owq)[same])
+
+
 # ---------------------------------------------------------------- dispatch
 
 
