@@ -36,15 +36,23 @@ __device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
   return max(v, dpp_u32<0x140>(v));
 }
 
+// A callable that issues nothing (the default `after_loads` below).
+struct NoIssue {
+  __device__ void operator()() const {}
+};
+
 // Tokens t0 .. t0+3 (row r of the wavefront holds token t0 + r; rows past T
 // compute and store nothing).  part is [T][E][splits] float64; E <= 128,
 // k <= 16, T <= 64.  Slot i of token t goes to s_ids[t*k + i] and
 // s_sc[t*k + i] (act bits), and bit t is set in s_mask[expert] (LDS, zeroed
-// by the caller).  Every lane of the wavefront must call it.
-template <int DT>
+// by the caller).  Every lane of the wavefront must call it.  after_loads()
+// runs once, right after the partial logits are requested and before they
+// are used (a caller's own loads issued there queue behind them).
+template <int DT, class Issue = NoIssue>
 __device__ __forceinline__ void finalize_rows(const double *__restrict__ part, int splits, int t0,
                                               int T, int E, int k, int norm, int *s_ids,
-                                              uint16_t *s_sc, uint64_t *s_mask) {
+                                              uint16_t *s_sc, uint64_t *s_mask,
+                                              Issue after_loads = Issue{}) {
   using A = Act<DT>;
   constexpr int P = A::kPrec, EMIN = A::kEmin;
   const int lane = threadIdx.x & 63, c = lane & 15;
@@ -60,11 +68,15 @@ __device__ __forceinline__ void finalize_rows(const double *__restrict__ part, i
       const int e = c + 16 * j;
       v[j] = bload16(pr, tok && e < E ? ((t * E + e) * 2) * 8 : kMaskedOffset, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    after_loads();
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       sum[j] = (0.0 + __builtin_bit_cast(double, u32x2{v[j].x, v[j].y})) +
                __builtin_bit_cast(double, u32x2{v[j].z, v[j].w});
   } else {
+    after_loads();
 #pragma unroll
     for (int j = 0; j < 8; ++j) sum[j] = 0.0;
     for (int z = 0; z < splits; ++z) {
@@ -142,16 +154,24 @@ __device__ __forceinline__ void finalize_rows(const double *__restrict__ part, i
 // (t, j) is the number of tokens below t in its expert's mask.
 // Fills s_ids/s_sc [T*k], s_off [E+1] (slot offsets), s_cb [E+1] (exclusive
 // prefix of ceil(count / chunk_rows)) and s_sorted [T*k].  All threads of
-// the block must call it; it ends with a barrier.
-template <int DT>
+// the block must call it; it ends with a barrier.  issue() runs once per
+// wavefront: behind its partial-logit requests when it finalises one group
+// of four tokens, else before them.
+template <int DT, class Issue = NoIssue>
 __device__ __forceinline__ void route_in_block(const double *__restrict__ part, int splits, int T, int E, int k,
                                int norm, int chunk_rows, int *s_ids, uint16_t *s_sc,
-                               uint64_t *s_mask, int *s_off, int *s_cb, int *s_sorted) {
+                               uint64_t *s_mask, int *s_off, int *s_cb, int *s_sorted,
+                               Issue issue = Issue{}) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
   for (int e = tid; e < E; e += blockDim.x) s_mask[e] = 0ull;
   __syncthreads();
-  for (int t0 = 4 * wv; t0 < T; t0 += 4 * NW)
-    finalize_rows<DT>(part, splits, t0, T, E, k, norm, s_ids, s_sc, s_mask);
+  if (4 * wv < T && 4 * (wv + NW) >= T) {
+    finalize_rows<DT>(part, splits, 4 * wv, T, E, k, norm, s_ids, s_sc, s_mask, issue);
+  } else {
+    issue();
+    for (int t0 = 4 * wv; t0 < T; t0 += 4 * NW)
+      finalize_rows<DT>(part, splits, t0, T, E, k, norm, s_ids, s_sc, s_mask);
+  }
   __syncthreads();
   if (wv == 0) {
     int carry = 0, ccarry = 0;

@@ -32,6 +32,7 @@
 //   evenly: block b owns units [bU/n, (b+1)U/n), its wavefronts take them in
 //   turn.
 #include <algorithm>
+#include <cstdlib>
 
 #include "common.h"
 #include "finalize.h"
@@ -81,8 +82,19 @@ __device__ __forceinline__ uint32_t sb_val(const u32x2 &v, int j) {
 
 // FUSED: the gate/up product that finalises the routing in its prologue
 // (a distinct instance, so that profiles tell the two apart).
-template <int DT, bool DUAL, int NS, bool FUSED>
-__global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, int RT) {
+//
+// STATIC: expert-major blocks for batches that touch most experts.  Block b
+// owns expert b / SPE and its weight-row tiles [p RT / SPE, (p + 1) RT / SPE),
+// p = b % SPE, and each wavefront a fixed eighth of those tiles, so a
+// wavefront knows its first tile's weights before the routing does: its ring
+// and scale/bias window are requested at the very start (behind the partial
+// logits when the routing is finalised here, behind the expert offsets
+// otherwise) and stream in while the routing and the staging run.  A block
+// whose expert no token chose ends there.  Its units are the (tile, chunk)
+// pairs of its tiles and its expert's chunks, tile-major, so that an expert
+// of more than 16 rows reads a tile's weights again from the cache.
+template <int DT, bool DUAL, int NS, bool FUSED, bool STATIC>
+__global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, int RT, int SPE) {
   using A = Act<DT>;
   constexpr int D = NS % 4 == 0 ? 4 : 3;  // ring slots
   static_assert(NS % D == 0, "the ring must divide the steps of a unit");
@@ -111,59 +123,26 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
   __shared__ uint64_t s_mask[FUSED ? kRowExperts : 1];  // token set of each expert
 
   hoist_args(a.act, a.act_ld, a.act_rows, a.a_map, a.a_div, a.offsets, a.w0, a.s0, a.b0, a.w1,
-             a.s1, a.b1, a.R, a.gs, a.E, a.out, a.o_map, a.out_ld, RT);
+             a.s1, a.b1, a.R, a.gs, a.E, a.out, a.o_map, a.out_ld, RT, SPE);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, G = lane >> 4;
   const int E = a.E, R = a.R;
   constexpr bool fused = FUSED;
+  // The wavefronts w and w + 4 of a block share a SIMD: they take ranges 2w
+  // and 2w + 1 of the eight, so that every SIMD gets a quarter of the units
+  // (to one unit).
+  const int ri = (wv & 3) * 2 + (wv >> 2);
 
-  // ---- routing: finalised and sorted here, or the offsets of dispatch
-  if constexpr (fused) {
-    const int T = (int)a.act_rows, k = a.a_div, n = T * k;
-    route_in_block<DT>(a.route_part, a.route_splits, T, E, k, a.route_norm, kRows, s_rids, s_rsc,
-                       s_mask, s_off, s_cb, s_sorted);
-    if (blockIdx.x == 0) {
-      // the routing for the stages after this one (down product, combine)
-      for (int i = tid; i < n; i += 64 * kW) {
-        a.r_ids[i] = s_rids[i];
-        a.r_scores[i] = s_rsc[i];
-        a.r_sorted[i] = s_sorted[i];
-      }
-      for (int i = tid; i <= E; i += 64 * kW) a.r_offsets[i] = s_off[i];
-    }
-  } else {
-    // (no offsets: one expert over all act_rows rows, the dense product)
-    for (int i = tid; i <= E; i += 64 * kW)
-      s_off[i] = a.offsets ? a.offsets[i] : (i == 0 ? 0 : (int)a.act_rows);
-    __syncthreads();
-    if (wv == 0) {
-      // chunk bases: exclusive prefix over experts of ceil(rows / 16)
-      int carry = 0;
-      for (int e0 = 0; e0 < E; e0 += 64) {
-        const int e = e0 + lane;
-        const int n = e < E ? (s_off[e + 1] - s_off[e] + kRows - 1) / kRows : 0;
-        const int inc = wave_incl_scan(n, lane);
-        if (e < E) s_cb[e] = carry + inc - n;
-        carry += __shfl(inc, 63);
-      }
-      if (lane == 0) s_cb[E] = carry;
-    }
-    __syncthreads();
+  // STATIC: the block's expert and this wavefront's tiles [tw0, tw1)
+  int e_s = 0, tw0 = 0, tw1 = 0;
+  if constexpr (STATIC) {
+    e_s = blockIdx.x / SPE;
+    const int part = blockIdx.x - e_s * SPE;
+    const int b0 = part * RT / SPE, b1 = (part + 1) * RT / SPE;
+    tw0 = b0 + ri * (b1 - b0) / kW;
+    tw1 = b0 + (ri + 1) * (b1 - b0) / kW;
   }
-
-  // ---- the block's share of units [u0, u1); unit u = (chunk u / RT, tile u % RT)
-  const int U = s_cb[E] * RT;
-  int u0, u1;
-  if ((int64_t)U * gridDim.x < (1ll << 31)) {
-    u0 = (int)((unsigned)(blockIdx.x * U) / gridDim.x);
-    u1 = (int)((unsigned)((blockIdx.x + 1) * U) / gridDim.x);
-  } else {
-    u0 = (int)((int64_t)blockIdx.x * U / gridDim.x);
-    u1 = (int)((int64_t)(blockIdx.x + 1) * U / gridDim.x);
-  }
-  if (u1 <= u0) return;  // uniform over the block, before any further barrier
-  const int c_last = (u1 - 1) / RT;
 
   // whole-tensor descriptors: every expert's rows are reached through 32-bit
   // offsets (the host keeps E * R * K / 2 below 2 GiB)
@@ -175,9 +154,6 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
   const rsrc_t b_r[NM] = {make_rsrc(a.b0, (uint32_t)(ER * G64 * 2)),
                           make_rsrc(DUAL ? a.b1 : a.b0, (uint32_t)(ER * G64 * 2))};
   const rsrc_t act_r = make_rsrc(a.act, (uint32_t)(a.act_rows * a.act_ld * 2));
-
-  const uint32_t nib_mask = sgpr_const(0x000F000Fu << A::kCodeShift);
-  const uint32_t magic = vgpr_const(A::kMagic2);
 
   // ring: the weights, two 16-byte loads per matrix and step
   u32x4 wq[D][NM][2];
@@ -209,6 +185,101 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
         bu[m][j] = bload16(b_r[m], ad.sb[m] + 16 * G + 64 * j, 0);
       }
   };
+  // row offsets of weight-row tile rt of expert e (masked when !ok or past R)
+  auto setup_tile = [&](bool ok, int e, int rt, Addr &ad) {
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      const int row = rt * RU + (DUAL ? 0 : kRows * m) + col;
+      const bool rok = ok && row < R;
+      const int er = e * R + row;
+      ad.w[m] = rok ? er * (KW * 4) + 16 * G : kMasked;
+      ad.sb[m] = rok ? er * (G64 * 2) : kMasked;
+    }
+  };
+  Addr cur, nxt;
+  // STATIC: the first tile's scale/bias window and ring, before the routing
+  auto prefetch = [&]() {
+    if constexpr (STATIC) {
+      setup_tile(tw0 < tw1, e_s, tw0, cur);
+      sb_issue(su_cur, bu_cur, cur);
+#pragma unroll
+      for (int d = 0; d < D; ++d) issue(d, d, cur);
+    }
+  };
+
+  const uint32_t nib_mask = sgpr_const(0x000F000Fu << A::kCodeShift);
+  const uint32_t magic = vgpr_const(A::kMagic2);
+
+  // ---- routing: finalised and sorted here, or the offsets of dispatch
+  if constexpr (fused) {
+    const int T = (int)a.act_rows, k = a.a_div, n = T * k;
+    route_in_block<DT>(a.route_part, a.route_splits, T, E, k, a.route_norm, kRows, s_rids, s_rsc,
+                       s_mask, s_off, s_cb, s_sorted, prefetch);
+    if (blockIdx.x == 0) {
+      // the routing for the stages after this one (down product, combine)
+      for (int i = tid; i < n; i += 64 * kW) {
+        a.r_ids[i] = s_rids[i];
+        a.r_scores[i] = s_rsc[i];
+        a.r_sorted[i] = s_sorted[i];
+      }
+      for (int i = tid; i <= E; i += 64 * kW) a.r_offsets[i] = s_off[i];
+    }
+  } else if constexpr (STATIC) {
+    // the expert's two offsets first, then the ring behind them
+    int o = 0;
+    if (tid < 2) o = a.offsets[e_s + tid];
+    __builtin_amdgcn_sched_barrier(0);
+    prefetch();
+    __builtin_amdgcn_sched_barrier(0);
+    if (tid < 2) s_off[e_s + tid] = o;
+    __syncthreads();
+  } else {
+    // (no offsets: one expert over all act_rows rows, the dense product)
+    for (int i = tid; i <= E; i += 64 * kW)
+      s_off[i] = a.offsets ? a.offsets[i] : (i == 0 ? 0 : (int)a.act_rows);
+    __syncthreads();
+    if (wv == 0) {
+      // chunk bases: exclusive prefix over experts of ceil(rows / 16)
+      int carry = 0;
+      for (int e0 = 0; e0 < E; e0 += 64) {
+        const int e = e0 + lane;
+        const int n = e < E ? (s_off[e + 1] - s_off[e] + kRows - 1) / kRows : 0;
+        const int inc = wave_incl_scan(n, lane);
+        if (e < E) s_cb[e] = carry + inc - n;
+        carry += __shfl(inc, 63);
+      }
+      if (lane == 0) s_cb[E] = carry;
+    }
+    __syncthreads();
+  }
+
+  // ---- the block's chunks [c_first, c_last] and, dynamic, its share of
+  // units [u0, u1); unit u = (chunk u / RT, tile u % RT).  STATIC chunk
+  // indices are the expert's own (0 .. its chunk count - 1).
+  int u0 = 0, u1 = 0, c_first, c_last;
+  if constexpr (STATIC) {
+    const int n_e = s_off[e_s + 1] - s_off[e_s];
+    if (n_e == 0) {
+      // no token chose this expert: the prefetched ring is not used (its
+      // requests complete before the wavefront ends)
+      __builtin_amdgcn_s_waitcnt(0);
+      return;  // uniform over the block, before any further barrier
+    }
+    c_first = 0;
+    c_last = (n_e + kRows - 1) / kRows - 1;
+  } else {
+    const int U = s_cb[E] * RT;
+    if ((int64_t)U * gridDim.x < (1ll << 31)) {
+      u0 = (int)((unsigned)(blockIdx.x * U) / gridDim.x);
+      u1 = (int)((unsigned)((blockIdx.x + 1) * U) / gridDim.x);
+    } else {
+      u0 = (int)((int64_t)blockIdx.x * U / gridDim.x);
+      u1 = (int)((int64_t)(blockIdx.x + 1) * U / gridDim.x);
+    }
+    if (u1 <= u0) return;  // uniform over the block, before any further barrier
+    c_first = u0 / RT;
+    c_last = (u1 - 1) / RT;
+  }
 
   // the staged rows' activation rows (and, single product, output rows)
   auto act_row = [&](int sl) {
@@ -245,22 +316,34 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
     *(float *)(row + 2 * K + 4 * g) = gs;
   };
 
-  for (int cb = u0 / RT; cb <= c_last;) {
+  for (int cb = c_first; cb <= c_last;) {
+    const bool prefetched = STATIC && cb == c_first;
     // ---- phase: chunks cb .. cb + n - 1, as many as fit the LDS (at least
     // one); their rows are staged one after another
     if (wv == 0) {
-      // the chunks cb .. cb + 63 (within the block's range) from the experts
-      // holding them: expert e owns chunks s_cb[e] .. s_cb[e + 1] - 1
+      // the chunks cb .. cb + 63 (within the block's range): expert, first
+      // slot and rows of each
       const int c_end = min(c_last + 1, cb + kMaxRounds);
-      for (int e0 = 0; e0 < E; e0 += 64) {
-        const int e = e0 + lane;
-        if (e < E) {
-          const int c0 = max(s_cb[e], cb), c1 = min(s_cb[e + 1], c_end);
-          for (int ci = c0; ci < c1; ++ci) {
-            const int slot0 = s_off[e] + (ci - s_cb[e]) * kRows;
-            s_round[ci - cb][0] = e;
-            s_round[ci - cb][1] = slot0;
-            s_round[ci - cb][2] = min(kRows, s_off[e + 1] - slot0);
+      if constexpr (STATIC) {
+        const int ci = cb + lane;
+        if (ci < c_end) {
+          const int slot0 = s_off[e_s] + ci * kRows;
+          s_round[lane][0] = e_s;
+          s_round[lane][1] = slot0;
+          s_round[lane][2] = min(kRows, s_off[e_s + 1] - slot0);
+        }
+      } else {
+        // expert e owns chunks s_cb[e] .. s_cb[e + 1] - 1
+        for (int e0 = 0; e0 < E; e0 += 64) {
+          const int e = e0 + lane;
+          if (e < E) {
+            const int c0 = max(s_cb[e], cb), c1 = min(s_cb[e + 1], c_end);
+            for (int ci = c0; ci < c1; ++ci) {
+              const int slot0 = s_off[e] + (ci - s_cb[e]) * kRows;
+              s_round[ci - cb][0] = e;
+              s_round[ci - cb][1] = slot0;
+              s_round[ci - cb][2] = min(kRows, s_off[e + 1] - slot0);
+            }
           }
         }
       }
@@ -289,46 +372,59 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
       }
     }
 
-    // ---- this wavefront's units of the phase: a contiguous range [p0, p1).
-    // The wavefronts w and w + 4 of a block share a SIMD: they take ranges
-    // 2w and 2w + 1 of the eight, so that every SIMD gets a quarter of the
-    // units (to one unit).
-    const int ua = max(u0, cb * RT), ub = min(u1, (cb + n) * RT);
-    const int P = ub - ua;
-    auto range_start = [&](int ri) { return ua + (int)((unsigned)(ri * P) / kW); };
-    const int ri = (wv & 3) * 2 + (wv >> 2);
-    const int p0 = range_start(ri), p1 = range_start(ri + 1);
+    // ---- this wavefront's units of the phase: a contiguous range [p0, p1)
+    // of the phase's units (dynamic) or its tiles times the phase's chunks,
+    // tile-major (STATIC)
+    int ua = 0, p0, p1;
+    if constexpr (STATIC) {
+      p0 = 0;
+      p1 = (tw1 - tw0) * n;
+    } else {
+      ua = max(u0, cb * RT);
+      const int ub = min(u1, (cb + n) * RT);
+      const int P = ub - ua;
+      auto range_start = [&](int i) { return ua + (int)((unsigned)(i * P) / kW); };
+      p0 = range_start(ri);
+      p1 = range_start(ri + 1);
+    }
+    // unit u -> its chunk r within the phase and its tile rt
+    auto unit_of = [&](int u, int &r, int &rt) {
+      if constexpr (STATIC) {
+        const int q = n == 1 ? u : u / n;
+        r = u - q * n;
+        rt = tw0 + q;
+      } else {
+        const int ci = u / RT;
+        r = ci - cb;
+        rt = u - ci * RT;
+      }
+    };
     // unit u: row offsets of its rows (uniform except the lane's rows; a unit
     // past the range is masked)
     auto setup = [&](int u, Addr &ad) {
       const bool ok = u < p1;
-      const int uu = ok ? u : ua;
-      const int ci = uu / RT, rt = uu - ci * RT;
-      const int e = __builtin_amdgcn_readfirstlane(s_round[ci - cb][0]);
-#pragma unroll
-      for (int m = 0; m < NM; ++m) {
-        const int row = rt * RU + (DUAL ? 0 : kRows * m) + col;
-        const bool rok = ok && row < R;
-        const int er = e * R + row;
-        ad.w[m] = rok ? er * (KW * 4) + 16 * G : kMasked;
-        ad.sb[m] = rok ? er * (G64 * 2) : kMasked;
-      }
+      int r, rt;
+      unit_of(ok ? u : (STATIC ? 0 : ua), r, rt);
+      const int e = STATIC ? e_s : __builtin_amdgcn_readfirstlane(s_round[r][0]);
+      setup_tile(ok, e, rt, ad);
     };
 
     // The first two staging reads, then the first unit's scale/bias window and
     // ring slot 0 (queued behind those reads, so they do not delay them), the
     // staging stores and a barrier, then ring slots 1..D-1.  (All D slots
     // requested ahead of the stores measure no better: later staging reads
-    // would wait behind the ring's whole first burst.)
-    Addr cur, nxt;
-    setup(p0, cur);
+    // would wait behind the ring's whole first burst.)  The first phase of a
+    // STATIC block has its ring and window in flight already.
+    if (!prefetched) setup(p0, cur);
     setup(p0 + 1, nxt);
     {
       u32x4 v0[8], v1[8];
       stage_load(tid, tot, n, v0);
       stage_load(tid + 64 * kW, tot, n, v1);
-      sb_issue(su_cur, bu_cur, cur);
-      issue(0, 0, cur);
+      if (!prefetched) {
+        sb_issue(su_cur, bu_cur, cur);
+        issue(0, 0, cur);
+      }
       stage_store(tid, tot, v0);
       stage_store(tid + 64 * kW, tot, v1);
       for (int item = tid + 128 * kW; item < tot; item += 64 * kW) {
@@ -337,12 +433,15 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
       }
     }
     __syncthreads();
+    if (!prefetched) {
 #pragma unroll
-    for (int d = 1; d < D; ++d) issue(d, d, cur);
+      for (int d = 1; d < D; ++d) issue(d, d, cur);
+    }
 
     // unit u's epilogue: lane (c, G) holds routed rows 4G..4G+3 of weight row c
     auto epilogue = [&](int u, const f32x4 (&o)[NM]) {
-      const int ci = u / RT, r = ci - cb, rt = u - ci * RT;
+      int r, rt;
+      unit_of(u, r, rt);
       const int slot0 = __builtin_amdgcn_readfirstlane(s_round[r][1]);
       const int cnt = __builtin_amdgcn_readfirstlane(s_round[r][2]);
 #pragma unroll
@@ -370,7 +469,8 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
     };
 
     for (int u = p0; u < p1; ++u) {
-      const int ci = u / RT, r = ci - cb;
+      int r, rt_unused;
+      unit_of(u, r, rt_unused);
       const int cnt = __builtin_amdgcn_readfirstlane(s_round[r][2]);
       const uint8_t *arow =
           smem + (__builtin_amdgcn_readfirstlane(s_round[r][3]) + min(col, cnt - 1)) * ROWB;
@@ -479,7 +579,22 @@ bool gemv3_supports(int K, int R, int E, int gs) {
   return (int64_t)E * R * (K / 2) <= kMasked;
 }
 
-template <int DT, bool DUAL, int NS, bool FUSED>
+// Expert-major (STATIC) blocks pay when most experts have rows: a block
+// whose expert has none ends at once, and the weights stream on the others.
+// Taken when the batch has at least two routed rows per expert (with
+// uniform routing about 86 % of the experts are then touched) and there are
+// offsets (expert products).  NVM_GEMV_STATIC=0/1 overrides the choice.
+bool use_static(const GroupedArgs &a) {
+  if (!a.offsets && !a.route_part) return false;
+  static const int env = [] {
+    const char *v = getenv("NVM_GEMV_STATIC");
+    return v && (v[0] == '0' || v[0] == '1') ? v[0] - '0' : -1;
+  }();
+  if (env >= 0) return env == 1;
+  return a.act_rows * a.a_div >= 2 * (int64_t)a.E;
+}
+
+template <int DT, bool DUAL, int NS, bool FUSED, bool STATIC>
 hipError_t launch_v3(const GroupedArgs &a, hipStream_t st) {
   const int RU = DUAL ? kRows : 2 * kRows;
   const int RT = (a.R + RU - 1) / RU;
@@ -488,21 +603,31 @@ hipError_t launch_v3(const GroupedArgs &a, hipStream_t st) {
   static bool attr_set[64] = {false};
   int dev = 0;
   if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !attr_set[dev]) {
-    (void)hipFuncSetAttribute((const void *)&gemv3_kernel<DT, DUAL, NS, FUSED>,
+    (void)hipFuncSetAttribute((const void *)&gemv3_kernel<DT, DUAL, NS, FUSED, STATIC>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, kActLds);
     attr_set[dev] = true;
   }
-  hipLaunchKernelGGL((gemv3_kernel<DT, DUAL, NS, FUSED>), dim3(cu_count()), dim3(64 * kW), kActLds,
-                     st, a, RT);
+  // STATIC: SPE blocks per expert, about one block per compute unit in all
+  // (and at least one tile a block)
+  const int spe = STATIC ? std::max(1, std::min(cu_count() / a.E, RT)) : 1;
+  const int grid = STATIC ? a.E * spe : cu_count();
+  hipLaunchKernelGGL((gemv3_kernel<DT, DUAL, NS, FUSED, STATIC>), dim3(grid), dim3(64 * kW),
+                     kActLds, st, a, RT, spe);
   return hipGetLastError();
 }
 
 template <int DT, bool DUAL, int NS>
 hipError_t launch_v3_f(const GroupedArgs &a, hipStream_t st) {
+  const bool stat = use_static(a);
   if constexpr (DUAL) {
-    if (a.route_part) return launch_v3<DT, true, NS, true>(a, st);
+    if (a.route_part)
+      return stat ? launch_v3<DT, true, NS, true, true>(a, st)
+                  : launch_v3<DT, true, NS, true, false>(a, st);
+    return launch_v3<DT, true, NS, false, false>(a, st);
+  } else {
+    return stat ? launch_v3<DT, false, NS, false, true>(a, st)
+                : launch_v3<DT, false, NS, false, false>(a, st);
   }
-  return launch_v3<DT, DUAL, NS, false>(a, st);
 }
 
 template <int DT, bool DUAL>
