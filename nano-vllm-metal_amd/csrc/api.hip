@@ -122,7 +122,8 @@ MoeWs carve_moe(void *base, int64_t T, int64_t H, int64_t I, int64_t E, int k) {
   Carve c(base);
   MoeWs w;
   const int64_t N = T * k;
-  const int splits = std::max(nvm::route_splits(T, H, E), nvm::decode_route_splits(T, H, E));
+  const int splits =
+      std::max(nvm::route_workspace_splits(T, H, E), nvm::decode_route_splits(T, H, E));
   w.partial = c.take<double>((size_t)splits * T * E);
   w.ids = c.take<int32_t>(N);
   w.scores = c.take<uint16_t>(N);
@@ -354,7 +355,7 @@ int nvm_quantized_matmul(const void *scales, const void *biases, int group_size,
 int nvm_route_workspace_size(int64_t T, int64_t H, int64_t E, size_t *bytes) {
   NVM_REQUIRE(bytes, "route_workspace_size: null output");
   NVM_REQUIRE(T >= 0 && H > 0 && E > 0, "route_workspace_size: bad shape");
-  *bytes = sizeof(double) * (size_t)nvm::route_splits(T, H, E) * (size_t)T * (size_t)E;
+  *bytes = sizeof(double) * (size_t)nvm::route_workspace_splits(T, H, E) * (size_t)T * (size_t)E;
   return NVM_OK;
 }
 
@@ -404,7 +405,7 @@ int nvm_route_dispatch_workspace_size(int64_t T, int64_t H, int64_t E, int top_k
   NVM_REQUIRE(bytes, "route_dispatch_workspace_size: null output");
   NVM_REQUIRE(T >= 0 && H > 0 && E > 0 && top_k > 0, "route_dispatch_workspace_size: bad shape");
   Carve c(nullptr);
-  c.take<double>((size_t)nvm::route_splits(T, H, E) * T * E);
+  c.take<double>((size_t)nvm::route_workspace_splits(T, H, E) * T * E);
   c.take<int32_t>((size_t)nvm::dispatch_workspace_bytes(T * top_k, E) / sizeof(int32_t));
   c.take<unsigned>(1);
   *bytes = (c.off + 255) & ~(size_t)255;
@@ -425,7 +426,7 @@ int nvm_moe_route_dispatch(const void *x, int64_t T, int64_t H, const uint32_t *
   if (!workspace || workspace_bytes < need)
     return fail(NVM_ERR_WORKSPACE, "route_dispatch: workspace of %zu bytes needed", need);
   Carve c(workspace);
-  double *partial = c.take<double>((size_t)nvm::route_splits(T, H, E) * T * E);
+  double *partial = c.take<double>((size_t)nvm::route_workspace_splits(T, H, E) * T * E);
   int32_t *counts =
       c.take<int32_t>((size_t)nvm::dispatch_workspace_bytes(T * top_k, E) / sizeof(int32_t));
   unsigned *done = c.take<unsigned>(1);

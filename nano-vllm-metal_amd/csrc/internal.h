@@ -58,7 +58,18 @@ bool fused_route_supports(int64_t T, int64_t E, int k);
 
 // Router.  Partial float64 logits over hidden splits, then per-token finalise.
 // With final_act the logits are rounded and stored as act [T, E] directly.
+// route_splits: the splits launch_route_partial writes (read the environment
+// override of route_i8_applies at each call); route_workspace_splits: an
+// upper bound of them for any setting, for workspace sizes.
 int route_splits(int64_t T, int64_t H, int64_t E);
+int route_workspace_splits(int64_t T, int64_t H, int64_t E);
+// The exact int8-MFMA partial logits (route_i8.hip), taken by
+// launch_route_partial (without final_act) when route_i8_applies.
+bool route_i8_applies(int64_t T, int64_t H);
+int route_i8_splits(int64_t T, int64_t H, int64_t E);
+hipError_t launch_route_i8(int dtype, const void *x, int64_t T, int64_t H, const uint32_t *wr,
+                           const void *sr, const void *br, int64_t E, int gs, double *partial,
+                           unsigned *done, hipStream_t st);
 // `done` (may be NULL) is a counter the partial launch zeroes for the fused
 // finalise-and-dispatch launch that follows it.
 hipError_t launch_route_partial(int dtype, const void *x, int64_t T, int64_t H, const uint32_t *wr,

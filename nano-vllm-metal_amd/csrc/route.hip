@@ -11,6 +11,8 @@
 // most a few thousand products of a bf16/fp16 activation and an fp32-exact
 // weight is within ~2^-40 relative of the exact sum, so the rounded logits,
 // and with them the top-k ids, do not depend on summation order.
+#include <algorithm>
+
 #include "common.h"
 #include "finalize.h"
 #include "internal.h"
@@ -428,7 +430,14 @@ hipError_t launch_route_t(const void *x, int64_t T, int64_t H, const uint32_t *w
 
 }  // namespace
 
-int route_splits(int64_t T, int64_t H, int64_t E) { return route_plan(T, H, E).splits; }
+int route_splits(int64_t T, int64_t H, int64_t E) {
+  return route_i8_applies(T, H) ? route_i8_splits(T, H, E) : route_plan(T, H, E).splits;
+}
+
+int route_workspace_splits(int64_t T, int64_t H, int64_t E) {
+  const int f = route_plan(T, H, E).splits;
+  return H % 64 == 0 ? std::max(f, route_i8_splits(T, H, E)) : f;
+}
 
 int decode_route_splits(int64_t T, int64_t H, int64_t E) {
   return decode_route_plan(T, H, E).splits;
@@ -447,6 +456,8 @@ hipError_t launch_route_partial(int dtype, const void *x, int64_t T, int64_t H,
                                 const uint32_t *wr, const void *sr, const void *br, int64_t E,
                                 int gs, bool final_act, double *partial, void *fin,
                                 unsigned *done, hipStream_t st) {
+  if (!final_act && route_i8_applies(T, H))
+    return launch_route_i8(dtype, x, T, H, wr, sr, br, E, gs, partial, done, st);
   RoutePlan p = route_plan(T, H, E);
   // rounded logits: the four wavefronts of a block split the hidden range
   // when it is whole 128-column blocks per split

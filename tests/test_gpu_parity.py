@@ -29,6 +29,15 @@ def _route_case(seed, T, H, E, k, act, gs, norm, x_std=1.0, router_std=0.02):
 # ---------------------------------------------------------------- router
 
 
+@pytest.fixture(params=["f64", "i8"])
+def route_kernel(request, monkeypatch):
+    """The router's partial logits on the float64 matrix cores or, exactly,
+    on the int8 ones (route_i8.hip; chosen for batches of 128 tokens or more,
+    forced here for every batch)."""
+    monkeypatch.setenv("NVM_ROUTE_I8", "0" if request.param == "f64" else "1")
+    return request.param
+
+
 @pytest.mark.parametrize("T,H,E,k,act,gs", [
     (32, 256, 16, 4, "float16", 64),       # tiny parity config
     (4, 128, 4, 2, "float16", 128),        # reference test_router_topk shape
@@ -42,9 +51,11 @@ def _route_case(seed, T, H, E, k, act, gs, norm, x_std=1.0, router_std=0.02):
     (24, 384, 16, 4, "float16", 128),      # 128-column blocks: one hidden split
     (24, 640, 16, 4, "float16", 64),
     (300, 1152, 64, 6, "bfloat16", 128),   # nine 128-column blocks
+    (200, 512, 40, 4, "bfloat16", 64),     # experts not a multiple of 16
+    (130, 1024, 512, 8, "float16", 64),    # four 128-expert ranges
 ])
 @pytest.mark.parametrize("norm", [False, True])
-def test_route_bit_exact(T, H, E, k, act, gs, norm):
+def test_route_bit_exact(T, H, E, k, act, gs, norm, route_kernel):
     from nano_vllm_metal_amd import route_topk
 
     x, router = _route_case(1000 + T + H + E, T, H, E, k, act, gs, norm)
@@ -57,8 +68,40 @@ def test_route_bit_exact(T, H, E, k, act, gs, norm):
     assert np.array_equal(to_np(scores), sc_ref), "scores differ"
 
 
+@pytest.mark.parametrize("act", ["bfloat16", "float16"])
+def test_route_wide_exponent_range(act, route_kernel):
+    """Activations over many binades -- zero rows, values 2^-30 and 2^-60 (bf16)
+    below their neighbours, subnormals, large values -- take several exponent
+    bands in the int8 router; ids, probabilities and scores must still equal
+    the oracle's exactly rounded ones, as the float64 kernel's do."""
+    from nano_vllm_metal_amd import route_topk
+
+    T, H, E, k, gs = 40, 1024, 128, 8, 64
+    bf = act == "bfloat16"
+    rng = np.random.default_rng(77)
+    x = rng.standard_normal((T, H))
+    x[1] = 0.0                                   # no band at all
+    x[2, ::7] *= 2.0 ** (-30 if bf else -12)     # two bands
+    x[3, ::5] *= 2.0 ** (-60 if bf else -20)     # subnormal fp16 / far below (bf16)
+    x[3, 1::5] *= 2.0 ** (-30 if bf else -10)    # three bands
+    x[4, ::3] = 0.0
+    x[5, 10] = 2.0 ** (-130 if bf else -23)      # one subnormal
+    x[6] *= 2.0 ** (-100 if bf else -8)          # a whole row far from 1
+    x[7, ::11] *= 2.0 ** 12                      # large values
+    x[17:33] *= 2.0 ** -20 if bf else 1.0        # a tile of small rows next to normal ones
+    x = O.round_act(x, act)
+    wr = O.round_act(rng.standard_normal((E, H)) * 0.02, act)
+    router = O.quantize(wr, gs, 4, act)
+    _, probs_ref, ids_ref, sc_ref = O.route_topk(x, *router, gs, k, True, act)
+    probs, ids, scores = route_topk(to_act(x, act, DEV), qweights(router, act, gs, DEV), k, True)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy(), ids_ref), "top-k ids differ"
+    assert np.array_equal(to_np(probs), probs_ref), "probs differ"
+    assert np.array_equal(to_np(scores), sc_ref), "scores differ"
+
+
 @pytest.mark.parametrize("T", [1, 5, 32, 64, 65, 700])
-def test_route_and_dispatch_matches_oracle(T):
+def test_route_and_dispatch_matches_oracle(T, route_kernel):
     """One call: routing plus the stable sort (single launch for T <= 64)."""
     from nano_vllm_metal_amd import route_and_dispatch
 
