@@ -679,8 +679,8 @@ COPY_PROBE_BYTES = 256 << 20
 # finalises the routing in its prologue (inside nvm_moe_forward);
 # decode_gateup is the product alone (nvm_moe_expert_gateup).
 KERNEL_KEYS = (
-    ("decode_gateup_fused", r"gemv3_kernel<1, true, \d+, true>"),
-    ("decode_gateup", r"gemv3_kernel<1, true, \d+, false>|gemv_kernel<1, true"),
+    ("decode_gateup_fused", r"gemv3_kernel<1, true, \d+, true,"),
+    ("decode_gateup", r"gemv3_kernel<1, true, \d+, false,|gemv_kernel<1, true"),
     ("decode_down", r"gemv3_kernel<1, false|gemv_kernel<1, false"),
     # prefill GEMMs of the forward (activations converted to fp16 once, by
     # act_to_f16) and of the stage entry points (converting their own rows)
@@ -689,7 +689,7 @@ KERNEL_KEYS = (
     ("prefill_gateup_stage", r"gemm_kernel<1, true, false>"),
     ("prefill_down_stage", r"gemm_kernel<1, false, false>"),
     ("prefill_act_f16", r"act_to_f16_kernel"),
-    ("route_partial", r"route_mfma_kernel<1"),
+    ("route_partial", r"route_mfma_kernel<1|route_i8_kernel<1"),
     ("route_finalize_dispatch", r"route_finalize_dispatch_kernel<1"),
     ("route_finalize", r"route_finalize_kernel<1"),
     ("dispatch_count", r"dispatch_count_kernel"),

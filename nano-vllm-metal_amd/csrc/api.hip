@@ -138,11 +138,29 @@ MoeWs carve_moe(void *base, int64_t T, int64_t H, int64_t I, int64_t E, int k) {
 }
 
 // Routing then dispatch: one single-block launch finalises and sorts decode
-// batches; larger batches finalise per token and sort over blocks.
+// batches; batches the int8 router takes are routed whole in one launch and
+// sorted in another (without probabilities, E <= 128); other batches
+// finalise per token and sort over blocks.  xh (bf16 x; may be NULL): where
+// the whole-routing launch may also store the fp16 copy of x that
+// launch_act_to_f16 makes; *xh_done says whether it did.
 int run_route_dispatch(int dtype, const void *x, int64_t T, int64_t H, const uint32_t *wr,
                        const void *sr, const void *br, int64_t E, int gs, int k, int norm,
                        void *probs, int32_t *ids, void *scores, int32_t *offsets, int32_t *sorted,
-                       double *partial, int32_t *counts, unsigned *done, hipStream_t st) {
+                       double *partial, int32_t *counts, unsigned *done, hipStream_t st,
+                       void *xh = nullptr, bool *xh_done = nullptr) {
+  if (xh_done) *xh_done = false;
+  if (!probs && !nvm::route_fused_dispatch(T, k) && nvm::route_i8_fin_supports(T, H, E, gs, k)) {
+    // the histograms [T/16][E] live in the partial-logit workspace, which
+    // this path does not use (T * E doubles at least)
+    int32_t *hist = (int32_t *)partial;
+    void *xo = dtype == NVM_DTYPE_BF16 ? xh : nullptr;
+    NVM_TRY_HIP(nvm::launch_route_i8_fin(dtype, x, T, H, wr, sr, br, E, gs, k, norm, ids, scores,
+                                         hist, xo, st));
+    NVM_TRY_HIP(nvm::launch_dispatch_hist(ids, T * k, E, hist, (T + 15) / 16, 16 * k, offsets,
+                                          sorted, st));
+    if (xh_done) *xh_done = xo != nullptr;
+    return NVM_OK;
+  }
   const int splits = nvm::route_splits(T, H, E);
   const bool fused = nvm::route_fused_dispatch(T, k);
   NVM_TRY_HIP(nvm::launch_route_partial(dtype, x, T, H, wr, sr, br, E, gs, false, partial, nullptr,
@@ -673,18 +691,23 @@ int moe_stages(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int to
     g.r_sorted = ws.sorted;
     if (int r = run_products(dtype, true, true, g, N, st)) return r;
   } else {
+    // Both products on the prefill GEMM, which computes in fp16: x is
+    // converted once (into the down buffer, which only the down product
+    // writes, later; by the routing launch where it can) and the gate/up
+    // epilogue stores h converted, instead of every tile of every block
+    // converting its rows again.  The values are the ones the GEMMs' staging
+    // would make.
+    const bool gemm_both =
+        dtype == NVM_DTYPE_BF16 && !use_decode(regime, N, E, H) && !use_decode(regime, N, E, I);
+    bool xh_done = false;
     if (int r = run_route_dispatch(dtype, x, T, H, wr, sr, br, E, group_size, top_k,
                                    norm_topk_prob, nullptr, ids, scores, ws.offsets, ws.sorted,
-                                   ws.partial, ws.counts, ws.done, st))
+                                   ws.partial, ws.counts, ws.done, st,
+                                   gemm_both ? ws.down : nullptr, &xh_done))
       return r;
     if (int r = check_products(H, I, E, top_k, group_size, bits, dtype, regime)) return r;
-    if (dtype == NVM_DTYPE_BF16 && !use_decode(regime, N, E, H) && !use_decode(regime, N, E, I)) {
-      // Both products on the prefill GEMM, which computes in fp16: x is
-      // converted once (into the down buffer, which only the down product
-      // writes, later) and the gate/up epilogue stores h converted, instead
-      // of every tile of every block converting its rows again.  The values
-      // are the ones the GEMMs' staging would make.
-      NVM_TRY_HIP(nvm::launch_act_to_f16(x, T * H, ws.down, st));
+    if (gemm_both) {
+      if (!xh_done) NVM_TRY_HIP(nvm::launch_act_to_f16(x, T * H, ws.down, st));
       nvm::GroupedArgs g = gateup_args(ws.down, T, H, I, E, top_k, group_size, wg, sg, bg, wu, su,
                                        bu, ws.offsets, ws.sorted, ws.h);
       g.act_h = 1;

@@ -6,6 +6,8 @@
 // derives its output bases from all histograms (exclusive prefix over
 // experts of the totals, plus the counts of the blocks before it) and
 // scatters its pairs.  No atomics and no host synchronisation.
+#include <algorithm>
+
 #include "internal.h"
 #include "sort.h"
 
@@ -109,7 +111,113 @@ __global__ __launch_bounds__(kSortThreads) void dispatch_scatter_kernel(
   sort_scatter(get, start, end, E, nbits, cnt + wv * E, sorted, b0);
 }
 
+// launch_dispatch_hist: block b sorts the pairs of count runs [b CB, (b+1) CB)
+// (runs of cb_pairs pairs).  Its output bases come from the run histograms:
+// the expert totals (offsets) and the pairs of each expert in earlier runs.
+// Thread (quad, part) sums experts 4 quad..4 quad+3 over runs part, part + P,
+// ... with 16-byte loads, eight in flight at a time (E a multiple of 4), and
+// the P parts meet in LDS.
+constexpr int kHistLoads = 8;
+__global__ __launch_bounds__(kSortThreads) void dispatch_hist_kernel(
+    const int32_t *__restrict__ ids, int n, int E, int nbits, const int32_t *__restrict__ counts,
+    int n_cb, int cb_pairs, int CB, int32_t *__restrict__ offsets, int32_t *__restrict__ sorted) {
+  extern __shared__ int lds[];
+  const int W = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int Q = E / 4;                // expert quads
+  const int P = (int)blockDim.x / Q;  // parts (blockDim >= Q)
+  const int cb0 = blockIdx.x * CB;
+  const int b0 = cb0 * cb_pairs, nb = min(CB * cb_pairs, n - b0);
+  int *cnt = lds;           // [W][E]
+  int *tot = lds + W * E;   // [E]: totals, then expert offsets
+  int *pre = tot + E;       // [E]: pairs of expert e in runs before this block's
+  int *ps = pre + E;        // [P][E] partial totals
+  int *pp = ps + P * E;     // [P][E] partial prefixes
+  for (int i = tid; i < W * E; i += blockDim.x) cnt[i] = 0;
+  if (tid < P * Q) {
+    const int qd = tid % Q, p = tid / Q;
+    const rsrc_t cr = make_rsrc(counts, (uint32_t)((int64_t)n_cb * E * 4));
+    u32x4 t = {0u, 0u, 0u, 0u}, q = {0u, 0u, 0u, 0u};
+    for (int r0 = p; r0 < n_cb; r0 += kHistLoads * P) {
+      u32x4 v[kHistLoads];
+#pragma unroll
+      for (int u = 0; u < kHistLoads; ++u) {
+        const int r = r0 + u * P;
+        v[u] = bload16(cr, r < n_cb ? (r * E + 4 * qd) * 4 : kMaskedOffset, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < kHistLoads; ++u) {
+        t += v[u];
+        if (r0 + u * P < cb0) q += v[u];
+      }
+    }
+    *(u32x4 *)(ps + p * E + 4 * qd) = t;
+    *(u32x4 *)(pp + p * E + 4 * qd) = q;
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += blockDim.x) {
+    int t = 0, q = 0;
+    for (int p = 0; p < P; ++p) {
+      t += ps[p * E + e];
+      q += pp[p * E + e];
+    }
+    tot[e] = t;
+    pre[e] = q;
+  }
+  __syncthreads();
+  int start, end;
+  sort_range(nb, W, wv, start, end);
+  auto get = [&](int p) { return ids[b0 + p]; };
+  sort_count(get, start, end, E, nbits, cnt + wv * E);
+  if (wv == 0) {
+    int carry = 0;
+    for (int c0 = 0; c0 < E; c0 += 64) {
+      const int e = c0 + lane;
+      const int v = e < E ? tot[e] : 0;
+      const int inc = wave_incl_scan(v, lane);
+      if (e < E) {
+        tot[e] = carry + inc - v;
+        if (blockIdx.x == 0) offsets[e] = carry + inc - v;
+      }
+      carry += __shfl(inc, 63);
+    }
+    if (lane == 0 && blockIdx.x == 0) offsets[E] = carry;
+  }
+  __syncthreads();
+  // run[w][e] = offset[e] + earlier runs + earlier wavefronts of this block
+  for (int e = tid; e < E; e += blockDim.x) {
+    int run = tot[e] + pre[e];
+    for (int w = 0; w < W; ++w) {
+      const int c = cnt[w * E + e];
+      cnt[w * E + e] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  sort_scatter(get, start, end, E, nbits, cnt + wv * E, sorted, b0);
+}
+
 }  // namespace
+
+hipError_t launch_dispatch_hist(const int32_t *ids, int64_t n, int64_t E, const int32_t *counts,
+                                int64_t n_cb, int cb_pairs, int32_t *offsets, int32_t *sorted,
+                                hipStream_t st) {
+  if (n <= 0 || cb_pairs <= 0 || E <= 0 || E > kMaxExperts || n_cb * cb_pairs < n)
+    return hipErrorInvalidValue;
+  const int nbits = bits_for(E);
+  const int W = kSortThreads / 64;
+  if (E % 4 != 0 || E / 4 > kSortThreads) return hipErrorInvalidValue;
+  const int P = kSortThreads / ((int)E / 4);
+  // about 1024 pairs a block, whole runs
+  const int CB = std::max(1, 1024 / cb_pairs);
+  if ((int64_t)CB * cb_pairs > kSortChunk) return hipErrorInvalidValue;
+  const int nblocks = (int)((n_cb + CB - 1) / CB);
+  const size_t lds = sizeof(int) * (size_t)(W * E + 2 * E + 2 * P * E);
+  if (lds > 65536) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(dispatch_hist_kernel, dim3(nblocks), dim3(kSortThreads), lds, st, ids, (int)n,
+                     (int)E, nbits, counts, (int)n_cb, cb_pairs, CB, offsets, sorted);
+  return hipGetLastError();
+}
 
 int64_t dispatch_workspace_bytes(int64_t n, int64_t E) {
   if (n <= kSortChunk) return 0;

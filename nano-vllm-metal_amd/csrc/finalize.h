@@ -41,55 +41,21 @@ struct NoIssue {
   __device__ void operator()() const {}
 };
 
-// Tokens t0 .. t0+3 (row r of the wavefront holds token t0 + r; rows past T
-// compute and store nothing).  part is [T][E][splits] float64; E <= 128,
-// k <= 16, T <= 64.  Slot i of token t goes to s_ids[t*k + i] and
-// s_sc[t*k + i] (act bits), and bit t is set in s_mask[expert] (LDS, zeroed
-// by the caller).  Every lane of the wavefront must call it.  after_loads()
-// runs once, right after the partial logits are requested and before they
-// are used (a caller's own loads issued there queue behind them).
-template <int DT, class Issue = NoIssue>
-__device__ __forceinline__ void finalize_rows(const double *__restrict__ part, int splits, int t0,
-                                              int T, int E, int k, int norm, int *s_ids,
-                                              uint16_t *s_sc, uint64_t *s_mask,
-                                              Issue after_loads = Issue{}) {
+// The rest of route_topk for the token of this lane's 16-lane row, from the
+// float64 logit sums of its experts c + 16 j (c = lane % 16; experts past E
+// ignored): the sums are rounded once to the activation dtype, the softmax
+// of those act logits runs in float64 and each probability is rounded once,
+// top-k takes (probability desc, expert index asc), and with norm_topk_prob
+// the scores are rnd(p / rnd(sum of the k probabilities)).  With `tok`, slot i
+// goes to s_ids[t*k + i] / s_sc[t*k + i] (act bits) and bit t is set in
+// s_mask[expert] (LDS).  Every lane of the wavefront must call it.
+template <int DT>
+__device__ __forceinline__ void finalize_sums(const double (&sum)[8], int t, bool tok, int E, int k,
+                                              int norm, int *s_ids, uint16_t *s_sc,
+                                              uint64_t *s_mask) {
   using A = Act<DT>;
   constexpr int P = A::kPrec, EMIN = A::kEmin;
   const int lane = threadIdx.x & 63, c = lane & 15;
-  const int t = t0 + (lane >> 4);
-  const bool tok = t < T;
-  // all loads of the lane in flight together; absent tokens/experts read zeros
-  const rsrc_t pr = make_rsrc(part, (uint32_t)((int64_t)T * E * splits * 8));
-  double sum[8];
-  if (splits == 2) {
-    u32x4 v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int e = c + 16 * j;
-      v[j] = bload16(pr, tok && e < E ? ((t * E + e) * 2) * 8 : kMaskedOffset, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    after_loads();
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      sum[j] = (0.0 + __builtin_bit_cast(double, u32x2{v[j].x, v[j].y})) +
-               __builtin_bit_cast(double, u32x2{v[j].z, v[j].w});
-  } else {
-    after_loads();
-#pragma unroll
-    for (int j = 0; j < 8; ++j) sum[j] = 0.0;
-    for (int z = 0; z < splits; ++z) {
-      u32x2 v[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int e = c + 16 * j;
-        v[j] = bload8(pr, tok && e < E ? ((t * E + e) * splits + z) * 8 : kMaskedOffset, 0);
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sum[j] += __builtin_bit_cast(double, v[j]);
-    }
-  }
   double lg[8];
   double m = -INFINITY;
 #pragma unroll
@@ -143,6 +109,56 @@ __device__ __forceinline__ void finalize_rows(const double *__restrict__ part, i
     __hip_atomic_fetch_or(&s_mask[my_id], 1ull << t, __ATOMIC_RELAXED,
                           __HIP_MEMORY_SCOPE_WORKGROUP);
   }
+}
+
+// Tokens t0 .. t0+3 (row r of the wavefront holds token t0 + r; rows past T
+// compute and store nothing).  part is [T][E][splits] float64; E <= 128,
+// k <= 16, T <= 64.  Slot i of token t goes to s_ids[t*k + i] and
+// s_sc[t*k + i] (act bits), and bit t is set in s_mask[expert] (LDS, zeroed
+// by the caller).  Every lane of the wavefront must call it.  after_loads()
+// runs once, right after the partial logits are requested and before they
+// are used (a caller's own loads issued there queue behind them).
+template <int DT, class Issue = NoIssue>
+__device__ __forceinline__ void finalize_rows(const double *__restrict__ part, int splits, int t0,
+                                              int T, int E, int k, int norm, int *s_ids,
+                                              uint16_t *s_sc, uint64_t *s_mask,
+                                              Issue after_loads = Issue{}) {
+  const int lane = threadIdx.x & 63, c = lane & 15;
+  const int t = t0 + (lane >> 4);
+  const bool tok = t < T;
+  // all loads of the lane in flight together; absent tokens/experts read zeros
+  const rsrc_t pr = make_rsrc(part, (uint32_t)((int64_t)T * E * splits * 8));
+  double sum[8];
+  if (splits == 2) {
+    u32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e = c + 16 * j;
+      v[j] = bload16(pr, tok && e < E ? ((t * E + e) * 2) * 8 : kMaskedOffset, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    after_loads();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      sum[j] = (0.0 + __builtin_bit_cast(double, u32x2{v[j].x, v[j].y})) +
+               __builtin_bit_cast(double, u32x2{v[j].z, v[j].w});
+  } else {
+    after_loads();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum[j] = 0.0;
+    for (int z = 0; z < splits; ++z) {
+      u32x2 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = c + 16 * j;
+        v[j] = bload8(pr, tok && e < E ? ((t * E + e) * splits + z) * 8 : kMaskedOffset, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sum[j] += __builtin_bit_cast(double, v[j]);
+    }
+  }
+  finalize_sums<DT>(sum, t, tok, E, k, norm, s_ids, s_sc, s_mask);
 }
 
 // The routing of a decode batch (T <= 64 tokens, E <= 128 experts, k <= 16)

@@ -70,6 +70,17 @@ int route_i8_splits(int64_t T, int64_t H, int64_t E);
 hipError_t launch_route_i8(int dtype, const void *x, int64_t T, int64_t H, const uint32_t *wr,
                            const void *sr, const void *br, int64_t E, int gs, double *partial,
                            unsigned *done, hipStream_t st);
+// The whole routing of batches the int8 router takes, for E <= 128 and
+// top-k <= 16 (and at most 64 groups a row): logits, softmax, top-k and
+// renormalisation in one launch of one block per 16 tokens, which writes
+// ids/scores [T][k], its expert histogram counts[T/16][E] (for
+// launch_dispatch_hist) and, with xh (bf16 x only), the fp16 copy of x that
+// launch_act_to_f16 makes.
+bool route_i8_fin_supports(int64_t T, int64_t H, int64_t E, int gs, int k);
+hipError_t launch_route_i8_fin(int dtype, const void *x, int64_t T, int64_t H, const uint32_t *wr,
+                               const void *sr, const void *br, int64_t E, int gs, int k, int norm,
+                               int32_t *ids, void *scores, int32_t *counts, void *xh,
+                               hipStream_t st);
 // `done` (may be NULL) is a counter the partial launch zeroes for the fused
 // finalise-and-dispatch launch that follows it.
 hipError_t launch_route_partial(int dtype, const void *x, int64_t T, int64_t H, const uint32_t *wr,
@@ -105,6 +116,12 @@ constexpr int64_t kSortChunk = 4096;
 int64_t dispatch_workspace_bytes(int64_t n, int64_t E);
 hipError_t launch_dispatch(const int32_t *ids, int64_t n, int64_t E, int32_t *offsets,
                            int32_t *sorted, void *workspace, hipStream_t st);
+// The same sort from per-block histograms counts[n_cb][E] of consecutive
+// runs of cb_pairs pairs (the last run may be short), as route_i8_fin writes
+// them: one launch.
+hipError_t launch_dispatch_hist(const int32_t *ids, int64_t n, int64_t E, const int32_t *counts,
+                                int64_t n_cb, int cb_pairs, int32_t *offsets, int32_t *sorted,
+                                hipStream_t st);
 
 // Grouped products.  dual = fused gate/up with SwiGLU epilogue.
 // Decode products need the reduction dimension in at most 8 slices of 1, 2,
