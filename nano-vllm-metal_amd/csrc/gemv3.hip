@@ -586,11 +586,8 @@ bool gemv3_supports(int K, int R, int E, int gs) {
 // offsets (expert products).  NVM_GEMV_STATIC=0/1 overrides the choice.
 bool use_static(const GroupedArgs &a) {
   if (!a.offsets && !a.route_part) return false;
-  static const int env = [] {
-    const char *v = getenv("NVM_GEMV_STATIC");
-    return v && (v[0] == '0' || v[0] == '1') ? v[0] - '0' : -1;
-  }();
-  if (env >= 0) return env == 1;
+  const char *v = getenv("NVM_GEMV_STATIC");
+  if (v && (v[0] == '0' || v[0] == '1')) return v[0] == '1';
   return a.act_rows * a.a_div >= 2 * (int64_t)a.E;
 }
 

@@ -100,13 +100,18 @@ def test_route_wide_exponent_range(act, route_kernel):
     assert np.array_equal(to_np(scores), sc_ref), "scores differ"
 
 
-@pytest.mark.parametrize("T", [1, 5, 32, 64, 65, 700])
-def test_route_and_dispatch_matches_oracle(T, route_kernel):
-    """One call: routing plus the stable sort (single launch for T <= 64)."""
+@pytest.mark.parametrize("T,E,k", [(1, 128, 8), (5, 128, 8), (32, 128, 8), (64, 128, 8),
+                                   (65, 128, 8), (700, 128, 8), (130, 64, 6), (131, 40, 4),
+                                   (300, 512, 8)])
+def test_route_and_dispatch_matches_oracle(T, E, k, route_kernel):
+    """One call: routing plus the stable sort (single launch for T <= 64; for
+    the int8 router with E <= 128, routing in one launch per 16 tokens and the
+    sort from its per-block histograms -- ragged last blocks, one 64-expert
+    range, expert counts not a multiple of 16)."""
     from nano_vllm_metal_amd import route_and_dispatch
 
-    H, E, k, act, gs = 2048, 128, 8, "bfloat16", 64
-    x, router = _route_case(3000 + T, T, H, E, k, act, gs, True)
+    H, act, gs = 2048, "bfloat16", 64
+    x, router = _route_case(3000 + T + E, T, H, E, k, act, gs, True)
     _, _, ids_ref, sc_ref = O.route_topk(x, *router, gs, k, True, act)
     off_ref, srt_ref = O.dispatch(ids_ref, E)
     ids, scores, off, srt = route_and_dispatch(to_act(x, act, DEV), qweights(router, act, gs, DEV),
@@ -375,6 +380,20 @@ def test_moe_reference_test_shape(regime):
 def test_moe_30b_decode(T):
     x, w = _moe_case(100 + T, T, 2048, 128, 768, "bfloat16")
     _check_moe(x, w, 8, True, "bfloat16", 64, "auto")
+
+
+@pytest.mark.parametrize("T,E", [(1, 128), (8, 128), (32, 128), (64, 128), (16, 64), (40, 512),
+                                 (3, 1)])
+@pytest.mark.parametrize("static", ["0", "1"])
+def test_moe_decode_expert_major_and_dealt(T, E, static, monkeypatch):
+    """The decode products (K 2048 and 768) as expert-major blocks (weights
+    requested before the routing; blocks of untouched experts end at once)
+    and as dealt units, each forced at every batch size: few touched experts,
+    four blocks per expert (E = 64), more blocks than CUs (E = 512), one
+    expert over 48 blocks."""
+    monkeypatch.setenv("NVM_GEMV_STATIC", static)
+    x, w = _moe_case(150 + T + E, T, 2048, E, 768, "bfloat16")
+    _check_moe(x, w, min(8, E), True, "bfloat16", 64, "decode")
 
 
 @pytest.mark.parametrize("H,I,T_full", [(2048, 768, 64), (4096, 1536, 32)])
