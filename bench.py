@@ -690,6 +690,8 @@ KERNEL_KEYS = (
     ("prefill_down_stage", r"gemm_kernel<1, false, false>"),
     ("prefill_act_f16", r"act_to_f16_kernel"),
     ("route_partial", r"route_mfma_kernel<1|route_i8_kernel<1"),
+    ("route_i8_fin", r"route_i8_fin_kernel<1"),
+    ("dispatch_hist", r"dispatch_hist_kernel"),
     ("route_finalize_dispatch", r"route_finalize_dispatch_kernel<1"),
     ("route_finalize", r"route_finalize_kernel<1"),
     ("dispatch_count", r"dispatch_count_kernel"),

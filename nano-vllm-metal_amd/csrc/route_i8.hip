@@ -453,7 +453,9 @@ int route_i8_splits(int64_t T, int64_t H, int64_t E) {
 }
 
 bool route_i8_fin_supports(int64_t T, int64_t H, int64_t E, int gs, int k) {
-  return route_i8_applies(T, H) && gs % 64 == 0 && E <= 128 && k <= kRowTopK && H / gs <= kSbGroups;
+  // (E a multiple of 4: the sort reads the histograms four experts at a time)
+  return route_i8_applies(T, H) && gs % 64 == 0 && E <= 128 && E % 4 == 0 && k <= kRowTopK &&
+         H / gs <= kSbGroups;
 }
 
 hipError_t launch_route_i8_fin(int dtype, const void *x, int64_t T, int64_t H, const uint32_t *wr,
