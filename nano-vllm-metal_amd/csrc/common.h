@@ -118,6 +118,33 @@ __device__ __forceinline__ float silu_act(float g) {
   return round_act<DT>(g * sg);
 }
 
+// Two values rounded to the activation dtype and back with one packed
+// conversion (each rounds as round_act rounds it).
+template <int DT>
+__device__ __forceinline__ void round_act2(float &a, float &b) {
+  const uint32_t p = Act<DT>::pack2(a, b);
+  a = Act<DT>::lo(p);
+  b = Act<DT>::hi(p);
+}
+
+// SwiGLU of two gate/up pairs of act values: the act pair
+// (rnd(silu_act(g0) * u0), rnd(silu_act(g1) * u1)), packed as Act::pack2
+// packs it.  Each rounding of silu_act, done for two values at once.
+template <int DT>
+__device__ __forceinline__ uint32_t swiglu_act2(float g0, float g1, float u0, float u1) {
+  float e0 = __expf(-fabsf(g0)), e1 = __expf(-fabsf(g1));
+  round_act2<DT>(e0, e1);
+  float d0 = 1.0f + e0, d1 = 1.0f + e1;
+  round_act2<DT>(d0, d1);
+  float s0 = __builtin_amdgcn_rcpf(d0), s1 = __builtin_amdgcn_rcpf(d1);
+  round_act2<DT>(s0, s1);
+  float t0 = 1.0f - s0, t1 = 1.0f - s1;
+  round_act2<DT>(t0, t1);
+  float r0 = g0 * (g0 < 0.0f ? t0 : s0), r1 = g1 * (g1 < 0.0f ? t1 : s1);
+  round_act2<DT>(r0, r1);
+  return Act<DT>::pack2(r0 * u0, r1 * u1);
+}
+
 // Round a float64 value to a floating format with `prec` significant bits and
 // smallest normal exponent `emin`, ties to even, directly from float64.  The
 // scaling by a power of two and rint() are both exact, so this is the single

@@ -19,8 +19,9 @@
 // biases come in windows of four groups.  The four wavefronts split the tile along N: a
 // wavefront owns 2 x 32 weight rows (gate/up: the same 32 columns of both
 // matrices, so the SwiGLU pair lands in one lane) and all 128 routed rows
-// (4 x 2 tiles of v_mfma_f32_32x32x16).  Each weight word is dequantised once
-// per tile, in registers, right before its MFMA.
+// (4 x 2 tiles of v_mfma_f32_32x32x16, weights as the A operand).  Each
+// weight word is dequantised once per tile, in registers, right before its
+// MFMA.  Outputs leave through an LDS tile, as whole rows of 16-byte stores.
 //
 // Operands are fp16 for both activation dtypes.  A weight q*s + b (s, b of
 // 8 or 11 significant bits, q of 4) needs about 12 significant bits: rounded
@@ -116,12 +117,6 @@ __device__ __forceinline__ uint32_t sb_pair_h(uint32_t bits) {
   else
     h = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float(bits << 16));
   return h | (h << 16);
-}
-
-// fp16 bits of x, rounded toward zero as v_cvt_pkrtz_f16_f32 rounds (the
-// conversion act_to_h applies to bf16 activations)
-__device__ __forceinline__ uint16_t f16_rtz(float x) {
-  return (uint16_t)(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x, x)) & 0xFFFFu);
 }
 
 __device__ __forceinline__ f32x16 mfma32_h(u32x4 a, u32x4 b, f32x16 c) {
@@ -346,7 +341,10 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
   const uint32_t magic = vgpr_const(0x64006400u);  // fp16 (1024, 1024)
   // Software-pipelined over the four 16-wide chunks: the A reads and the
   // dequantisation of chunk c + 1 are issued ahead of chunk c's MFMAs.
-  auto compute = [&](int ks) {
+  // NA: the 32-row blocks of routed rows computed (the tile's rows lie in
+  // the first NA; the others' A reads and MFMAs are left out).
+  auto compute = [&](int ks, auto NA) {
+    constexpr int na = decltype(NA)::value;
     const uint8_t *As = smem + (ks & 1) * A_STAGE;
     const uint8_t *Bs = smem + 2 * A_STAGE + ((ks >> 1) & 1) * B_STAGE + 32 * (ks & 1);
     u32x4 bw[2];
@@ -355,7 +353,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
     auto load_a = [&](int c, u32x4 (&af)[4]) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        af[i] = *(const u32x4 *)(As + (32 * i + l32) * A_PITCH + 16 * (4 * h + c));
+        if (i < na) af[i] = *(const u32x4 *)(As + (32 * i + l32) * A_PITCH + 16 * (4 * h + c));
     };
     auto deq = [&](int c, u32x4 (&bf)[2]) {
 #pragma unroll
@@ -374,7 +372,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
 #pragma unroll
       for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[s][i] = mfma32_h(af[i], bf[s], acc[s][i]);
+        for (int i = 0; i < 4; ++i)
+          if (i < na) acc[s][i] = mfma32_h(bf[s], af[i], acc[s][i]);
       if (c < 3) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) af[i] = afn[i];
@@ -390,61 +389,107 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
   // then ks + 1 (issued a k-step earlier) is stored into the other stage,
   // and at the end of an odd k-step the next pair's weights.  Two k-steps per
   // loop trip keep the register sets static.
-  Stage g0, g1;
-  PairB gb;
-  issue(g0, 0);
-  issue_b(gb, 0);
-  issue(g1, 1);
-  store(g0, 0);
-  store_b(gb, 0);
-  take_sb(0);
-  __syncthreads();
-  int ks = 0;
-  for (; ks + 1 < nk; ks += 2) {
-    // even k-step
-    issue(g0, ks + 2);
-    issue_b(gb, ks + 2);
-    compute(ks);
-    store(g1, 1);
-    take_sb(ks + 1);
+  auto k_loop = [&](auto NA) {
+    Stage g0, g1;
+    PairB gb;
+    issue(g0, 0);
+    issue_b(gb, 0);
+    issue(g1, 1);
+    store(g0, 0);
+    store_b(gb, 0);
+    take_sb(0);
     __syncthreads();
-    // odd k-step
-    issue(g1, ks + 3);
-    compute(ks + 1);
-    if (ks + 2 < nk) {
-      store(g0, 0);
-      store_b(gb, ((ks + 2) >> 1) & 1);
-      take_sb(ks + 2);
+    int ks = 0;
+    for (; ks + 1 < nk; ks += 2) {
+      // even k-step
+      issue(g0, ks + 2);
+      issue_b(gb, ks + 2);
+      compute(ks, NA);
+      store(g1, 1);
+      take_sb(ks + 1);
+      __syncthreads();
+      // odd k-step
+      issue(g1, ks + 3);
+      compute(ks + 1, NA);
+      if (ks + 2 < nk) {
+        store(g0, 0);
+        store_b(gb, ((ks + 2) >> 1) & 1);
+        take_sb(ks + 2);
+      }
+      __syncthreads();
     }
-    __syncthreads();
-  }
-  if (ks < nk) compute(ks);  // an odd count: the last k-step, already staged
+    if (ks < nk) compute(ks, NA);  // an odd count: the last k-step, already staged
+  };
+  // A tile of at most 64 routed rows (an expert's last, short tile) runs the
+  // k-steps with a half or a quarter of the MFMAs.
+  if (mcnt > 64)
+    k_loop(std::integral_constant<int, 4>{});
+  else if (mcnt > 32)
+    k_loop(std::integral_constant<int, 2>{});
+  else
+    k_loop(std::integral_constant<int, 1>{});
 
-  // C fragment of v_mfma_f32_32x32x16: lane l, register 4*q+j holds row
-  // 8*q + 4*(l/32) + j, column l%32
+  // Epilogue through LDS.  The MFMAs take the weights as A and the routed
+  // rows as B, so lane l holds routed row 32 i + l % 32 of every accumulator
+  // and, in register 4 q + j, weight column 8 q + 4 (l / 32) + j of its 32:
+  // four consecutive output columns, written to a [BM][OCOLS] tile over the
+  // staging buffers with one 8-byte LDS store.  The block then writes each
+  // routed row's OCOLS outputs with 16-byte stores (whole 128-byte lines of
+  // the output row), where one 2-byte store per value and lane had covered
+  // two rows' 64 bytes.
+  constexpr int OCOLS = DUAL ? WROWS / 2 : WROWS;
+  constexpr int O_PITCH = 2 * OCOLS + 16;  // bytes (+16: rows start 4 banks apart)
+  static_assert(BM * O_PITCH <= kGemmLds, "output tile exceeds the staging LDS");
+  __syncthreads();  // every wavefront is done with the stages
+  uint8_t *Os = smem;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    uint8_t *orow = Os + (32 * i + l32) * O_PITCH;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int m = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-      if (m >= mcnt) continue;
-      uint16_t *op = a.out + (int64_t)s_orow[m] * a.out_ld;
+    for (int q = 0; q < 4; ++q) {
       if (DUAL) {
-        const int col = n0 + 32 * wv + l32;
-        if (col < R) {
-          const float gv = round_act<DT>(acc[0][i][r]);
-          const float uv = round_act<DT>(acc[1][i][r]);
-          const uint16_t o = A::from_f32(silu_act<DT>(gv) * uv);
-          // (out_h: the act value in the fp16 form of the down product's staging)
-          op[col] = DT == DT_BF16 && a.out_h ? f16_rtz(A::to_f32(o)) : o;
+        // silu(gate) * up of the act-rounded sums, op by op as silu_act
+        uint32_t o[2];
+#pragma unroll
+        for (int j = 0; j < 4; j += 2) {
+          float g0 = acc[0][i][4 * q + j], g1 = acc[0][i][4 * q + j + 1];
+          float u0 = acc[1][i][4 * q + j], u1 = acc[1][i][4 * q + j + 1];
+          round_act2<DT>(g0, g1);
+          round_act2<DT>(u0, u1);
+          const uint32_t v = swiglu_act2<DT>(g0, g1, u0, u1);
+          // (out_h: the act values in the fp16 form of the down product's
+          // staging, rounded toward zero as act_to_h rounds them)
+          o[j >> 1] = DT == DT_BF16 && a.out_h
+                          ? __builtin_bit_cast(uint32_t,
+                                               __builtin_amdgcn_cvt_pkrtz(A::lo(v), A::hi(v)))
+                          : v;
         }
+        *(u32x2 *)(orow + 2 * (32 * wv + 8 * q + 4 * h)) = u32x2{o[0], o[1]};
       } else {
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const int col = n0 + 64 * wv + 32 * s + l32;
-          if (col < R) op[col] = A::from_f32(acc[s][i][r]);
-        }
+        for (int s = 0; s < 2; ++s)
+          *(u32x2 *)(orow + 2 * (64 * wv + 32 * s + 8 * q + 4 * h)) =
+              u32x2{A::pack2(acc[s][i][4 * q], acc[s][i][4 * q + 1]),
+                    A::pack2(acc[s][i][4 * q + 2], acc[s][i][4 * q + 3])};
       }
+    }
+  }
+  __syncthreads();
+  // 16-byte chunk c of rows tid / CPR + k * (256 / CPR); columns past R are
+  // not written, and rows whose 16 bytes are not 16-byte aligned in `out`
+  // are written a value at a time
+  constexpr int CPR = OCOLS / 8;
+  const int c = tid % CPR, col = n0 + 8 * c;
+  const bool vec = (a.out_ld & 7) == 0 && ((uintptr_t)a.out & 15) == 0 && col + 8 <= R;
+  for (int r = tid / CPR; r < mcnt; r += 256 / CPR) {
+    const u32x4 v = *(const u32x4 *)(Os + r * O_PITCH + 16 * c);
+    uint16_t *op = a.out + (int64_t)s_orow[r] * a.out_ld + col;
+    if (vec) {
+      *(u32x4 *)op = v;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (col + e < R) op[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
     }
   }
 }
