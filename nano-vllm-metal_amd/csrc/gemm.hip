@@ -50,13 +50,20 @@ constexpr int BM = kGemmBM;       // routed rows per tile
 constexpr int WROWS = 256;        // weight rows per tile
 constexpr int BK = 64;            // k per stage
 constexpr int A_PITCH = 144;      // bytes per staged activation row (128 + 16 pad)
-// bytes per staged weight row: the packed codes of two k-steps (64) + 16 pad
-constexpr int B_PITCH = 80;
+// bytes per staged weight row: the packed codes of two k-steps, as four
+// 16-byte chunks, chunk c of row r at slot c ^ ((r >> 2) & 3) (16 consecutive
+// rows' chunk c then fall in distinct banks)
+constexpr int B_PITCH = 64;
 constexpr int A_STAGE = BM * A_PITCH;
 constexpr int B_STAGE = WROWS * B_PITCH;
-// two activation stages (one k-step each) and two weight stages (a k-step
-// pair each): 76 KB, two blocks per CU
-constexpr int kGemmLds = 2 * A_STAGE + 2 * B_STAGE;
+// scales and biases of a wavefront's 32 (x 2) weight rows over one window of
+// eight groups: per row and group the fp16 (scale 0, bias 0, scale 1, bias 1);
+// 72-byte rows (eight groups + 8 pad: 32 rows' 8-byte reads in distinct banks)
+constexpr int W_PITCH = 72;
+constexpr int W_WAVE = 32 * W_PITCH;
+// two activation stages (one k-step each), two weight stages (a k-step pair
+// each) and the four wavefronts' scale/bias windows: 77 KB, two blocks per CU
+constexpr int kGemmLds = 2 * A_STAGE + 2 * B_STAGE + 4 * W_WAVE;
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
@@ -107,16 +114,14 @@ __device__ __forceinline__ u32x4 act_to_h(u32x4 v) {
   }
 }
 
-// A scale or bias (act bits) as the fp16 pair (v, v); bf16 values convert
-// with round to nearest even (exactly, inside fp16's normal range).
+// A scale or bias (act bits) as fp16 bits; bf16 values convert with round to
+// nearest even (exactly, inside fp16's normal range).
 template <int DT>
-__device__ __forceinline__ uint32_t sb_pair_h(uint32_t bits) {
-  uint32_t h;
+__device__ __forceinline__ uint32_t sb_h(uint32_t bits) {
   if constexpr (DT == DT_F16)
-    h = bits & 0xFFFFu;
+    return bits & 0xFFFFu;
   else
-    h = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float(bits << 16));
-  return h | (h << 16);
+    return __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float(bits << 16));
 }
 
 __device__ __forceinline__ f32x16 mfma32_h(u32x4 a, u32x4 b, f32x16 c) {
@@ -131,7 +136,9 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_arow[BM];
   __shared__ int s_orow[BM];
-  __shared__ int s_tiles[kMaxExperts + 1];
+  // (the m-tile list, read only before the first stage is stored)
+  int *const s_tiles = (int *)smem;
+  static_assert((kMaxExperts + 1) * 4 <= A_STAGE, "m-tile list exceeds an activation stage");
 
   hoist_args(a.act, a.act_ld, a.act_rows, a.a_map, a.a_div, a.offsets, a.w0, a.s0, a.b0, a.w1,
              a.s1, a.b1, a.R, a.K, a.gs, a.E, a.out, a.o_map, a.out_ld, n_tiles);
@@ -258,13 +265,14 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
       g.b[c] = bload16(c < 2 ? rw0 : rw1, ok ? b_voff[c] : kMaskedOffset, sb);
   };
   // Scales and biases of the lane's two weight rows come in windows of eight
-  // groups split over the lane halves: half h holds groups 4h..4h+3 of the
-  // window, one 8-byte load per row and matrix every eight groups, and a
-  // k-step takes its group's value from the half that holds it with one
-  // v_permlane32_swap (lanes l and l + 32 own the same rows).  (One 2-byte
-  // load per k-step made as many memory requests as the activation and
-  // weight loads together: each lane reads a different row.)  The next window
-  // is requested, into the same registers, once the last group is taken.
+  // groups split over the lane halves: half h loads groups 4h..4h+3 of the
+  // window, one 8-byte load per row and matrix every eight groups (lanes l
+  // and l + 32 own the same rows).  (One 2-byte load per k-step made as many
+  // memory requests as the activation and weight loads together: each lane
+  // reads a different row.)  At a window's first k-step the wavefront moves
+  // the window, arrived in registers, to its rows' LDS as fp16 values, and
+  // requests the next window into the same registers: it has the window's
+  // eight groups of k-steps to arrive.
   u32x2 wcur[4];  // scale 0, bias 0, scale 1, bias 1
   // (A half's four groups are one 8-byte load when a row's groups are a
   // multiple of four: they then start on a dword and end inside their row.
@@ -304,7 +312,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
     uint8_t *Bs = smem + 2 * A_STAGE + pbuf * B_STAGE;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      *(u32x4 *)(Bs + ((tid >> 2) + 64 * c) * B_PITCH + 16 * (tid & 3)) = g.b[c];
+      *(u32x4 *)(Bs + ((tid >> 2) + 64 * c) * B_PITCH + 16 * ((tid & 3) ^ ((tid >> 4) & 3))) =
+          g.b[c];
   };
 
   f32x16 acc[2][4];
@@ -316,25 +325,31 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
       for (int r = 0; r < 16; ++r) acc[s][i][r] = 0.f;
 
   // k-step ks's scale and bias of the lane's two weight rows, fp16 pairs
-  // (k-step ks lies in group ks * 64 / gs; calls come in k-step order)
+  // (k-step ks lies in group ks * 64 / gs; calls come in k-step order).  The
+  // window in LDS: per row of the wavefront and group, the fp16 values
+  // (scale 0, bias 0, scale 1, bias 1); only the wavefront itself writes and
+  // reads its rows, in order.
+  uint8_t *const w_lds = smem + 2 * A_STAGE + 2 * B_STAGE + wv * W_WAVE + l32 * W_PITCH;
   uint32_t sc[2], bi[2];
   auto take_sb = [&](int ks) {
-    const int g = ks * BK / a.gs;
-    const int j = g & 7;
-    // the word of group j in every lane: half (j >> 2)'s copy, both halves'
-    // after the swap
-    auto pick = [&](const u32x2 &w) {
-      const uint32_t x = (j & 2) ? w.y : w.x;
-      const auto pr = __builtin_amdgcn_permlane32_swap(x, x, false, false);
-      return ((j & 4) ? pr[1] : pr[0]) >> (16 * (j & 1));
-    };
+    const int j = (ks * BK / a.gs) & 7;
+    if ((ks * BK) % (8 * a.gs) == 0) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      sc[s] = sb_pair_h<DT>(pick(wcur[2 * s]));
-      bi[s] = sb_pair_h<DT>(pick(wcur[2 * s + 1]));
+      for (int i = 0; i < 4; ++i) {  // group 4h + i: value i of the half's four
+        auto val = [&](const u32x2 &w) {
+          const uint32_t d = (i & 2) ? w.y : w.x;
+          return sb_h<DT>((i & 1) ? d >> 16 : d & 0xFFFFu);
+        };
+        *(u32x2 *)(w_lds + 8 * (4 * h + i)) =
+            u32x2{val(wcur[0]) | (val(wcur[1]) << 16), val(wcur[2]) | (val(wcur[3]) << 16)};
+      }
+      issue_w(wcur, ++w_idx);
     }
-    // the window's last k-step: the next window, in the same registers
-    if (j == 7 && (ks + 1) * BK / a.gs != g) issue_w(wcur, ++w_idx);
+    const u32x2 v = *(const u32x2 *)(w_lds + 8 * j);
+    sc[0] = perm_b32(v.x, v.x, 0x01000100u);
+    bi[0] = perm_b32(v.x, v.x, 0x03020302u);
+    sc[1] = perm_b32(v.y, v.y, 0x01000100u);
+    bi[1] = perm_b32(v.y, v.y, 0x03020302u);
   };
   // nibble-expansion constants in registers (one v_and_or_b32 per dword)
   const uint32_t nib_mask = sgpr_const(0x000F000Fu);
@@ -346,10 +361,12 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
   auto compute = [&](int ks, auto NA) {
     constexpr int na = decltype(NA)::value;
     const uint8_t *As = smem + (ks & 1) * A_STAGE;
-    const uint8_t *Bs = smem + 2 * A_STAGE + ((ks >> 1) & 1) * B_STAGE + 32 * (ks & 1);
+    const uint8_t *Bs = smem + 2 * A_STAGE + ((ks >> 1) & 1) * B_STAGE;
     u32x4 bw[2];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) bw[s] = *(const u32x4 *)(Bs + lrow[s] * B_PITCH + 16 * h);
+    for (int s = 0; s < 2; ++s)
+      bw[s] = *(const u32x4 *)(Bs + lrow[s] * B_PITCH +
+                               16 * ((2 * (ks & 1) + h) ^ ((lrow[s] >> 2) & 3)));
     auto load_a = [&](int c, u32x4 (&af)[4]) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
