@@ -92,7 +92,8 @@ __device__ __forceinline__ u32x4 dequant8_h(uint32_t w, uint32_t s2, uint32_t b2
 }
 
 // Eight consecutive activations x0..x7 (one 16-byte chunk of a row) -> fp16
-// in the pair order (x0,x4)(x1,x5)(x2,x6)(x3,x7) of dequant8_h.  bf16 values
+// in the pair order (x0,x4)(x1,x5)(x2,x6)(x3,x7) of dequant8_h.  (Activations
+// that arrive in fp16, GroupedArgs::act_h, are in that order already.)  bf16 values
 // convert exactly (fp16 carries more significand bits) within fp16's range;
 // v_cvt_pkrtz_f16_f32 only rounds below it (|x| < 2^-14, with a contribution
 // far under the product's rounding) and saturates above 65504.
@@ -306,7 +307,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       *(u32x4 *)(As + ((tid >> 3) + 32 * c) * A_PITCH + 16 * (tid & 7)) =
-          act_to_h<AH ? DT_F16 : DT>(g.a[c]);
+          (AH ? g.a[c] : act_to_h<DT>(g.a[c]));
   };
   auto store_b = [&](const PairB &g, int pbuf) {
     uint8_t *Bs = smem + 2 * A_STAGE + pbuf * B_STAGE;
@@ -499,7 +500,9 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
   const int c = tid % CPR, col = n0 + 8 * c;
   const bool vec = (a.out_ld & 7) == 0 && ((uintptr_t)a.out & 15) == 0 && col + 8 <= R;
   for (int r = tid / CPR; r < mcnt; r += 256 / CPR) {
-    const u32x4 v = *(const u32x4 *)(Os + r * O_PITCH + 16 * c);
+    u32x4 v = *(const u32x4 *)(Os + r * O_PITCH + 16 * c);
+    // (out_h: each 16-byte chunk in the pair order the down product stages)
+    if (DUAL && DT == DT_BF16 && a.out_h) v = pair_order(v);
     uint16_t *op = a.out + (int64_t)s_orow[r] * a.out_ld + col;
     if (vec) {
       *(u32x4 *)op = v;
@@ -543,18 +546,20 @@ hipError_t launch_t(bool dual, const GroupedArgs &a, int64_t max_m_tiles, hipStr
   return hipGetLastError();
 }
 
-// bf16 -> fp16 as act_to_h converts (pairs in natural order), eight values a
-// thread
+// bf16 -> fp16 as act_to_h converts, eight values a thread, stored in the
+// pair order (x0,x4)(x1,x5)(x2,x6)(x3,x7)
 __global__ __launch_bounds__(256) void act_to_f16_kernel(const uint16_t *__restrict__ x,
                                                         int64_t n8, uint16_t *__restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n8) return;
   const u32x4 v = ldg16(x + 8 * i);
   u32x4 o;
+  auto el = [&](int i) {
+    return __uint_as_float((i & 1) ? (v[i >> 1] & 0xFFFF0000u) : (v[i >> 1] << 16));
+  };
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    o[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(v[j] << 16),
-                                                                   __uint_as_float(v[j] & 0xFFFF0000u)));
+    o[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(el(j), el(j + 4)));
   *(u32x4 *)(out + 8 * i) = o;
 }
 

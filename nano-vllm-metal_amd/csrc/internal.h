@@ -45,9 +45,11 @@ struct GroupedArgs {
   int32_t *r_offsets, *r_sorted;
   // Prefill GEMM with bf16 activations only: act_h says `act` holds the
   // activations already in the fp16 form the GEMM's staging makes of them
-  // (launch_act_to_f16), and out_h has the gate/up epilogue store its
-  // bf16-rounded outputs in that form too (the act of a down product with
-  // act_h set).  The decode products ignore both.
+  // (launch_act_to_f16), each 16-byte chunk x0..x7 stored in the pair order
+  // (x0,x4)(x1,x5)(x2,x6)(x3,x7) of its MFMA operands, and out_h has the
+  // gate/up epilogue store its bf16-rounded outputs in that form too (the act
+  // of a down product with act_h set; R a multiple of 8).  The decode
+  // products ignore both.
   int act_h, out_h;
 };
 
@@ -138,8 +140,9 @@ constexpr int kGemmBN = 128;   // prefill tile columns per weight matrix
 hipError_t launch_gemm(int dtype, bool dual, const GroupedArgs &a, int64_t max_m_tiles,
                        hipStream_t st);
 // bf16 x [n] -> the fp16 values the prefill GEMM's staging makes of them
-// (round toward zero below fp16's normal range, saturating above it); n a
-// multiple of 8, 16-byte aligned buffers.
+// (round toward zero below fp16's normal range, saturating above it), each
+// 16-byte chunk in the pair order of GroupedArgs::act_h; n a multiple of 8,
+// 16-byte aligned buffers.
 hipError_t launch_act_to_f16(const void *x, int64_t n, void *out, hipStream_t st);
 
 // Combine fused with the residual add and RMSNorm that follow the MoE block

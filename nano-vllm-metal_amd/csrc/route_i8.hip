@@ -145,15 +145,19 @@ __device__ __forceinline__ void i8_wave_sums(rsrc_t xr, rsrc_t wrr, int xo, int 
     const u32x4 (&xv)[2] = cu.xv;
     const u32x2 (&wq)[kI8Tiles] = cu.wq;
     if (xh && xh_ok) {
-      // the fp16 copy of this lane's 16 activations (pairs in natural order)
+      // the fp16 copy of this lane's 16 activations, each 16-byte chunk of
+      // x0..x7 stored in the pair order (x0,x4)(x1,x5)(x2,x6)(x3,x7) the
+      // prefill GEMM's MFMA operands use
       u32x4 o[2];
+      auto el = [&](const u32x4 &v, int i) {
+        return __uint_as_float((i & 1) ? (v[i >> 1] & 0xFFFF0000u) : (v[i >> 1] << 16));
+      };
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          o[h][j] = __builtin_bit_cast(
-              uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(xv[h][j] << 16),
-                                                   __uint_as_float(xv[h][j] & 0xFFFF0000u)));
+          o[h][j] = __builtin_bit_cast(uint32_t,
+                                       __builtin_amdgcn_cvt_pkrtz(el(xv[h], j), el(xv[h], j + 4)));
       u32x4 *dst = (u32x4 *)((uint8_t *)xh + xo + 128 * ks);
       dst[0] = o[0];
       dst[1] = o[1];

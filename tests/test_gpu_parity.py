@@ -199,6 +199,7 @@ def test_quantized_matmul_matches_oracle(M, N, K, act, gs):
     (4096, 2048, 128, "float16", 128, "gemm"),
     (600, 768, 1024, "bfloat16", 128, "gemm"),   # 6 groups a row: windows of 2-byte loads
     (520, 192, 1024, "float16", 64, "gemm"),     # 3 k-steps: the last one after the pairs
+    (600, 1024, 528, "bfloat16", 64, "gemm"),    # last n-tile of 16 columns (epilogue bound)
 ])
 def test_quantized_matmul_dense_products(M, N, K, act, gs, path):
     from nano_vllm_metal_amd import quantized_matmul
