@@ -195,6 +195,80 @@ class Stages:
         return self.y
 
 
+class ForwardStages:
+    """The launches of nvm_moe_forward one stage at a time
+    (nvm_moe_forward_stage: 0 routing, 1 gate/up, 2 down, 3 combine), on a
+    workspace of their own: the kernels the layer runs, timed apart."""
+
+    def __init__(self, moe, T, dev):
+        import torch
+        from nano_vllm_metal_amd import _lib
+
+        self.lib, self.L, self.moe, self.dev = _lib.load(), _lib, moe, dev
+        E = moe.w_router.weight.shape[0]
+        H = moe.w_router.weight.shape[1] * 8
+        I = moe.w_gate.weight.shape[1]
+        k = moe.num_experts_per_tok
+        self.T, self.H, self.I, self.E, self.k = T, H, I, E, k
+        size = ctypes.c_size_t()
+        self.L.check(self.lib.nvm_moe_workspace_size(T, H, I, E, k, ctypes.byref(size)))
+        self.ws = torch.empty(size.value, dtype=torch.uint8, device=dev)
+        self.y = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+        self.ops = moe._operands()
+
+    def launch(self, stage, x):
+        L, m = self.L, self.moe
+        flat = [t.data_ptr() for trio in self.ops for t in trio]
+        L.check(self.lib.nvm_moe_forward_stage(
+            stage, x.data_ptr(), self.T, self.H, self.I, self.E, self.k,
+            int(bool(m.norm_topk_prob)), m.w_gate.group_size, m.w_gate.bits,
+            L.dtype_code(x.dtype), *flat, self.y.data_ptr(), None, None,
+            L.REGIME_AUTO, self.ws.data_ptr(), self.ws.numel(), L.stream_of(self.dev)))
+
+    def run(self, x, upto=4):
+        """Stages 0 .. upto-1."""
+        for s in range(upto):
+            self.launch(s, x)
+        return self.y
+
+
+def forward_stage_us(layers, xs, stage, n=64):
+    """Duration (us) of one stage of the layer's own launch sequence: a HIP
+    graph of `n` back-to-back launches of that stage (weight sets cycled, each
+    set's earlier stages run beforehand), timed with HIP events on the stream
+    the graph's kernels run on; the mean per launch, the figure that
+    `rocprofv3 --kernel-trace` reports as the kernel's average."""
+    import torch
+
+    T = xs[0].shape[0]
+    fs = [ForwardStages(m, T, layers[0].w_gate.weight.device) for m in layers]
+    # (each set's stages before this one: a later stage may overwrite what
+    # this one reads, as the down product overwrites the fp16 copy of x)
+    for i, f in enumerate(fs):
+        f.run(xs[i % len(xs)], upto=stage)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i, f in enumerate(fs):
+            f.launch(stage, xs[i % len(xs)])
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fs[i % len(fs)].launch(stage, xs[i % len(fs) % len(xs)])
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del fs
+    return e0.elapsed_time(e1) * 1e3 / n
+
+
 # route = routing and dispatch (nvm_moe_route_dispatch)
 STAGE_NAMES = ["route", "gateup", "down", "combine"]
 
@@ -350,6 +424,7 @@ def decode_bench(layers, T, steps, warmup, dev, use_graph=True, shape=None, n_me
     stages = [Stages(m, T, dev) for m in layers]
     graph_kernel_us = {n: stage_kernel_us(stages, xs, n) for n in ("gateup", "down")}
     del stages
+    fwd_kernel_us = {n: forward_stage_us(layers, xs, i) for i, n in enumerate(STAGE_NAMES)}
     gu_b, dn_b = bytes_per_expert(H, I, gs)
     avg_touched = sum(touched) / len(touched)
     layer_bytes = avg_touched * (gu_b + dn_b) + router_bytes(H, E, gs) + 2 * T * H * 2
@@ -368,11 +443,17 @@ def decode_bench(layers, T, steps, warmup, dev, use_graph=True, shape=None, n_me
         "eager_staged_layer_us": eager_layer_us,
         "kernel_us": stage_us,
         "kernel_us_back_to_back": graph_kernel_us,
+        "forward_kernel_us": fwd_kernel_us,
+        "forward_kernel_us_note": "the layer's own launches one stage at a time "
+                                  "(nvm_moe_forward_stage: route = partial logits, gateup = "
+                                  "gate/up with the routing finalised in its prologue), each a "
+                                  "HIP graph of 64 back-to-back launches timed with events",
         "touched_experts_avg": avg_touched,
         "layer_algorithmic_bytes": layer_bytes,
         "hbm_gbs": layer_bytes / (layer_us * 1e-6) / 1e9,
         "gateup_algorithmic_bytes": gateup_bytes,
         "gateup_gbs": gateup_bytes / (graph_kernel_us["gateup"] * 1e-6) / 1e9,
+        "forward_gateup_gbs": gateup_bytes / (fwd_kernel_us["gateup"] * 1e-6) / 1e9,
         "down_gbs": avg_touched * dn_b / (graph_kernel_us["down"] * 1e-6) / 1e9,
     }
 
@@ -387,6 +468,7 @@ def prefill_bench(layers, T, steps, warmup, dev, zipf, shape=None):
     # stage entry points, whose GEMMs convert their staged rows themselves
     stage_us, stage_layer_us, touched, ids = eager_stage_pass(layers, xs, steps, warmup, dev)
     layer_us = eager_fused_pass(layers, xs, steps, warmup, dev)
+    fwd_us = {n: forward_stage_us(layers, xs, i, n=16) for i, n in enumerate(STAGE_NAMES)}
     N = T * k
     gateup_flops = 2.0 * N * H * 2 * I
     down_flops = 2.0 * N * I * H
@@ -402,6 +484,13 @@ def prefill_bench(layers, T, steps, warmup, dev, zipf, shape=None):
         "kernel_us": stage_us,
         "kernel_us_note": "stage entry points (route+dispatch, gate/up, down, combine), "
                           "each timed with HIP events",
+        "forward_kernel_us": fwd_us,
+        "forward_kernel_us_note": "the layer's own launches one stage at a time "
+                                  "(nvm_moe_forward_stage; the GEMMs on the fp16 copies of x "
+                                  "and h), each a HIP graph of 16 back-to-back launches timed "
+                                  "with events",
+        "forward_gateup_tflops": gateup_flops / (fwd_us["gateup"] * 1e-6) / 1e12,
+        "forward_down_tflops": down_flops / (fwd_us["down"] * 1e-6) / 1e12,
         "layer_tflops": layer_flops / (layer_us * 1e-6) / 1e12,
         "gateup_tflops": gateup_flops / (stage_us["gateup"] * 1e-6) / 1e12,
         "down_tflops": down_flops / (stage_us["down"] * 1e-6) / 1e12,
@@ -941,7 +1030,7 @@ def main():
         f"{head['hbm_gbs']:.0f} GB/s, kernels {head['kernel_us']}")
 
     gu_b, _ = bytes_per_expert(H, I, gs)
-    achieved = head["gateup_gbs"]
+    achieved = head["forward_gateup_gbs"]
     out = {
         "metric": METRIC,
         "value": head["tokens_per_s"],
@@ -961,22 +1050,35 @@ def main():
                    "moe_intermediate": I, "group_size": gs, "bits": 4,
                    "weight_sets": args.layers, "timing": head["timing"]},
         "hbm_gbs": head["hbm_gbs"],
+        # BASELINE.md's GPU timing protocol: the median of >= 100 individually
+        # timed layer calls after 10 warm-ups, weight sets rotated
+        "median_protocol": {"layer_us": head["layer_us_median"],
+                            "tokens_per_s": head["tokens_per_s_median"],
+                            "samples": head["median_samples"],
+                            "hbm_gbs": head["layer_algorithmic_bytes"]
+                            / (head["layer_us_median"] * 1e-6) / 1e9
+                            if head["layer_us_median"] else None},
         "roofline": {
-            "kernel": "gemv3_kernel<bf16, gate/up+SwiGLU, K=2048> (nvm_moe_expert_gateup, decode)",
+            "kernel": "gemv3_kernel<bf16, gate/up+SwiGLU, routing finalised in the prologue, "
+                      "K=2048> (the layer's gate/up launch, nvm_moe_forward_stage 1)",
             "bound": "hbm",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": read_traffic("decode_gateup"),
+            "traffic": read_traffic("decode_gateup_fused"),
             "algorithmic_bytes_per_launch": head["gateup_algorithmic_bytes"],
-            "avg_launch_us": head["kernel_us_back_to_back"]["gateup"],
-            "timing": "HIP events around a graph of 64 back-to-back gate/up launches "
-                      "(8 weight sets cycled), mean per launch",
-            **rocprof_check("decode_gateup", head["gateup_algorithmic_bytes"], achieved),
-            # the same product with the routing finalised in its prologue, as
-            # the headline layer runs it (from the committed profile)
-            "fused_routing_rocprof_median_us": read_rocprof_us("decode_gateup_fused")[1],
+            "avg_launch_us": head["forward_kernel_us"]["gateup"],
+            "timing": "HIP events around a graph of 64 back-to-back launches of the layer's "
+                      "gate/up stage (8 weight sets cycled), mean per launch",
+            **rocprof_check("decode_gateup_fused", head["gateup_algorithmic_bytes"], achieved),
+            # the same product without the routing in its prologue (the stage
+            # entry point nvm_moe_expert_gateup), beside it
+            "stage_entry_point": {
+                "kernel": "gemv3_kernel<bf16, gate/up+SwiGLU, K=2048> (nvm_moe_expert_gateup)",
+                "avg_launch_us": head["kernel_us_back_to_back"]["gateup"],
+                "achieved": head["gateup_gbs"], "frac": head["gateup_gbs"] / HBM_PEAK_GBS,
+                "traffic": read_traffic("decode_gateup")},
         },
         "layer_roofline": {"bound": "hbm", "achieved": head["hbm_gbs"], "peak": HBM_PEAK_GBS,
                            "unit": "GB/s", "frac": head["hbm_gbs"] / HBM_PEAK_GBS,
@@ -1020,21 +1122,21 @@ def main():
                 f"prefill {out['e2e']['prefill_tokens_per_s']:.0f} tok/s")
         u = out["prefill"]["uniform"]
         out["prefill_roofline"] = {
-            "kernel": "gemm_kernel<bf16, gate/up+SwiGLU> (nvm_moe_expert_gateup, prefill; "
-                      "converts its staged bf16 rows to fp16 itself)",
-            "bound": "mfma", "achieved": u["gateup_tflops"], "peak": MFMA_BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": u["gateup_tflops"] / MFMA_BF16_PEAK_TFLOPS,
-            "traffic": read_traffic("prefill_gateup_stage"),
+            "kernel": "gemm_kernel<bf16, gate/up+SwiGLU, fp16 copy of x> (the layer's gate/up "
+                      "launch at 4096 tokens, nvm_moe_forward_stage 1)",
+            "bound": "mfma", "achieved": u["forward_gateup_tflops"],
+            "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": u["forward_gateup_tflops"] / MFMA_BF16_PEAK_TFLOPS,
+            "avg_launch_us": u["forward_kernel_us"]["gateup"],
+            "traffic": read_traffic("prefill_gateup"),
+            "layer_frac": u["layer_mfma_frac"],
         }
-        # the forward's gate/up GEMM (fp16 activations converted once), from
-        # the committed kernel trace of the same workload
         avg, med = read_rocprof_us("prefill_gateup", PROFILE_PREFILL)
-        if med is not None:
+        if avg is not None:
             fl = 2.0 * 4096 * SHAPE["k"] * SHAPE["H"] * 2 * SHAPE["I"]
-            out["prefill_roofline"]["forward_gateup"] = {
-                "rocprof_median_us": med, "tflops": fl / (med * 1e-6) / 1e12,
-                "frac": fl / (med * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-                "rocprof_profile": str(PROFILE_PREFILL.relative_to(ROOT))}
+            out["prefill_roofline"]["rocprof"] = {
+                "avg_us": avg, "median_us": med, "frac_from_avg": fl / (avg * 1e-6) / 1e12
+                / MFMA_BF16_PEAK_TFLOPS, "profile": str(PROFILE_PREFILL.relative_to(ROOT))}
     if not args.no_cpu:
         log(f"[bench] CPU baseline (~{args.cpu_seconds:.0f} s)")
         out["cpu_baseline"] = cpu_baseline(layers[0], args.batch, args.cpu_seconds, dev)

@@ -198,6 +198,26 @@ int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, i
                     void *workspace, size_t workspace_bytes, nvm_stream_t stream);
 
 /*
+ * One stage of nvm_moe_forward's launch sequence, for timing the block's
+ * kernels one at a time: 0 = routing and dispatch (decode batches: the
+ * partial logits only, the gate/up stage finalising the routing), 1 = gate/up
+ * products with SwiGLU, 2 = down products, 3 = combine.  Stage s reads what
+ * stages 0..s-1 of a call with the same arguments and workspace left there;
+ * stages 0..3 in order compute exactly what nvm_moe_forward computes (the
+ * Moe.__call__ steps of layers/moe.py:77-86, one at a time).  ids_out and
+ * scores_out, when given, must be the same in every stage; y is written by
+ * stage 3 only.
+ */
+int nvm_moe_forward_stage(int stage, const void *x, int64_t T, int64_t H, int64_t I, int64_t E,
+                          int top_k, int norm_topk_prob, int group_size, int bits, int dtype,
+                          const uint32_t *wr, const void *sr, const void *br,
+                          const uint32_t *wg, const void *sg, const void *bg,
+                          const uint32_t *wu, const void *su, const void *bu,
+                          const uint32_t *wd, const void *sd, const void *bd,
+                          void *y, int32_t *ids_out, void *scores_out, int regime,
+                          void *workspace, size_t workspace_bytes, nvm_stream_t stream);
+
+/*
  * nvm_moe_forward without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference: it is
@@ -211,6 +231,9 @@ int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, i
  * calls that overlap in time on one GPU (other streams, other threads) race.
  * Nothing in the array needs to start at zero (the routing kernels reset
  * the one counter they use).  The current device must be the stream's.
+ * nvm_moe_scratch_bytes also locates the current device's array: call it on
+ * each device before capturing a noalloc call into a HIP graph (otherwise
+ * the first call on a device locates it, which may load the code object).
  */
 int nvm_moe_scratch_bytes(size_t *bytes);
 int nvm_moe_forward_noalloc(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int top_k,

@@ -55,18 +55,23 @@ constexpr int64_t kMaxProductK = 8192;
 // Largest buffer the kernels' 32-bit buffer descriptors and offsets address.
 constexpr int64_t k2GiB = 0x7FFF0000ll;
 
-// Bump allocator over the caller's workspace (256-byte aligned slices).
+// Bump allocator over the caller's workspace: slices at 256-byte aligned
+// device addresses, whatever the alignment of the workspace itself.  Sizes
+// (Carve over nullptr) include 256 bytes of slack for the first slice's
+// alignment.
 struct Carve {
   size_t off = 0;
   char *base;
   explicit Carve(void *b) : base((char *)b) {}
   template <class T>
   T *take(size_t count) {
-    off = (off + 255) & ~(size_t)255;
+    off = (size_t)((((uintptr_t)base + off + 255) & ~(uintptr_t)255) - (uintptr_t)base);
     T *p = base ? (T *)(base + off) : nullptr;
     off += count * sizeof(T);
     return p;
   }
+  // bytes a workspace needs for the slices taken so far (base == nullptr)
+  size_t bytes() const { return ((off + 255) & ~(size_t)255) + 256; }
 };
 
 int check_quant(int group_size, int bits, int dtype) {
@@ -133,7 +138,7 @@ MoeWs carve_moe(void *base, int64_t T, int64_t H, int64_t I, int64_t E, int k) {
   w.done = c.take<unsigned>(1);
   w.h = c.take<uint16_t>((size_t)N * I);
   w.down = c.take<uint16_t>((size_t)N * H);
-  w.bytes = (c.off + 255) & ~(size_t)255;
+  w.bytes = c.bytes();
   return w;
 }
 
@@ -274,7 +279,8 @@ int moe_stages(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int to
                const void *bg, const uint32_t *wu, const void *su, const void *bu,
                const uint32_t *wd, const void *sd, const void *bd, int32_t *ids_out,
                void *scores_out, int regime, void *workspace, size_t workspace_bytes,
-               nvm_stream_t stream, MoeWs &ws, uint16_t *&scores);
+               nvm_stream_t stream, MoeWs &ws, uint16_t *&scores, int first = 0,
+               int last = 2);
 
 // Workspace of nvm_moe_forward_noalloc: a file-scope device array, one copy
 // per GPU, held until the process ends.  Host code never uses the array's
@@ -426,7 +432,7 @@ int nvm_route_dispatch_workspace_size(int64_t T, int64_t H, int64_t E, int top_k
   c.take<double>((size_t)nvm::route_workspace_splits(T, H, E) * T * E);
   c.take<int32_t>((size_t)nvm::dispatch_workspace_bytes(T * top_k, E) / sizeof(int32_t));
   c.take<unsigned>(1);
-  *bytes = (c.off + 255) & ~(size_t)255;
+  *bytes = c.bytes();
   return NVM_OK;
 }
 
@@ -462,7 +468,7 @@ int nvm_grouped_linear_workspace_size(int64_t n, int64_t D, int64_t O, int64_t E
   c.take<int32_t>(E + 1);
   c.take<int32_t>(n);
   c.take<int32_t>((size_t)nvm::dispatch_workspace_bytes(n, E) / sizeof(int32_t));
-  *bytes = (c.off + 255) & ~(size_t)255;
+  *bytes = c.bytes();
   return NVM_OK;
 }
 
@@ -579,9 +585,39 @@ int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, i
   return nvm_moe_combine(ws.down, scores, T, top_k, H, dtype, y, stream);
 }
 
+int nvm_moe_forward_stage(int stage, const void *x, int64_t T, int64_t H, int64_t I, int64_t E,
+                          int top_k, int norm_topk_prob, int group_size, int bits, int dtype,
+                          const uint32_t *wr, const void *sr, const void *br,
+                          const uint32_t *wg, const void *sg, const void *bg,
+                          const uint32_t *wu, const void *su, const void *bu,
+                          const uint32_t *wd, const void *sd, const void *bd, void *y,
+                          int32_t *ids_out, void *scores_out, int regime, void *workspace,
+                          size_t workspace_bytes, nvm_stream_t stream) {
+  NVM_REQUIRE(stage >= 0 && stage <= 3, "moe_stage: stage %d outside [0, 3]", stage);
+  NVM_REQUIRE(y || T == 0 || stage < 3, "moe_stage: null pointer");
+  MoeWs ws{};
+  uint16_t *scores = nullptr;
+  if (int r = moe_stages(x, T, H, I, E, top_k, norm_topk_prob, group_size, bits, dtype, wr, sr,
+                         br, wg, sg, bg, wu, su, bu, wd, sd, bd, ids_out, scores_out, regime,
+                         workspace, workspace_bytes, stream, ws, scores, stage, stage))
+    return r;
+  if (T == 0 || stage < 3) return NVM_OK;
+  return nvm_moe_combine(ws.down, scores, T, top_k, H, dtype, y, stream);
+}
+
 int nvm_moe_scratch_bytes(size_t *bytes) {
   NVM_REQUIRE(bytes, "moe_scratch_bytes: null output");
   *bytes = kScratchBytes;
+  // Locate the current device's array now, outside any graph capture (the
+  // lookup may load the code object).  Without a usable device this is a
+  // size query only; the first noalloc call then locates it.
+  int dev = -1;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    void *p = nullptr;
+    if (int r = scratch_for_current_device(&p)) return r;
+  } else {
+    (void)hipGetLastError();
+  }
   return NVM_OK;
 }
 
@@ -644,12 +680,20 @@ int moe_stages(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int to
                const void *bg, const uint32_t *wu, const void *su, const void *bu,
                const uint32_t *wd, const void *sd, const void *bd, int32_t *ids_out,
                void *scores_out, int regime, void *workspace, size_t workspace_bytes,
-               nvm_stream_t stream, MoeWs &ws, uint16_t *&scores) {
+               nvm_stream_t stream, MoeWs &ws, uint16_t *&scores, int first, int last) {
   if (int r = check_products(H, I, E, top_k, group_size, bits, dtype, regime)) return r;
   NVM_REQUIRE(T >= 0, "moe: bad shape");
   NVM_REQUIRE(x && wr && sr && br && wg && sg && bg && wu && su && bu && wd && sd && bd,
               "moe: null pointer");
   if (T == 0) return NVM_OK;
+  // Every kernel of the block addresses x, its fp16 copy, h and the router
+  // weights through 32-bit buffer offsets: refuse larger operands here,
+  // before the first launch, so that no stage runs on a batch a later stage
+  // would refuse.
+  NVM_SUPPORTED(T * H * 2 <= k2GiB && T * top_k * I * 2 <= k2GiB && E * (H / 2) <= k2GiB,
+                "moe: activations of %lld bytes, h of %lld bytes or router weights of %lld "
+                "bytes exceed 2 GiB; split the batch",
+                (long long)(T * H * 2), (long long)(T * top_k * I * 2), (long long)(E * (H / 2)));
   const size_t need = carve_moe(nullptr, T, H, I, E, top_k).bytes;
   if (!workspace || workspace_bytes < need)
     return fail(NVM_ERR_WORKSPACE, "moe: workspace of %zu bytes needed", need);
@@ -658,38 +702,44 @@ int moe_stages(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int to
   scores = scores_out ? (uint16_t *)scores_out : ws.scores;
   const int64_t N = T * top_k;
   hipStream_t st = (hipStream_t)stream;
+  // stages: 0 routing (and dispatch), 1 gate/up + SwiGLU, 2 down; each reads
+  // what the one before it left in the workspace
+  auto runs = [&](int s) { return first <= s && s <= last; };
   if (nvm::fused_route_supports(T, E, top_k) && use_decode(regime, N, E, H)) {
     // Decode batches: one launch of float64 partial logits, then the gate/up
     // product finalises the routing and sorts the pairs in every block's
     // prologue (block 0 stores ids, scores, offsets and the sorted pairs).
-    NVM_TRY_HIP(nvm::launch_route_partial_decode(dtype, x, T, H, wr, sr, br, E, group_size,
-                                                 ws.partial, st));
-    nvm::GroupedArgs g{};
-    g.act = (const uint16_t *)x;
-    g.act_ld = H;
-    g.act_rows = T;
-    g.a_div = top_k;
-    g.offsets = ws.offsets;
-    g.w0 = wg;
-    g.s0 = (const uint16_t *)sg;
-    g.b0 = (const uint16_t *)bg;
-    g.w1 = wu;
-    g.s1 = (const uint16_t *)su;
-    g.b1 = (const uint16_t *)bu;
-    g.R = (int)I;
-    g.K = (int)H;
-    g.gs = group_size;
-    g.E = (int)E;
-    g.out = ws.h;
-    g.out_ld = I;
-    g.route_part = ws.partial;
-    g.route_splits = nvm::decode_route_splits(T, H, E);
-    g.route_norm = norm_topk_prob;
-    g.r_ids = ids;
-    g.r_scores = scores;
-    g.r_offsets = ws.offsets;
-    g.r_sorted = ws.sorted;
-    if (int r = run_products(dtype, true, true, g, N, st)) return r;
+    if (runs(0))
+      NVM_TRY_HIP(nvm::launch_route_partial_decode(dtype, x, T, H, wr, sr, br, E, group_size,
+                                                   ws.partial, st));
+    if (runs(1)) {
+      nvm::GroupedArgs g{};
+      g.act = (const uint16_t *)x;
+      g.act_ld = H;
+      g.act_rows = T;
+      g.a_div = top_k;
+      g.offsets = ws.offsets;
+      g.w0 = wg;
+      g.s0 = (const uint16_t *)sg;
+      g.b0 = (const uint16_t *)bg;
+      g.w1 = wu;
+      g.s1 = (const uint16_t *)su;
+      g.b1 = (const uint16_t *)bu;
+      g.R = (int)I;
+      g.K = (int)H;
+      g.gs = group_size;
+      g.E = (int)E;
+      g.out = ws.h;
+      g.out_ld = I;
+      g.route_part = ws.partial;
+      g.route_splits = nvm::decode_route_splits(T, H, E);
+      g.route_norm = norm_topk_prob;
+      g.r_ids = ids;
+      g.r_scores = scores;
+      g.r_offsets = ws.offsets;
+      g.r_sorted = ws.sorted;
+      if (int r = run_products(dtype, true, true, g, N, st)) return r;
+    }
   } else {
     // Both products on the prefill GEMM, which computes in fp16: x is
     // converted once (into the down buffer, which only the down product
@@ -699,31 +749,40 @@ int moe_stages(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int to
     // would make.
     const bool gemm_both =
         dtype == NVM_DTYPE_BF16 && !use_decode(regime, N, E, H) && !use_decode(regime, N, E, I);
-    bool xh_done = false;
-    if (int r = run_route_dispatch(dtype, x, T, H, wr, sr, br, E, group_size, top_k,
-                                   norm_topk_prob, nullptr, ids, scores, ws.offsets, ws.sorted,
-                                   ws.partial, ws.counts, ws.done, st,
-                                   gemm_both ? ws.down : nullptr, &xh_done))
-      return r;
-    if (int r = check_products(H, I, E, top_k, group_size, bits, dtype, regime)) return r;
-    if (gemm_both) {
-      if (!xh_done) NVM_TRY_HIP(nvm::launch_act_to_f16(x, T * H, ws.down, st));
-      nvm::GroupedArgs g = gateup_args(ws.down, T, H, I, E, top_k, group_size, wg, sg, bg, wu, su,
-                                       bu, ws.offsets, ws.sorted, ws.h);
-      g.act_h = 1;
-      g.out_h = 1;
-      if (int r = run_products(dtype, false, true, g, N, st)) return r;
-      nvm::GroupedArgs d = down_args(ws.h, N, H, I, E, group_size, wd, sd, bd, ws.offsets,
-                                     ws.sorted, ws.down);
-      d.act_h = 1;
-      return run_products(dtype, false, false, d, N, st);
+    if (runs(0)) {
+      bool xh_done = false;
+      if (int r = run_route_dispatch(dtype, x, T, H, wr, sr, br, E, group_size, top_k,
+                                     norm_topk_prob, nullptr, ids, scores, ws.offsets, ws.sorted,
+                                     ws.partial, ws.counts, ws.done, st,
+                                     gemm_both ? ws.down : nullptr, &xh_done))
+        return r;
+      if (gemm_both && !xh_done) NVM_TRY_HIP(nvm::launch_act_to_f16(x, T * H, ws.down, st));
     }
-    if (int r = nvm_moe_expert_gateup(x, T, H, I, E, top_k, group_size, bits, dtype, wg, sg, bg,
-                                      wu, su, bu, ws.offsets, ws.sorted, ws.h, regime, stream))
-      return r;
+    if (gemm_both) {
+      if (runs(1)) {
+        nvm::GroupedArgs g = gateup_args(ws.down, T, H, I, E, top_k, group_size, wg, sg, bg, wu,
+                                         su, bu, ws.offsets, ws.sorted, ws.h);
+        g.act_h = 1;
+        g.out_h = 1;
+        if (int r = run_products(dtype, false, true, g, N, st)) return r;
+      }
+      if (runs(2)) {
+        nvm::GroupedArgs d = down_args(ws.h, N, H, I, E, group_size, wd, sd, bd, ws.offsets,
+                                       ws.sorted, ws.down);
+        d.act_h = 1;
+        if (int r = run_products(dtype, false, false, d, N, st)) return r;
+      }
+      return NVM_OK;
+    }
+    if (runs(1))
+      if (int r = nvm_moe_expert_gateup(x, T, H, I, E, top_k, group_size, bits, dtype, wg, sg, bg,
+                                        wu, su, bu, ws.offsets, ws.sorted, ws.h, regime, stream))
+        return r;
   }
-  return nvm_moe_expert_down(ws.h, N, H, I, E, group_size, bits, dtype, wd, sd, bd, ws.offsets,
-                             ws.sorted, ws.down, regime, stream);
+  if (runs(2))
+    return nvm_moe_expert_down(ws.h, N, H, I, E, group_size, bits, dtype, wd, sd, bd, ws.offsets,
+                               ws.sorted, ws.down, regime, stream);
+  return NVM_OK;
 }
 
 }  // namespace

@@ -547,12 +547,21 @@ hipError_t launch_t(bool dual, const GroupedArgs &a, int64_t max_m_tiles, hipStr
 }
 
 // bf16 -> fp16 as act_to_h converts, eight values a thread, stored in the
-// pair order (x0,x4)(x1,x5)(x2,x6)(x3,x7)
+// pair order (x0,x4)(x1,x5)(x2,x6)(x3,x7).  ALIGNED: x is 16-byte aligned
+// (one 16-byte load a thread, else eight 2-byte loads).
+template <bool ALIGNED>
 __global__ __launch_bounds__(256) void act_to_f16_kernel(const uint16_t *__restrict__ x,
                                                         int64_t n8, uint16_t *__restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n8) return;
-  const u32x4 v = ldg16(x + 8 * i);
+  u32x4 v;
+  if constexpr (ALIGNED) {
+    v = ldg16(x + 8 * i);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      v[j] = (uint32_t)x[8 * i + 2 * j] | ((uint32_t)x[8 * i + 2 * j + 1] << 16);
+  }
   u32x4 o;
   auto el = [&](int i) {
     return __uint_as_float((i & 1) ? (v[i >> 1] & 0xFFFF0000u) : (v[i >> 1] << 16));
@@ -573,11 +582,16 @@ hipError_t launch_gemm(int dtype, bool dual, const GroupedArgs &a, int64_t max_m
 }
 
 hipError_t launch_act_to_f16(const void *x, int64_t n, void *out, hipStream_t st) {
-  if (n % 8 || ((uintptr_t)x | (uintptr_t)out) % 16) return hipErrorInvalidValue;
+  if (n % 8 || (uintptr_t)out % 16 || (uintptr_t)x % 2) return hipErrorInvalidValue;
   const int64_t n8 = n / 8;
   if (n8 == 0) return hipSuccess;
-  hipLaunchKernelGGL(act_to_f16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st,
-                     (const uint16_t *)x, n8, (uint16_t *)out);
+  const dim3 grid((unsigned)((n8 + 255) / 256));
+  if ((uintptr_t)x % 16 == 0)
+    hipLaunchKernelGGL(act_to_f16_kernel<true>, grid, dim3(256), 0, st, (const uint16_t *)x, n8,
+                       (uint16_t *)out);
+  else
+    hipLaunchKernelGGL(act_to_f16_kernel<false>, grid, dim3(256), 0, st, (const uint16_t *)x, n8,
+                       (uint16_t *)out);
   return hipGetLastError();
 }
 

@@ -158,7 +158,7 @@ __device__ __forceinline__ void i8_wave_sums(rsrc_t xr, rsrc_t wrr, int xo, int 
         for (int j = 0; j < 4; ++j)
           o[h][j] = __builtin_bit_cast(uint32_t,
                                        __builtin_amdgcn_cvt_pkrtz(el(xv[h], j), el(xv[h], j + 4)));
-      u32x4 *dst = (u32x4 *)((uint8_t *)xh + xo + 128 * ks);
+      u32x4 *dst = (u32x4 *)((uint8_t *)xh + (int64_t)xo + 128 * ks);
       dst[0] = o[0];
       dst[1] = o[1];
     }

@@ -191,11 +191,14 @@ class Moe:
                                               ctypes.byref(size)))
         if self._ws is None or self._ws.numel() < size.value or self._ws.device != dev:
             # A HIP graph captured earlier may still refer to the old buffer:
-            # it stays alive with the block (each replacement is larger, so
-            # the retired buffers total less than the current one).
+            # it stays alive with the block.  Replacements at least double
+            # in size, so the retired buffers total less than the current one.
+            need = size.value
             if self._ws is not None:
+                if self._ws.device == dev:
+                    need = max(need, 2 * self._ws.numel())
                 self._retired_ws.append(self._ws)
-            self._ws = _workspace(size.value, dev)
+            self._ws = _workspace(need, dev)
         return self._ws
 
     def check_operands(self, act: torch.dtype, H: int):

@@ -124,6 +124,11 @@ def test_operands_beyond_32bit_offsets_are_refused():
     assert r == L.NVM_ERR_UNSUPPORTED and "2 GiB" in _err(lib)
     r = lib.nvm_quantized_matmul(1, 1, 64, 4, 1, 1, 1, 1, T, 2048, 128, 1, None)
     assert r == L.NVM_ERR_UNSUPPORTED and "2 GiB" in _err(lib)
+    # the whole block refuses such a batch before its first launch (the
+    # routing would otherwise run and write the fp16 copy of x first)
+    assert _forward(lib, T=T) == L.NVM_ERR_UNSUPPORTED and "2 GiB" in _err(lib)
+    # h [T * k, I] beyond 2 GiB with x inside it
+    assert _forward(lib, T=200_000) == L.NVM_ERR_UNSUPPORTED and "2 GiB" in _err(lib)
 
 
 def test_quantized_matmul_validation():
@@ -283,3 +288,20 @@ def test_model_ops_validation(call, code, msg):
     _, lib = _lib()
     assert call(lib) == code
     assert msg in _err(lib)
+
+
+def test_forward_stage_validation():
+    """nvm_moe_forward_stage checks its stage index and then validates as
+    nvm_moe_forward does, before any device work."""
+    L, lib = _lib()
+    p = [1] * 12
+
+    def call(stage, T=4, bits=4):
+        return lib.nvm_moe_forward_stage(stage, 1, T, 2048, 768, 128, 8, 1, 64, bits, 1, *p, 1,
+                                         None, None, 0, 1, 1 << 40, None)
+
+    assert call(4) == L.NVM_ERR_INVALID and "stage" in _err(lib)
+    assert call(-1) == L.NVM_ERR_INVALID
+    assert call(1, bits=8) == L.NVM_ERR_UNSUPPORTED and "bits" in _err(lib)
+    assert call(0, T=0) == 0
+    assert call(2, T=600_000) == L.NVM_ERR_UNSUPPORTED and "2 GiB" in _err(lib)

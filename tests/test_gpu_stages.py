@@ -1,0 +1,74 @@
+"""nvm_moe_forward_stage: the block's launch sequence one stage at a time.
+
+Stages 0..3 run in order on one workspace must give exactly what
+nvm_moe_forward gives (the same kernels, the same workspace hand-offs), for
+each of the launch sequences the forward takes: decode batches (routing
+finalised in the gate/up prologue), prefill batches whose int8 router writes
+the fp16 copy of x, prefill batches converted by their own launch, and fp16
+activations.  Repeating a stage must not change what the next one reads.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+import torch
+
+from helpers import make_moe, to_act
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _call(lib, L, moe, x, ws, y, ids, sc, stage=None, regime=0):
+    T, H = x.shape
+    E, I = moe.check_operands(x.dtype, H)
+    ops = moe._operands()
+    flat = [t.data_ptr() for trio in ops for t in trio]
+    head = [x.data_ptr(), T, H, I, E, moe.num_experts_per_tok, int(moe.norm_topk_prob),
+            moe.w_gate.group_size, moe.w_gate.bits, L.dtype_code(x.dtype)]
+    tail = [y.data_ptr(), ids.data_ptr(), sc.data_ptr(), regime, ws.data_ptr(), ws.numel(),
+            L.stream_of(x.device)]
+    if stage is None:
+        L.check(lib.nvm_moe_forward(*head, *flat, *tail))
+    else:
+        L.check(lib.nvm_moe_forward_stage(stage, *head, *flat, *tail))
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("T,act,regime", [
+    (32, "bfloat16", 0),    # decode: partial logits, gate/up finalising the routing
+    (300, "bfloat16", 0),   # prefill: int8 router writes the fp16 copy of x
+    (100, "bfloat16", 2),   # prefill regime below the int8 router's batch: act_to_f16 launch
+    (200, "float16", 0),    # fp16 activations: the GEMMs stage x themselves
+])
+def test_stages_in_order_equal_the_forward(T, act, regime):
+    from nano_vllm_metal_amd import _lib as L
+
+    lib = L.load()
+    x, w = O.make_packed_inputs(7 + T, T, 2048, 128, 768, act, 64)
+    x = to_act(x, act, DEV)
+    moe = make_moe(w, act, 64, 8, True, DEV)
+    k = moe.num_experts_per_tok
+    size = ctypes.c_size_t()
+    L.check(lib.nvm_moe_workspace_size(T, 2048, 768, 128, k, ctypes.byref(size)))
+    outs = []
+    for staged in (False, True):
+        ws = torch.empty(size.value, dtype=torch.uint8, device=DEV)
+        y = torch.full_like(x, float("nan"))
+        ids = torch.full((T, k), -1, dtype=torch.int32, device=DEV)
+        sc = torch.full((T, k), float("nan"), dtype=x.dtype, device=DEV)
+        if staged:
+            for s in range(4):
+                # every stage twice: a repeat must leave the next stage's inputs as they were
+                for _ in range(2):
+                    _call(lib, L, moe, x, ws, y, ids, sc, stage=s, regime=regime)
+        else:
+            _call(lib, L, moe, x, ws, y, ids, sc, regime=regime)
+        outs.append((y, ids, sc))
+    print(f"stages T={T} {act} regime={regime}", flush=True)
+    for a, b, what in zip(outs[0], outs[1], ("y", "ids", "scores")):
+        assert torch.equal(a, b), f"{what} of the staged calls differs from nvm_moe_forward"

@@ -105,3 +105,39 @@ def test_noalloc_rejects_batches_beyond_the_array():
     assert rc == _lib.NVM_ERR_UNSUPPORTED
     assert b"static scratch" in lib.nvm_last_error()
     assert bool((y == 3.0).all())
+
+
+def test_noalloc_call_captured_in_a_graph():
+    """The entry point is for callers under HIP graph capture: one noalloc
+    call captured in a torch CUDA graph (after nvm_moe_scratch_bytes located
+    the array outside the capture), replayed three times with eager work and
+    synchronisations between the replays, equals nvm_moe_forward bitwise on
+    every replay."""
+    from nano_vllm_metal_amd import _lib
+
+    lib = _lib.load()
+    cap = ctypes.c_size_t()
+    _lib.check(lib.nvm_moe_scratch_bytes(ctypes.byref(cap)))
+    x, moe = _case(43, 32)
+    (y0, ids0, sc0), _, _ = _run_both(moe, x, 0)
+    head, flat, ops = _args(moe, x)
+    T, k = x.shape[0], moe.num_experts_per_tok
+    y = torch.empty_like(x)
+    ids = torch.empty((T, k), dtype=torch.int32, device=x.device)
+    sc = torch.empty((T, k), dtype=x.dtype, device=x.device)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = lib.nvm_moe_forward_noalloc(*head, *flat, y.data_ptr(), ids.data_ptr(),
+                                         sc.data_ptr(), 0, _lib.stream_of(x.device))
+    assert rc == 0, lib.nvm_last_error()
+    for rep in range(3):
+        y.fill_(float("nan"))
+        ids.fill_(-7)
+        sc.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        print(f"noalloc graph replay {rep}", flush=True)
+        for u, v, what in ((y0, y, "y"), (ids0, ids, "ids"), (sc0, sc, "scores")):
+            assert torch.equal(u, v), f"replay {rep}: {what} differs from nvm_moe_forward"
+    del ops
