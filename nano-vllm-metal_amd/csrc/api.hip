@@ -120,6 +120,7 @@ struct MoeWs {
   int32_t *offsets, *sorted, *counts;
   unsigned *done;
   uint16_t *h, *down;
+  uint8_t *xsh, *hsh;  // group shifts of the prefill GEMMs' fp16 copies of x and h
   size_t bytes;
 };
 
@@ -138,6 +139,8 @@ MoeWs carve_moe(void *base, int64_t T, int64_t H, int64_t I, int64_t E, int k) {
   w.done = c.take<unsigned>(1);
   w.h = c.take<uint16_t>((size_t)N * I);
   w.down = c.take<uint16_t>((size_t)N * H);
+  w.xsh = c.take<uint8_t>((size_t)T * (H / 64));
+  w.hsh = c.take<uint8_t>((size_t)N * (I / 64));
   w.bytes = c.bytes();
   return w;
 }
@@ -146,13 +149,13 @@ MoeWs carve_moe(void *base, int64_t T, int64_t H, int64_t I, int64_t E, int k) {
 // batches; batches the int8 router takes are routed whole in one launch and
 // sorted in another (without probabilities, E <= 128); other batches
 // finalise per token and sort over blocks.  xh (bf16 x; may be NULL): where
-// the whole-routing launch may also store the fp16 copy of x that
-// launch_act_to_f16 makes; *xh_done says whether it did.
+// the whole-routing launch may also store the fp16 copy of x (with its group
+// shifts in xsh) that launch_act_to_f16 makes; *xh_done says whether it did.
 int run_route_dispatch(int dtype, const void *x, int64_t T, int64_t H, const uint32_t *wr,
                        const void *sr, const void *br, int64_t E, int gs, int k, int norm,
                        void *probs, int32_t *ids, void *scores, int32_t *offsets, int32_t *sorted,
                        double *partial, int32_t *counts, unsigned *done, hipStream_t st,
-                       void *xh = nullptr, bool *xh_done = nullptr) {
+                       void *xh = nullptr, uint8_t *xsh = nullptr, bool *xh_done = nullptr) {
   if (xh_done) *xh_done = false;
   if (!probs && !nvm::route_fused_dispatch(T, k) && nvm::route_i8_fin_supports(T, H, E, gs, k)) {
     // the histograms [T/16][E] live in the partial-logit workspace, which
@@ -160,7 +163,7 @@ int run_route_dispatch(int dtype, const void *x, int64_t T, int64_t H, const uin
     int32_t *hist = (int32_t *)partial;
     void *xo = dtype == NVM_DTYPE_BF16 ? xh : nullptr;
     NVM_TRY_HIP(nvm::launch_route_i8_fin(dtype, x, T, H, wr, sr, br, E, gs, k, norm, ids, scores,
-                                         hist, xo, st));
+                                         hist, xo, xo ? xsh : nullptr, st));
     NVM_TRY_HIP(nvm::launch_dispatch_hist(ids, T * k, E, hist, (T + 15) / 16, 16 * k, offsets,
                                           sorted, st));
     if (xh_done) *xh_done = xo != nullptr;
@@ -754,9 +757,10 @@ int moe_stages(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int to
       if (int r = run_route_dispatch(dtype, x, T, H, wr, sr, br, E, group_size, top_k,
                                      norm_topk_prob, nullptr, ids, scores, ws.offsets, ws.sorted,
                                      ws.partial, ws.counts, ws.done, st,
-                                     gemm_both ? ws.down : nullptr, &xh_done))
+                                     gemm_both ? ws.down : nullptr, ws.xsh, &xh_done))
         return r;
-      if (gemm_both && !xh_done) NVM_TRY_HIP(nvm::launch_act_to_f16(x, T * H, ws.down, st));
+      if (gemm_both && !xh_done)
+        NVM_TRY_HIP(nvm::launch_act_to_f16(x, T * H, ws.down, ws.xsh, st));
     }
     if (gemm_both) {
       if (runs(1)) {
@@ -764,12 +768,15 @@ int moe_stages(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int to
                                          su, bu, ws.offsets, ws.sorted, ws.h);
         g.act_h = 1;
         g.out_h = 1;
+        g.act_sh = ws.xsh;
+        g.out_sh = ws.hsh;
         if (int r = run_products(dtype, false, true, g, N, st)) return r;
       }
       if (runs(2)) {
         nvm::GroupedArgs d = down_args(ws.h, N, H, I, E, group_size, wd, sd, bd, ws.offsets,
                                        ws.sorted, ws.down);
         d.act_h = 1;
+        d.act_sh = ws.hsh;
         if (int r = run_products(dtype, false, false, d, N, st)) return r;
       }
       return NVM_OK;

@@ -257,6 +257,45 @@ __device__ __forceinline__ uint32_t bload2(rsrc_t r, int voff, int soff) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
 }
 
+// fp16 copies of bf16 activations (the prefill GEMMs' operands) keep bf16's
+// range through a power-of-two shift per row and 64-value group: a group
+// whose largest |x| is 2^15 or more is stored as x * 2^-s, s = e - 14 for
+// that largest value's exponent e (so every stored value is below 2^15 and
+// exact: bf16 has fewer significand bits than fp16), every other group as it
+// is (s = 0).  The GEMMs undo the shift on their float32 sums.
+//
+// Largest |x| of eight bf16 values (four dwords), as a bf16 bit pattern.
+__device__ __forceinline__ uint32_t bf16_absmax_bits(u32x4 v) {
+  typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+  auto a = [](uint32_t d) { return __builtin_bit_cast(u16x2, d & 0x7FFF7FFFu); };
+  const u16x2 m = __builtin_elementwise_max(__builtin_elementwise_max(a(v.x), a(v.y)),
+                                            __builtin_elementwise_max(a(v.z), a(v.w)));
+  return max((uint32_t)m.x, (uint32_t)m.y);
+}
+// The shift of a group from its largest |x| (bf16 bits): exponent field - 141.
+__device__ __forceinline__ int f16_shift_of(uint32_t absmax_bits) {
+  return max(0, (int)(absmax_bits >> 7) - 141);
+}
+// 2^d as a float32, for |d| <= 126.
+__device__ __forceinline__ float pow2f(int d) { return __uint_as_float((uint32_t)(127 + d) << 23); }
+// Eight bf16 values -> fp16 of x * 2^-sh (exact for the group's values within
+// 2^-29 of its largest; smaller ones round toward zero), in the pair order
+// (x0,x4)(x1,x5)(x2,x6)(x3,x7).  v_cvt_pkrtz_f16_f32 rounds toward zero.
+__device__ __forceinline__ u32x4 bf16_to_f16_pairs(u32x4 v, int sh) {
+  const float f = pow2f(-sh);
+  auto el = [&](int i) {
+    return __uint_as_float((i & 1) ? (v[i >> 1] & 0xFFFF0000u) : (v[i >> 1] << 16)) * f;
+  };
+  u32x4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    o[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(el(j), el(j + 4)));
+  return o;
+}
+// Maximum over each aligned group of 8 lanes (quad swaps, then the half-row
+// mirror), every lane of the group active.
+__device__ __forceinline__ uint32_t max8_lanes(uint32_t v);
+
 // Wavefront reductions: DPP butterflies inside each 16-lane row (quad_perm
 // [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror), then the four
 // row results combined from scalar readlanes.  The combination order is fixed,
@@ -276,6 +315,12 @@ __device__ __forceinline__ double readlane_f64(double v, int lane) {
   const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
   const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
   return __builtin_bit_cast(double, lo | (hi << 32));
+}
+
+__device__ __forceinline__ uint32_t max8_lanes(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));
+  v = max(v, dpp_u32<0x4E>(v));
+  return max(v, dpp_u32<0x141>(v));
 }
 
 template <class Op>

@@ -201,6 +201,28 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
     s_orow[i] = i < mcnt ? (a.o_map ? a.o_map[slot] : slot) : -1;
   }
   __syncthreads();
+  // fp16 activations stored with group shifts (bf16_to_f16_pairs): does any
+  // group of this tile's rows carry one?  (Then the k-loop rescales the sums.)
+  const int KSG = a.K >> 6;  // k-steps (groups of 64) per row
+  bool shifted = false;
+  if constexpr (AH && DT == DT_BF16) {
+    uint32_t any = 0;
+    if (a.act_sh) {
+      if ((KSG & 3) == 0) {
+        const int W = KSG >> 2;
+        for (int j = tid; j < BM * W; j += 256) {
+          const int r = s_arow[j / W];
+          if (r >= 0) any |= *(const uint32_t *)(a.act_sh + (int64_t)r * KSG + 4 * (j % W));
+        }
+      } else {
+        for (int j = tid; j < BM * KSG; j += 256) {
+          const int r = s_arow[j / KSG];
+          if (r >= 0) any |= a.act_sh[(int64_t)r * KSG + j % KSG];
+        }
+      }
+    }
+    shifted = __syncthreads_or(any != 0);
+  }
 
   // ---- descriptors and per-thread offsets of the staging loads
   const rsrc_t ra = make_rsrc(a.act, (uint32_t)(a.act_rows * a.act_ld * 2));
@@ -407,7 +429,45 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
   // then ks + 1 (issued a k-step earlier) is stored into the other stage,
   // and at the end of an odd k-step the next pair's weights.  Two k-steps per
   // loop trip keep the register sets static.
-  auto k_loop = [&](auto NA) {
+  // SH (tiles with shifted groups): before k-step ks, lane row block i's sums
+  // are brought from the units of the previous group's shift to those of
+  // ks's (2^(old - new), exact), and after the last k-step back to units of
+  // one (2^shift); the shifts are read here, one byte per row and k-step.
+  // (the current shift of each lane's row block i: s_cur[wave][i][lane], in
+  // LDS so that no register is held across the k-loop for it)
+  __shared__ uint8_t s_cur[4][4][64];
+  auto k_loop = [&](auto NA, auto SH) {
+    constexpr bool kSh = decltype(SH)::value;
+    if constexpr (kSh) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_cur[wv][i][lane] = 0;
+    }
+    auto rescale = [&](int ks) {
+      if constexpr (kSh) {
+        for (int i = 0; i < 4; ++i) {
+          const int r = s_arow[32 * i + l32];
+          const int cs = s_cur[wv][i][lane];
+          const int nsh = r >= 0 ? (int)a.act_sh[(int64_t)r * KSG + ks] : cs;
+          if (nsh != cs) {
+            const float f = pow2f(cs - nsh);
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+              for (int q = 0; q < 16; ++q) acc[s][i][q] *= f;
+            s_cur[wv][i][lane] = (uint8_t)nsh;
+          }
+        }
+      }
+    };
+    auto step = [&](int ks) {
+      if constexpr (kSh) {
+        rescale(ks);
+        // (the rescale stays apart from the k-step's operand reads, which
+        // would otherwise be scheduled into it and raise register pressure)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      compute(ks, NA);
+    };
     Stage g0, g1;
     PairB gb;
     issue(g0, 0);
@@ -422,13 +482,13 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
       // even k-step
       issue(g0, ks + 2);
       issue_b(gb, ks + 2);
-      compute(ks, NA);
+      step(ks);
       store(g1, 1);
       take_sb(ks + 1);
       __syncthreads();
       // odd k-step
       issue(g1, ks + 3);
-      compute(ks + 1, NA);
+      step(ks + 1);
       if (ks + 2 < nk) {
         store(g0, 0);
         store_b(gb, ((ks + 2) >> 1) & 1);
@@ -436,16 +496,29 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
       }
       __syncthreads();
     }
-    if (ks < nk) compute(ks, NA);  // an odd count: the last k-step, already staged
+    if (ks < nk) step(ks);  // an odd count: the last k-step, already staged
+    if constexpr (kSh) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float f = pow2f(s_cur[wv][i][lane]);
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int q = 0; q < 16; ++q) acc[s][i][q] *= f;
+      }
+    }
   };
   // A tile of at most 64 routed rows (an expert's last, short tile) runs the
   // k-steps with a half or a quarter of the MFMAs.
-  if (mcnt > 64)
-    k_loop(std::integral_constant<int, 4>{});
+  using NoSh = std::false_type;
+  if (shifted)
+    k_loop(std::integral_constant<int, 4>{}, std::true_type{});
+  else if (mcnt > 64)
+    k_loop(std::integral_constant<int, 4>{}, NoSh{});
   else if (mcnt > 32)
-    k_loop(std::integral_constant<int, 2>{});
+    k_loop(std::integral_constant<int, 2>{}, NoSh{});
   else
-    k_loop(std::integral_constant<int, 1>{});
+    k_loop(std::integral_constant<int, 1>{}, NoSh{});
 
   // Epilogue through LDS.  The MFMAs take the weights as A and the routed
   // rows as B, so lane l holds routed row 32 i + l % 32 of every accumulator
@@ -474,13 +547,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
           float u0 = acc[1][i][4 * q + j], u1 = acc[1][i][4 * q + j + 1];
           round_act2<DT>(g0, g1);
           round_act2<DT>(u0, u1);
-          const uint32_t v = swiglu_act2<DT>(g0, g1, u0, u1);
-          // (out_h: the act values in the fp16 form of the down product's
-          // staging, rounded toward zero as act_to_h rounds them)
-          o[j >> 1] = DT == DT_BF16 && a.out_h
-                          ? __builtin_bit_cast(uint32_t,
-                                               __builtin_amdgcn_cvt_pkrtz(A::lo(v), A::hi(v)))
-                          : v;
+          o[j >> 1] = swiglu_act2<DT>(g0, g1, u0, u1);
         }
         *(u32x2 *)(orow + 2 * (32 * wv + 8 * q + 4 * h)) = u32x2{o[0], o[1]};
       } else {
@@ -501,8 +568,17 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
   const bool vec = (a.out_ld & 7) == 0 && ((uintptr_t)a.out & 15) == 0 && col + 8 <= R;
   for (int r = tid / CPR; r < mcnt; r += 256 / CPR) {
     u32x4 v = *(const u32x4 *)(Os + r * O_PITCH + 16 * c);
-    // (out_h: each 16-byte chunk in the pair order the down product stages)
-    if (DUAL && DT == DT_BF16 && a.out_h) v = pair_order(v);
+    if constexpr (DUAL && DT == DT_BF16) {
+      if (a.out_h) {
+        // out_h: the fp16 copy of h for the down product, each 64-column
+        // group (eight consecutive lanes: CPR is a multiple of 8) shifted,
+        // each 16-byte chunk in the pair order the down product stages
+        const int sh = f16_shift_of(max8_lanes(bf16_absmax_bits(v)));
+        v = bf16_to_f16_pairs(v, sh);
+        if ((c & 7) == 0 && a.out_sh && col < R)
+          a.out_sh[(int64_t)s_orow[r] * (R >> 6) + (col >> 6)] = (uint8_t)sh;
+      }
+    }
     uint16_t *op = a.out + (int64_t)s_orow[r] * a.out_ld + col;
     if (vec) {
       *(u32x4 *)op = v;
@@ -546,30 +622,32 @@ hipError_t launch_t(bool dual, const GroupedArgs &a, int64_t max_m_tiles, hipStr
   return hipGetLastError();
 }
 
-// bf16 -> fp16 as act_to_h converts, eight values a thread, stored in the
-// pair order (x0,x4)(x1,x5)(x2,x6)(x3,x7).  ALIGNED: x is 16-byte aligned
-// (one 16-byte load a thread, else eight 2-byte loads).
+// bf16 -> its fp16 copy for the prefill GEMMs, eight values a thread, stored
+// in the pair order (x0,x4)(x1,x5)(x2,x6)(x3,x7): each group of 64 values
+// (eight threads) shifted by bf16_to_f16_pairs, its shift in sh.  ALIGNED: x
+// is 16-byte aligned (one 16-byte load a thread, else eight 2-byte loads).
 template <bool ALIGNED>
 __global__ __launch_bounds__(256) void act_to_f16_kernel(const uint16_t *__restrict__ x,
-                                                        int64_t n8, uint16_t *__restrict__ out) {
+                                                        int64_t n8, uint16_t *__restrict__ out,
+                                                        uint8_t *__restrict__ sh) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n8) return;
-  u32x4 v;
-  if constexpr (ALIGNED) {
-    v = ldg16(x + 8 * i);
-  } else {
+  // (n8 is a multiple of 8: a group's eight threads are all in range or all
+  // out of it)
+  const bool ok = i < n8;
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (ok) {
+    if constexpr (ALIGNED) {
+      v = ldg16(x + 8 * i);
+    } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      v[j] = (uint32_t)x[8 * i + 2 * j] | ((uint32_t)x[8 * i + 2 * j + 1] << 16);
+      for (int j = 0; j < 4; ++j)
+        v[j] = (uint32_t)x[8 * i + 2 * j] | ((uint32_t)x[8 * i + 2 * j + 1] << 16);
+    }
   }
-  u32x4 o;
-  auto el = [&](int i) {
-    return __uint_as_float((i & 1) ? (v[i >> 1] & 0xFFFF0000u) : (v[i >> 1] << 16));
-  };
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    o[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(el(j), el(j + 4)));
-  *(u32x4 *)(out + 8 * i) = o;
+  const int s = f16_shift_of(max8_lanes(bf16_absmax_bits(v)));
+  if (!ok) return;
+  *(u32x4 *)(out + 8 * i) = bf16_to_f16_pairs(v, s);
+  if ((i & 7) == 0) sh[i >> 3] = (uint8_t)s;
 }
 
 }  // namespace
@@ -581,17 +659,17 @@ hipError_t launch_gemm(int dtype, bool dual, const GroupedArgs &a, int64_t max_m
                  : launch_t<DT_BF16, false>(dual, a, max_m_tiles, st);
 }
 
-hipError_t launch_act_to_f16(const void *x, int64_t n, void *out, hipStream_t st) {
-  if (n % 8 || (uintptr_t)out % 16 || (uintptr_t)x % 2) return hipErrorInvalidValue;
+hipError_t launch_act_to_f16(const void *x, int64_t n, void *out, uint8_t *sh, hipStream_t st) {
+  if (n % 64 || (uintptr_t)out % 16 || (uintptr_t)x % 2 || !sh) return hipErrorInvalidValue;
   const int64_t n8 = n / 8;
   if (n8 == 0) return hipSuccess;
   const dim3 grid((unsigned)((n8 + 255) / 256));
   if ((uintptr_t)x % 16 == 0)
     hipLaunchKernelGGL(act_to_f16_kernel<true>, grid, dim3(256), 0, st, (const uint16_t *)x, n8,
-                       (uint16_t *)out);
+                       (uint16_t *)out, sh);
   else
     hipLaunchKernelGGL(act_to_f16_kernel<false>, grid, dim3(256), 0, st, (const uint16_t *)x, n8,
-                       (uint16_t *)out);
+                       (uint16_t *)out, sh);
   return hipGetLastError();
 }
 

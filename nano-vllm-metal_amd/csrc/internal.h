@@ -51,6 +51,12 @@ struct GroupedArgs {
   // of a down product with act_h set; R a multiple of 8).  The decode
   // products ignore both.
   int act_h, out_h;
+  // With act_h and bf16 activations: the shift of each fp16 row group
+  // (bf16_to_f16_pairs), act_sh[row * K / 64 + k-step] for activation row
+  // `row` (NULL: no group shifted).  The gate/up epilogue with out_h writes
+  // the shifts of the h it stores into out_sh [rows, R / 64] (may be NULL).
+  const uint8_t *act_sh;
+  uint8_t *out_sh;
 };
 
 // Decode batches whose routing the gate/up product can finalise: at most
@@ -78,11 +84,12 @@ hipError_t launch_route_i8(int dtype, const void *x, int64_t T, int64_t H, const
 // ids/scores [T][k], its expert histogram counts[T/16][E] (for
 // launch_dispatch_hist) and, with xh (bf16 x only), the fp16 copy of x that
 // launch_act_to_f16 makes.
+// (xsh [T][H / 64]: the shifts of the fp16 copy's groups, written with xh)
 bool route_i8_fin_supports(int64_t T, int64_t H, int64_t E, int gs, int k);
 hipError_t launch_route_i8_fin(int dtype, const void *x, int64_t T, int64_t H, const uint32_t *wr,
                                const void *sr, const void *br, int64_t E, int gs, int k, int norm,
                                int32_t *ids, void *scores, int32_t *counts, void *xh,
-                               hipStream_t st);
+                               uint8_t *xsh, hipStream_t st);
 // `done` (may be NULL) is a counter the partial launch zeroes for the fused
 // finalise-and-dispatch launch that follows it.
 hipError_t launch_route_partial(int dtype, const void *x, int64_t T, int64_t H, const uint32_t *wr,
@@ -139,11 +146,11 @@ constexpr int kGemmBM = 128;   // prefill tile rows (routed pairs)
 constexpr int kGemmBN = 128;   // prefill tile columns per weight matrix
 hipError_t launch_gemm(int dtype, bool dual, const GroupedArgs &a, int64_t max_m_tiles,
                        hipStream_t st);
-// bf16 x [n] -> the fp16 values the prefill GEMM's staging makes of them
-// (round toward zero below fp16's normal range, saturating above it), each
-// 16-byte chunk in the pair order of GroupedArgs::act_h; n a multiple of 8,
-// 16-byte aligned buffers.
-hipError_t launch_act_to_f16(const void *x, int64_t n, void *out, hipStream_t st);
+// bf16 x [n] -> its fp16 copy for the prefill GEMMs: each 64-value group
+// shifted (bf16_to_f16_pairs) with its shift in sh [n / 64], each 16-byte
+// chunk in the pair order of GroupedArgs::act_h; n a multiple of 64, `out`
+// 16-byte aligned.
+hipError_t launch_act_to_f16(const void *x, int64_t n, void *out, uint8_t *sh, hipStream_t st);
 
 // Combine fused with the residual add and RMSNorm that follow the MoE block
 // in the model (rows of H <= 8192, a multiple of 8).

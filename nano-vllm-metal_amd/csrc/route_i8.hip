@@ -93,12 +93,14 @@ __device__ __forceinline__ void i8_stage_sb(rsrc_t srr, rsrc_t brr, int e0, int 
 // activations at byte offset xo (kMaskedOffset past T) of x, hidden columns
 // 16G..16G+15 of each k-step.  s_sb: the staged scales and biases from group
 // g0.  With xh (bf16 activations), the lane also stores its activations
-// converted to fp16 as act_to_f16 does, at xh + xo / 2 (xh_ok: a real token).
+// converted to fp16 as act_to_f16 does, at xh + xo / 2 (xh_ok: a real token),
+// and the k-step's group shift at xsh_row[ks] (xsh_row: the token's row of
+// shifts).
 template <int DT>
 __device__ __forceinline__ void i8_wave_sums(rsrc_t xr, rsrc_t wrr, int xo, int e0, int HW, int gs,
                                              int GPR, int g0, int k0, int k1,
                                              const uint8_t *s_sb, double (&acc)[kI8Tiles][4],
-                                             uint16_t *xh, bool xh_ok) {
+                                             uint16_t *xh, bool xh_ok, uint8_t *xsh_row) {
   using A = Act<DT>;
   constexpr bool BF = DT == DT_BF16;
   constexpr int MB = BF ? 7 : 10;  // stored significand bits
@@ -144,23 +146,23 @@ __device__ __forceinline__ void i8_wave_sums(rsrc_t xr, rsrc_t wrr, int xo, int 
     load(nx, ks + 1 < k1 ? ks + 1 : ks);
     const u32x4 (&xv)[2] = cu.xv;
     const u32x2 (&wq)[kI8Tiles] = cu.wq;
-    if (xh && xh_ok) {
-      // the fp16 copy of this lane's 16 activations, each 16-byte chunk of
-      // x0..x7 stored in the pair order (x0,x4)(x1,x5)(x2,x6)(x3,x7) the
-      // prefill GEMM's MFMA operands use
-      u32x4 o[2];
-      auto el = [&](const u32x4 &v, int i) {
-        return __uint_as_float((i & 1) ? (v[i >> 1] & 0xFFFF0000u) : (v[i >> 1] << 16));
-      };
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          o[h][j] = __builtin_bit_cast(uint32_t,
-                                       __builtin_amdgcn_cvt_pkrtz(el(xv[h], j), el(xv[h], j + 4)));
-      u32x4 *dst = (u32x4 *)((uint8_t *)xh + (int64_t)xo + 128 * ks);
-      dst[0] = o[0];
-      dst[1] = o[1];
+    if constexpr (BF) {
+      if (xh) {
+        // the fp16 copy of this lane's 16 activations, each 16-byte chunk of
+        // x0..x7 stored in the pair order (x0,x4)(x1,x5)(x2,x6)(x3,x7) the
+        // prefill GEMM's MFMA operands use; the k-step's 64 values of token
+        // row c (lanes c, c + 16, c + 32, c + 48) share one shift
+        uint32_t m = max(bf16_absmax_bits(xv[0]), bf16_absmax_bits(xv[1]));
+        m = max(m, (uint32_t)__shfl_xor((int)m, 16));
+        m = max(m, (uint32_t)__shfl_xor((int)m, 32));
+        const int sh = f16_shift_of(m);
+        if (xh_ok) {
+          u32x4 *dst = (u32x4 *)((uint8_t *)xh + (int64_t)xo + 128 * ks);
+          dst[0] = bf16_to_f16_pairs(xv[0], sh);
+          dst[1] = bf16_to_f16_pairs(xv[1], sh);
+          if (G == 0) xsh_row[ks] = (uint8_t)sh;
+        }
+      }
     }
     const int g = (ks * 64) / gs;
     uint32_t sv[kI8Tiles], bv[kI8Tiles];
@@ -308,7 +310,8 @@ __global__ __launch_bounds__(64 * kI8Waves, 2) void route_i8_kernel(
   i8_stage_sb(srr, brr, e0, GPR, g0, g1, s_sb, threadIdx.x, 64 * kI8Waves);
   __syncthreads();
   double acc[kI8Tiles][4];
-  i8_wave_sums<DT>(xr, wrr, xo, e0, HW, gs, GPR, g0, k0, k1, s_sb, acc, nullptr, false);
+  i8_wave_sums<DT>(xr, wrr, xo, e0, HW, gs, GPR, g0, k0, k1, s_sb, acc, nullptr, false,
+                   nullptr);
 
   // the wavefronts' partials meet in LDS, added in wavefront order
   // (a lane's slots are 512 bytes apart: compile-time offsets from one base)
@@ -347,8 +350,8 @@ __global__ __launch_bounds__(64 * kFinMaxWaves) void route_i8_fin_kernel(
     const uint16_t *__restrict__ x, int T, int H, const uint32_t *__restrict__ wr,
     const uint16_t *__restrict__ sr, const uint16_t *__restrict__ br, int E, int gs, int k,
     int norm, int32_t *__restrict__ ids, uint16_t *__restrict__ scores,
-    int32_t *__restrict__ counts, uint16_t *__restrict__ xh) {
-  hoist_args(x, T, H, wr, sr, br, E, gs, k, norm, ids, scores, counts, xh);
+    int32_t *__restrict__ counts, uint16_t *__restrict__ xh, uint8_t *__restrict__ xsh) {
+  hoist_args(x, T, H, wr, sr, br, E, gs, k, norm, ids, scores, counts, xh, xsh);
   extern __shared__ double s_lds[];
   // [ec][quarter - 1][tile][row][lane] partials, then the logits [16][128],
   // then the staged s/b of each expert range
@@ -383,7 +386,8 @@ __global__ __launch_bounds__(64 * kFinMaxWaves) void route_i8_fin_kernel(
   double acc[kI8Tiles][4];
   // (the first expert range's wavefronts write the fp16 copy)
   i8_wave_sums<DT>(xr, wrr, xo, e0, HW, gs, GPR, 0, k0, k1, s_sb0 + ec * 2 * kSbArr, acc,
-                   ec == 0 ? xh : nullptr, ta < T);
+                   ec == 0 ? xh : nullptr, ta < T,
+                   xsh ? xsh + (int64_t)ta * KS : nullptr);
 
   // quarters 1-3 publish their sums; quarter 0 adds them in order and writes
   // the logit sums [token][expert]
@@ -465,8 +469,9 @@ bool route_i8_fin_supports(int64_t T, int64_t H, int64_t E, int gs, int k) {
 hipError_t launch_route_i8_fin(int dtype, const void *x, int64_t T, int64_t H, const uint32_t *wr,
                                const void *sr, const void *br, int64_t E, int gs, int k, int norm,
                                int32_t *ids, void *scores, int32_t *counts, void *xh,
-                               hipStream_t st) {
+                               uint8_t *xsh, hipStream_t st) {
   if (!route_i8_fin_supports(T, H, E, gs, k) || T <= 0) return hipErrorInvalidValue;
+  if (xh && (dtype != DT_BF16 || !xsh)) return hipErrorInvalidValue;
   // more than 64 KB of dynamic LDS (once per device and dtype; a failure here
   // shows up as a failed launch below)
   static bool attr_set[2][64] = {};
@@ -484,11 +489,11 @@ hipError_t launch_route_i8_fin(int dtype, const void *x, int64_t T, int64_t H, c
   if (di)
     hipLaunchKernelGGL(route_i8_fin_kernel<DT_BF16>, grid, block, kFinLds, st, (const uint16_t *)x,
                        (int)T, (int)H, wr, (const uint16_t *)sr, (const uint16_t *)br, (int)E, gs,
-                       k, norm, ids, (uint16_t *)scores, counts, (uint16_t *)xh);
+                       k, norm, ids, (uint16_t *)scores, counts, (uint16_t *)xh, xsh);
   else
     hipLaunchKernelGGL(route_i8_fin_kernel<DT_F16>, grid, block, kFinLds, st, (const uint16_t *)x,
                        (int)T, (int)H, wr, (const uint16_t *)sr, (const uint16_t *)br, (int)E, gs,
-                       k, norm, ids, (uint16_t *)scores, counts, nullptr);
+                       k, norm, ids, (uint16_t *)scores, counts, nullptr, nullptr);
   return hipGetLastError();
 }
 
