@@ -619,6 +619,25 @@ def attention_bench(dev):
     out[f"prefill_causal_B{B}_L{L}"] = {"us": us, "tflops": flops / us / 1e6,
                                         "frac_mfma": flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS}
     del q, k, v
+    # chunked prefill / prefill after a prefix on the paged cache: 4 requests
+    # of 256 new rows over 1024 cached positions (causal; the matrix-core
+    # multi-query kernel); flops of the visible scores and values
+    B, L, ctx = 4, 256, 1280
+    g = torch.Generator(device=dev).manual_seed(13)
+    mp = (ctx + ps - 1) // ps
+    P = B * mp
+    q = torch.randn(B, Hq, L, D, device=dev, generator=g)
+    kp = torch.randn(P, Hkv, ps, D, device=dev, generator=g).to(torch.bfloat16)
+    vp = torch.randn(P, Hkv, ps, D, device=dev, generator=g).to(torch.bfloat16)
+    bt = torch.randperm(P, device=dev, generator=g).to(torch.int32).reshape(B, mp)
+    lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    us = _graph_us(lambda: paged_attention(q, kp, vp, bt, lens, ps, mask="causal"))
+    vis = sum(ctx - L + i + 1 for i in range(L))  # visible positions per (request, head)
+    flops = 2.0 * 2 * B * Hq * vis * D
+    out[f"prefill_chunk_B{B}_L{L}_ctx{ctx}"] = {
+        "us": us, "tflops": flops / us / 1e6, "frac_mfma": flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS,
+        "note": "query scores on three act-dtype parts of the float32 query (3 MFMAs a product)"}
+    del q, kp, vp, bt
     return out
 
 
@@ -653,7 +672,34 @@ def e2e_bench(dev, n_seqs=32, prompt_len=1024, gen=256, layers=48):
            "decode_step_ms": st.decode_s / st.decode_steps * 1e3,
            "prefill_tokens_per_s": st.prefill_tokens / st.prefill_s,
            "wall_s": wall, "generated_tokens_per_s": n_seqs * gen / wall}
-    del llm, model
+    # the run checked at its own size (as tests/test_gpu_e2e_config5.py does):
+    # every page free afterwards, and requests re-run alone reproducing the
+    # batch's greedy tokens up to a near-tie (recomputed logits, bf16 ulps of
+    # the row's largest logit)
+    pages_free = llm.cache.free_pages == llm.cache.num_pages
+    del llm
+    solo = LLM(model, max_num_seqs=1, max_model_len=prompt_len + gen + 16, page_size=16,
+               prefill_step=8 * prompt_len)
+    checks = []
+    for i in (0, n_seqs - 1):
+        alone = solo.generate([prompts[i]], SamplingParams(max_tokens=gen, ignore_eos=True))
+        alone = alone[0].token_ids
+        batch = outs[i].token_ids
+        d = next((j for j in range(gen) if batch[j] != alone[j]), gen)
+        j = min(d, gen - 1)
+        cache = model.create_kv_cache(-(-(prompt_len + gen) // 16), page_size=16)
+        cache.add(0)
+        lg = model.forward(torch.tensor([prompts[i] + alone[:j]], device=dev), cache, [0])[0]
+        lg = lg.float()
+        ulp = 2.0 ** (np.floor(np.log2(float(lg.abs().max().clamp_min(2.0 ** -100)))) - 7)
+        checks.append({"request": i, "same_tokens": d,
+                       "batch_token_gap_ulps": float(lg.max() - lg[batch[j]]) / ulp,
+                       "logits_finite": bool(torch.isfinite(lg).all())})
+        del cache
+    res["check"] = {"all_pages_free": pages_free, "requests_rerun_alone": checks,
+                    "bar": "tokens equal, or the batch's token within 4 ulps of the lone "
+                           "run's maximum logit where they part"}
+    del solo, model
     torch.cuda.empty_cache()
     return res
 

@@ -620,6 +620,14 @@ int nvm_paged_attention(const float *q, int64_t N, int64_t L, int64_t D, const v
     return NVM_OK;
   }
 
+  if (paged_prefill_supports(L, D, kv_dtype, num_kv_heads, num_heads)) {
+    const hipError_t e = launch_paged_prefill(q, B, L, D, key_pages, value_pages, P, page_size,
+                                              kv_dtype, block_table, max_pages, context_lens,
+                                              scale, is_causal, num_kv_heads, num_heads,
+                                              out_dtype, out, st);
+    if (e != hipSuccess) return set_error(NVM_ERR_HIP, "paged_attention: %s", hipGetErrorString(e));
+    return NVM_OK;
+  }
   const int64_t rows = N * L;
   const unsigned grid = (unsigned)((rows + 3) / 4);
   switch (kv_dtype) {

@@ -39,6 +39,8 @@
 // weight row (one 16-byte LDS read serves all four chunks) and its A operand
 // is the 16 bytes at offset 16*(4h + c) of the activation row, which staging
 // stores in that slot order.
+#include <stdlib.h>
+
 #include "common.h"
 #include "internal.h"
 
@@ -590,6 +592,429 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
   }
 }
 
+// ---------------------------------------------------------------------------
+// The forward's GEMM (bf16 activations given as their fp16 copy, act_h): the
+// tile, MFMA layout, arithmetic, scale/bias windows and epilogue are those of
+// gemm_kernel, but nothing is staged through registers.
+//  * The activation rows go from memory straight into LDS
+//    (buffer_load_dwordx4 ... lds), four stages deep: k-step ks + 3 is
+//    requested while ks is computed.  A stage holds 128 rows of 128 bytes;
+//    the 16-byte chunk k of row r lies at slot k ^ (r & 7), so eight rows'
+//    chunk k fall in distinct bank groups (the lane-to-chunk assignment of
+//    each load instruction makes the swizzle: LDS is written in lane order).
+//  * A wavefront's packed weights are its own (no other wavefront reads its
+//    rows), so they go from memory into a ring of registers a k-step pair at
+//    a time (two 16-byte loads per row half and k-step pair: the pair's 64
+//    bytes of a row in back-to-back requests), one pair ahead.
+// The register staging of gemm_kernel held two k-steps of activations and a
+// k-step pair of weights per thread; with the registers full, the compiler
+// placed the next loads after the k-step's MFMAs, so they had a k-step to
+// arrive.  Here nothing but the weight ring competes for registers.
+//
+// LDS waits: the compiler does not track the LDS written by these loads, so
+// each k-step waits for its own stage by count before the block barrier:
+// the loads of the two later stages (eight instructions a wavefront) may
+// still be in flight, everything before them has landed.
+constexpr int kDmaStages = 4;
+constexpr int D_STAGE = BM * 128;                          // 16 KB
+constexpr int kGemmDmaLds = kDmaStages * D_STAGE + 4 * W_WAVE;  // 73 KB
+
+__device__ __forceinline__ void dma16(rsrc_t r, void *lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16,
+                                           voff, soff, 0, 0);
+}
+template <bool DUAL>
+__global__ __launch_bounds__(256, 2) void gemm_dma_kernel(const GroupedArgs a, int n_tiles) {
+  constexpr int DT = DT_BF16;
+  using A = Act<DT>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ int s_arow[BM];
+  __shared__ int s_orow[BM];
+  int *const s_tiles = (int *)smem;
+  static_assert((kMaxExperts + 1) * 4 <= D_STAGE, "m-tile list exceeds an activation stage");
+
+  hoist_args(a.act, a.act_ld, a.act_rows, a.a_map, a.a_div, a.offsets, a.w0, a.s0, a.b0, a.w1,
+             a.s1, a.b1, a.R, a.K, a.gs, a.E, a.out, a.o_map, a.out_ld, n_tiles);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int l32 = lane & 31, h = lane >> 5;
+
+  // m-tile list (as gemm_kernel)
+  auto offs = [&](int i) { return a.offsets ? a.offsets[i] : (i == 0 ? 0 : (int)a.act_rows); };
+  if (wv == 0) {
+    int carry = 0;
+    for (int c0 = 0; c0 < a.E; c0 += 64) {
+      const int e = c0 + lane;
+      const int tv = e < a.E ? (offs(e + 1) - offs(e) + BM - 1) / BM : 0;
+      int inc = tv;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(inc, o);
+        if (lane >= o) inc += u;
+      }
+      if (e < a.E) s_tiles[e] = carry + inc - tv;
+      carry += __shfl(inc, 63);
+    }
+    if (lane == 0) s_tiles[a.E] = carry;
+  }
+  __syncthreads();
+  const int total = s_tiles[a.E] * n_tiles;
+  const int per_xcd = (total + 7) >> 3;
+  const int local = blockIdx.x >> 3;
+  if (local >= per_xcd) return;
+  const int t = (blockIdx.x & 7) * per_xcd + local;
+  if (t >= total) return;
+  const int mt = t / n_tiles, nt = t - mt * n_tiles;
+  int lo = 0, hi = a.E - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_tiles[mid] <= mt)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  const int e = lo;
+  const int m0 = offs(e) + (mt - s_tiles[e]) * BM;
+  const int mcnt = min(BM, offs(e + 1) - m0);
+  const int R = a.R, KW = a.K >> 3, GPR = a.K / a.gs;
+  const int n0 = nt * (DUAL ? WROWS / 2 : WROWS);
+
+  for (int i = tid; i < BM; i += 256) {
+    const int slot = m0 + i;
+    s_arow[i] = i < mcnt ? (a.a_map ? a.a_map[slot] / a.a_div : slot) : -1;
+    s_orow[i] = i < mcnt ? (a.o_map ? a.o_map[slot] : slot) : -1;
+  }
+  __syncthreads();
+  // fp16 copies stored with group shifts (as gemm_kernel)
+  const int KSG = a.K >> 6;
+  bool shifted = false;
+  {
+    uint32_t any = 0;
+    if (a.act_sh) {
+      if ((KSG & 3) == 0) {
+        const int W = KSG >> 2;
+        for (int j = tid; j < BM * W; j += 256) {
+          const int r = s_arow[j / W];
+          if (r >= 0) any |= *(const uint32_t *)(a.act_sh + (int64_t)r * KSG + 4 * (j % W));
+        }
+      } else {
+        for (int j = tid; j < BM * KSG; j += 256) {
+          const int r = s_arow[j / KSG];
+          if (r >= 0) any |= a.act_sh[(int64_t)r * KSG + j % KSG];
+        }
+      }
+    }
+    shifted = __syncthreads_or(any != 0);
+  }
+
+  const rsrc_t ra = make_rsrc(a.act, (uint32_t)(a.act_rows * a.act_ld * 2));
+  const int64_t eoff = (int64_t)e * R;
+  const rsrc_t rw0 = make_rsrc(a.w0 + eoff * KW, (uint32_t)R * KW * 4);
+  const rsrc_t rw1 = make_rsrc((DUAL ? a.w1 : a.w0) + eoff * KW, (uint32_t)R * KW * 4);
+  const rsrc_t rs0 = make_rsrc(a.s0 + eoff * GPR, (uint32_t)R * GPR * 2);
+  const rsrc_t rb0 = make_rsrc(a.b0 + eoff * GPR, (uint32_t)R * GPR * 2);
+  const rsrc_t rs1 = make_rsrc((DUAL ? a.s1 : a.s0) + eoff * GPR, (uint32_t)R * GPR * 2);
+  const rsrc_t rb1 = make_rsrc((DUAL ? a.b1 : a.b0) + eoff * GPR, (uint32_t)R * GPR * 2);
+
+  // Activation loads: instruction j of wavefront wv fills rows 32 wv + 8 j +
+  // (lane >> 3) of a stage; lane (lane & 7) of a row loads chunk
+  // (lane & 7) ^ (lane >> 3) (row & 7 = lane >> 3), which lands at slot
+  // lane & 7.
+  int a_voff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int ar = s_arow[32 * wv + 8 * j + (lane >> 3)];
+    a_voff[j] = ar >= 0 ? (int)(((int64_t)ar * a.act_ld) * 2) + 16 * ((lane & 7) ^ (lane >> 3))
+                        : kMaskedOffset;
+  }
+  const int nk = a.K / BK;
+  // k-step ks into stage ks % kDmaStages (k-steps past the end read zeros
+  // into a stage nothing reads: every k-step issues the same loads, so the
+  // wait counts below hold throughout)
+  auto dma_stage = [&](int ks) {
+    uint8_t *st = smem + (ks % kDmaStages) * D_STAGE + wv * 32 * 128;
+    const bool ok = ks < nk;
+    const int so = __builtin_amdgcn_readfirstlane(ok ? ks * BK * 2 : 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(ra, st + j * 1024, ok ? a_voff[j] : kMaskedOffset, so);
+  };
+  // the lane's two weight rows (sub 0/1), for the weight ring and the
+  // scale/bias windows
+  int srow[2], b_voff[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int grow = DUAL ? n0 + 32 * wv + l32 : n0 + 64 * wv + 32 * s + l32;
+    srow[s] = grow < R ? grow * GPR * 2 : kMaskedOffset;
+    b_voff[s] = grow < R ? grow * KW * 4 + 16 * h : kMaskedOffset;
+  }
+  // weight ring: slot p & 1 holds k-step pair p, [sub][k-step of the pair]
+  // (pairs past the end read zeros)
+  u32x4 bq[2][2][2];
+  const int np = (nk + 1) >> 1;
+  auto issue_b = [&](u32x4 (&q)[2][2], int p) {
+    const bool ok = p < np;
+    const int sb = __builtin_amdgcn_readfirstlane(ok ? p * BK : 0);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        q[s][kk] = bload16(s ? rw1 : rw0, ok ? b_voff[s] : kMaskedOffset, sb + kk * (BK / 2));
+  };
+  // scale/bias windows of eight 64-wide groups, one a trip of eight k-steps
+  // (group size 64; as gemm_kernel, one 8-byte load per row, matrix and half)
+  u32x2 wcur[4];
+  auto issue_w = [&](u32x2 (&w)[4], int wi) {
+    const int gh = 8 * wi + 4 * h;
+    const int so = __builtin_amdgcn_readfirstlane(16 * wi);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        const rsrc_t r = t2 ? (s ? rb1 : rb0) : (s ? rs1 : rs0);
+        w[2 * s + t2] = bload8(r, gh < GPR ? srow[s] + 8 * h : kMaskedOffset, so);
+      }
+  };
+
+  f32x16 acc[2][4];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[s][i][r] = 0.f;
+
+  uint8_t *const w_lds = smem + kDmaStages * D_STAGE + wv * W_WAVE + l32 * W_PITCH;
+  uint32_t sc[2], bi[2];
+  // at a trip's first k-step: the arrived window to LDS, the next requested
+  auto new_window = [&](int wi) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      auto val = [&](const u32x2 &w) {
+        const uint32_t d = (i & 2) ? w.y : w.x;
+        return sb_h<DT>((i & 1) ? d >> 16 : d & 0xFFFFu);
+      };
+      *(u32x2 *)(w_lds + 8 * (4 * h + i)) =
+          u32x2{val(wcur[0]) | (val(wcur[1]) << 16), val(wcur[2]) | (val(wcur[3]) << 16)};
+    }
+    issue_w(wcur, wi + 1);
+  };
+  auto take_sb = [&](int j) {  // group j of the window
+    const u32x2 v = *(const u32x2 *)(w_lds + 8 * j);
+    sc[0] = perm_b32(v.x, v.x, 0x01000100u);
+    bi[0] = perm_b32(v.x, v.x, 0x03020302u);
+    sc[1] = perm_b32(v.y, v.y, 0x01000100u);
+    bi[1] = perm_b32(v.y, v.y, 0x03020302u);
+  };
+  const uint32_t nib_mask = sgpr_const(0x000F000Fu);
+  const uint32_t magic = vgpr_const(0x64006400u);
+  // this lane's A read offsets within a stage: row l32 (+ 32 i), chunk
+  // 4 h + c at slot (4 h + c) ^ (l32 & 7)
+  int a_rd[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) a_rd[c] = l32 * 128 + 16 * ((4 * h + c) ^ (l32 & 7));
+  // k-step ks from stage ks % kDmaStages and the weights bw (as gemm_kernel)
+  auto compute = [&](int ks, const u32x4 (&bw)[2], auto NA) {
+    constexpr int na = decltype(NA)::value;
+    const uint8_t *As = smem + (ks % kDmaStages) * D_STAGE;
+    auto load_a = [&](int c, u32x4 (&af)[4]) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (i < na) af[i] = *(const u32x4 *)(As + a_rd[c] + 32 * 128 * i);
+    };
+    auto deq = [&](int c, u32x4 (&bf)[2]) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) bf[s] = dequant8_h(bw[s][c], sc[s], bi[s], nib_mask, magic);
+    };
+    u32x4 af[4], bf[2];
+    load_a(0, af);
+    deq(0, bf);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      u32x4 afn[4], bfn[2];
+      if (c < 3) {
+        load_a(c + 1, afn);
+        deq(c + 1, bfn);
+      }
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (i < na) acc[s][i] = mfma32_h(bf[s], af[i], acc[s][i]);
+      if (c < 3) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) af[i] = afn[i];
+        bf[0] = bfn[0];
+        bf[1] = bfn[1];
+      }
+    }
+  };
+
+  __shared__ uint8_t s_cur[4][4][64];
+  auto k_loop = [&](auto NA, auto SH) {
+    constexpr bool kSh = decltype(SH)::value;
+    if constexpr (kSh) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_cur[wv][i][lane] = 0;
+    }
+    auto rescale = [&](int ks) {
+      if constexpr (kSh) {
+        for (int i = 0; i < 4; ++i) {
+          const int r = s_arow[32 * i + l32];
+          const int cs = s_cur[wv][i][lane];
+          const int nsh = r >= 0 ? (int)a.act_sh[(int64_t)r * KSG + ks] : cs;
+          if (nsh != cs) {
+            const float f = pow2f(cs - nsh);
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+              for (int q = 0; q < 16; ++q) acc[s][i][q] *= f;
+            s_cur[wv][i][lane] = (uint8_t)nsh;
+          }
+        }
+      }
+    };
+    // prologue: the first window, weight pairs 0 and 1, stages 0..2 (the
+    // window first: its wait at the first trip then counts as many later
+    // loads as on every other trip)
+    issue_w(wcur, 0);
+    issue_b(bq[0], 0);
+    issue_b(bq[1], 1);
+#pragma unroll
+    for (int ks = 0; ks < kDmaStages - 1; ++ks) dma_stage(ks);
+    // Trips of eight k-steps (one window).  k-step ks waits for this
+    // wavefront's loads of stage ks (the two later stages' eight loads may
+    // be in flight; whatever else was issued after them only makes the wait
+    // longer), then meets the block: every wavefront's loads of ks have
+    // landed, and every wavefront is done with ks - 1, whose stage the loads
+    // of ks + 3 refill.  After an odd k-step its pair's slot takes the pair
+    // two ahead.  Only the products are skipped past the end; the loads are
+    // the same on every trip.
+    for (int ks0 = 0; ks0 < nk; ks0 += 8) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int ks = ks0 + j;
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        asm volatile("s_barrier" ::: "memory");
+        dma_stage(ks + kDmaStages - 1);
+        if (j == 0) new_window(ks0 >> 3);
+        take_sb(j);
+        if (ks < nk) {
+          if constexpr (kSh) {
+            rescale(ks);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          const u32x4 bw[2] = {bq[(j >> 1) & 1][0][j & 1], bq[(j >> 1) & 1][1][j & 1]};
+          compute(ks, bw, NA);
+        }
+        if (j & 1) issue_b(bq[(j >> 1) & 1], (ks >> 1) + 2);
+      }
+    }
+    if constexpr (kSh) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float f = pow2f(s_cur[wv][i][lane]);
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int q = 0; q < 16; ++q) acc[s][i][q] *= f;
+      }
+    }
+    // the zero-filling loads past the end land before LDS is reused
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  };
+  using NoSh = std::false_type;
+  if (shifted)
+    k_loop(std::integral_constant<int, 4>{}, std::true_type{});
+  else if (mcnt > 64)
+    k_loop(std::integral_constant<int, 4>{}, NoSh{});
+  else if (mcnt > 32)
+    k_loop(std::integral_constant<int, 2>{}, NoSh{});
+  else
+    k_loop(std::integral_constant<int, 1>{}, NoSh{});
+
+  // Epilogue through LDS (as gemm_kernel), over the stages and windows
+  constexpr int OCOLS = DUAL ? WROWS / 2 : WROWS;
+  constexpr int O_PITCH = 2 * OCOLS + 16;
+  static_assert(BM * O_PITCH <= kGemmDmaLds, "output tile exceeds the staging LDS");
+  __syncthreads();
+  uint8_t *Os = smem;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint8_t *orow = Os + (32 * i + l32) * O_PITCH;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (DUAL) {
+        uint32_t o[2];
+#pragma unroll
+        for (int j = 0; j < 4; j += 2) {
+          float g0 = acc[0][i][4 * q + j], g1 = acc[0][i][4 * q + j + 1];
+          float u0 = acc[1][i][4 * q + j], u1 = acc[1][i][4 * q + j + 1];
+          round_act2<DT>(g0, g1);
+          round_act2<DT>(u0, u1);
+          o[j >> 1] = swiglu_act2<DT>(g0, g1, u0, u1);
+        }
+        *(u32x2 *)(orow + 2 * (32 * wv + 8 * q + 4 * h)) = u32x2{o[0], o[1]};
+      } else {
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+          *(u32x2 *)(orow + 2 * (64 * wv + 32 * s + 8 * q + 4 * h)) =
+              u32x2{A::pack2(acc[s][i][4 * q], acc[s][i][4 * q + 1]),
+                    A::pack2(acc[s][i][4 * q + 2], acc[s][i][4 * q + 3])};
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int CPR = OCOLS / 8;
+  const int c = tid % CPR, col = n0 + 8 * c;
+  const bool vec = (a.out_ld & 7) == 0 && ((uintptr_t)a.out & 15) == 0 && col + 8 <= R;
+  for (int r = tid / CPR; r < mcnt; r += 256 / CPR) {
+    u32x4 v = *(const u32x4 *)(Os + r * O_PITCH + 16 * c);
+    if constexpr (DUAL) {
+      if (a.out_h) {
+        const int sh = f16_shift_of(max8_lanes(bf16_absmax_bits(v)));
+        v = bf16_to_f16_pairs(v, sh);
+        if ((c & 7) == 0 && a.out_sh && col < R)
+          a.out_sh[(int64_t)s_orow[r] * (R >> 6) + (col >> 6)] = (uint8_t)sh;
+      }
+    }
+    uint16_t *op = a.out + (int64_t)s_orow[r] * a.out_ld + col;
+    if (vec) {
+      *(u32x4 *)op = v;
+    } else {
+#pragma unroll
+      for (int e2 = 0; e2 < 8; ++e2)
+        if (col + e2 < R) op[e2] = (uint16_t)(v[e2 >> 1] >> (16 * (e2 & 1)));
+    }
+  }
+}
+
+template <bool DUAL>
+void allow_gemm_dma_lds() {
+  static bool done[64] = {false};
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !done[dev]) {
+    (void)hipFuncSetAttribute((const void *)&gemm_dma_kernel<DUAL>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kGemmDmaLds);
+    done[dev] = true;
+  }
+}
+
+hipError_t launch_dma(bool dual, const GroupedArgs &a, int64_t max_m_tiles, hipStream_t st) {
+  const int cols = dual ? WROWS / 2 : WROWS;
+  const int n_tiles = (a.R + cols - 1) / cols;
+  const int64_t total = max_m_tiles * n_tiles;
+  const unsigned grid = (unsigned)(8 * ((total + 7) / 8));
+  if (dual) {
+    allow_gemm_dma_lds<true>();
+    hipLaunchKernelGGL(gemm_dma_kernel<true>, dim3(grid), dim3(256), kGemmDmaLds, st, a, n_tiles);
+  } else {
+    allow_gemm_dma_lds<false>();
+    hipLaunchKernelGGL(gemm_dma_kernel<false>, dim3(grid), dim3(256), kGemmDmaLds, st, a,
+                       n_tiles);
+  }
+  return hipGetLastError();
+}
+
+
 // more than 64 KB of dynamic LDS: allowed once per device and instance (a
 // failure shows up as a failed launch)
 template <int DT, bool DUAL, bool AH>
@@ -655,6 +1080,11 @@ __global__ __launch_bounds__(256) void act_to_f16_kernel(const uint16_t *__restr
 hipError_t launch_gemm(int dtype, bool dual, const GroupedArgs &a, int64_t max_m_tiles,
                        hipStream_t st) {
   if (dtype != DT_BF16) return launch_t<DT_F16, false>(dual, a, max_m_tiles, st);
+  // (NVM_GEMM_NODMA=1, read at each launch, takes the register-staged
+  // kernel of the same arithmetic: the tests compare the two bit for bit)
+  const char *nodma = getenv("NVM_GEMM_NODMA");
+  if (a.act_h && a.gs == 64 && a.K % 256 == 0 && !(nodma && nodma[0] == '1'))
+    return launch_dma(dual, a, max_m_tiles, st);
   return a.act_h ? launch_t<DT_BF16, true>(dual, a, max_m_tiles, st)
                  : launch_t<DT_BF16, false>(dual, a, max_m_tiles, st);
 }

@@ -160,6 +160,16 @@ hipError_t launch_combine_residual_norm(int dtype, const void *down, const void 
                                         hipStream_t st);
 bool combine_residual_norm_supports(int64_t H);
 
+// Multi-query paged attention on the matrix cores (paged_prefill.hip): L > 1
+// query rows per request over f16/bf16 pages, head dims 64 and 128, 1, 2, 4,
+// 8 or 16 query heads per kv head; the arguments of nvm_paged_attention.
+bool paged_prefill_supports(int64_t L, int64_t D, int kv_dtype, int Hkv, int Hq);
+hipError_t launch_paged_prefill(const float *q, int64_t B, int64_t L, int64_t D, const void *kp,
+                                const void *vp, int64_t P, int64_t page_size, int kv_dtype,
+                                const int32_t *bt, int64_t max_pages, const int32_t *lens,
+                                float scale, int causal, int Hkv, int Hq, int out_dtype,
+                                void *out, hipStream_t st);
+
 // Combine: y[t] = rnd(sum_j rnd(down[t*k+j] * score[t,j])).
 hipError_t launch_combine(int dtype, const void *down, const void *scores, int64_t T, int k,
                           int64_t H, void *y, hipStream_t st);

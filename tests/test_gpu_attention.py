@@ -138,6 +138,37 @@ def test_multi_query_rows(L, causal):
     _run(107, 2, 8, 2, 128, 16, [40, 300], L=L, causal=causal)
 
 
+# ------------------------------------------------- multi-query matrix-core kernel
+
+
+def test_chunk_of_256_over_1024_cached_positions():
+    """Chunked prefill / prefill after a prefix at the 30B-A3B heads: four
+    requests add 256 query rows each over 1024 cached positions (1280 in the
+    context), causal (query row i sees j <= i + 1024), on the matrix-core
+    kernel (paged_prefill.hip)."""
+    _run(120, 4, 32, 4, 128, 16, [1280, 1280, 1100, 1280], L=256, causal=True, dtype="bfloat16")
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("Hq,Hkv,D,ps,L,causal", [
+    (8, 8, 64, 4, 17, True),     # one query head per kv head, small pages
+    (16, 8, 128, 24, 33, False),  # two per kv head, pages of 24 slots, not causal
+    (16, 4, 64, 128, 70, True),  # four per kv head, pages of 128 slots
+    (16, 1, 128, 16, 9, True),   # sixteen per kv head
+])
+def test_multi_query_matrix_core_shapes(dtype, Hq, Hkv, D, ps, L, causal):
+    """Head groupings, page sizes and ragged contexts (one shorter than the
+    chunk: its first rows see nothing), with missing pages and page ids past
+    the pool, which the reference skips."""
+    _run(121 + L, 3, Hq, Hkv, D, ps, [L + 150, L - 3, 2 * L], L=L, causal=causal, dtype=dtype,
+         holes=2, past_pool=1)
+
+
+def test_multi_query_query_magnitudes():
+    """float32 queries far from act-representable values (three-part split)."""
+    _run(130, 2, 8, 2, 128, 16, [200, 90], L=40, causal=True, dtype="bfloat16", q_scale=37.0)
+
+
 def test_int8_decode():
     """paged_attention_int8_decode: codes times per-slot scales."""
     _run(108, 4, 32, 4, 128, 16, [1, 90, 600, 0], int8=True, holes=1)

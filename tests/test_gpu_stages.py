@@ -72,3 +72,29 @@ def test_stages_in_order_equal_the_forward(T, act, regime):
     print(f"stages T={T} {act} regime={regime}", flush=True)
     for a, b, what in zip(outs[0], outs[1], ("y", "ids", "scores")):
         assert torch.equal(a, b), f"{what} of the staged calls differs from nvm_moe_forward"
+
+
+@pytest.mark.parametrize("T", [4096, 300, 129])
+def test_prefill_gemm_with_direct_to_lds_staging_is_bit_identical(T, monkeypatch):
+    """The forward's GEMMs on their fp16 copies stage activations straight
+    into LDS (gemm_dma_kernel); NVM_GEMM_NODMA=1 takes the register-staged
+    kernel of the same arithmetic.  Both must give the same bits: 4096
+    tokens (the headline prefill), 300 (ragged m-tiles) and 129 (one more
+    than the int8 router's threshold, many short tiles); the down product's
+    12 k-steps end in a partial trip of the k-loop."""
+    from nano_vllm_metal_amd import _lib as L
+
+    lib = L.load()
+    x, w = O.make_packed_inputs(800 + T, T, 2048, 128, 768, "bfloat16", 64)
+    x = to_act(x, "bfloat16", DEV)
+    moe = make_moe(w, "bfloat16", 64, 8, True, DEV)
+    moe.regime = "prefill"
+    outs = []
+    for nodma in ("1", "0"):
+        monkeypatch.setenv("NVM_GEMM_NODMA", nodma)
+        y, ids, sc = moe.forward(x, return_routing=True)
+        torch.cuda.synchronize()
+        outs.append((y.clone(), ids.clone(), sc.clone()))
+    print(f"dma vs register staging T={T}", flush=True)
+    for a, b, what in zip(outs[0], outs[1], ("y", "ids", "scores")):
+        assert torch.equal(a, b), f"{what}: direct-to-LDS GEMM differs from register staging"
