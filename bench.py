@@ -819,8 +819,8 @@ KERNEL_KEYS = (
     ("decode_down", r"gemv3_kernel<1, false|gemv_kernel<1, false"),
     # prefill GEMMs of the forward (activations converted to fp16 once, by
     # act_to_f16) and of the stage entry points (converting their own rows)
-    ("prefill_gateup", r"gemm_kernel<1, true, true>"),
-    ("prefill_down", r"gemm_kernel<1, false, true>"),
+    ("prefill_gateup", r"gemm_dma_kernel<true>|gemm_kernel<1, true, true>"),
+    ("prefill_down", r"gemm_dma_kernel<false>|gemm_kernel<1, false, true>"),
     ("prefill_gateup_stage", r"gemm_kernel<1, true, false>"),
     ("prefill_down_stage", r"gemm_kernel<1, false, false>"),
     ("prefill_act_f16", r"act_to_f16_kernel"),
@@ -915,6 +915,22 @@ def rocprof_summary(root: Path, write_traffic: bool) -> str:
     for k, d in durs.items():
         stats[k] = {"calls": len(d), "avg_us": sum(d) / len(d), "med_us": statistics.median(d),
                     "min_us": min(d), "max_us": max(d)}
+    # kernel_stats.csv (--stats): the whole run's kernels by total time
+    for f in sorted(root.rglob("*kernel_stats.csv")):
+        with open(f) as fh:
+            rows = list(csv.DictReader(fh))
+        if not rows:
+            continue
+        tot = sum(float(r["TotalDurationNs"]) for r in rows)
+        calls = sum(int(r["Calls"]) for r in rows)
+        lines.append(f"kernel stats ({f.name}): total kernel time {tot / 1e6:.1f} ms over "
+                     f"{calls} launches")
+        lines.append(" total ms   calls    avg us  kernel")
+        for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:30]:
+            name = r["Name"].replace("nvm::(anonymous namespace)::", "")
+            name = re.sub(r"\((?!anonymous).*", "", name).replace("void ", "")
+            lines.append(f"{float(r['TotalDurationNs']) / 1e6:9.1f} {int(r['Calls']):7d} "
+                         f"{float(r['AverageNs']) / 1e3:9.2f}  {name[:90]}")
     if stats:
         lines.append("kernel trace (rocprofv3 --kernel-trace; per key: all calls):")
         for k, s in stats.items():
