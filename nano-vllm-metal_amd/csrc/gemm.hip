@@ -599,9 +599,12 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
 //  * The activation rows go from memory straight into LDS
 //    (buffer_load_dwordx4 ... lds), four stages deep: k-step ks + 3 is
 //    requested while ks is computed.  A stage holds 128 rows of 128 bytes;
-//    the 16-byte chunk k of row r lies at slot k ^ (r & 7), so eight rows'
-//    chunk k fall in distinct bank groups (the lane-to-chunk assignment of
-//    each load instruction makes the swizzle: LDS is written in lane order).
+//    the 16-byte chunk k of row r lies at slot k ^ (r & 7) ^ ((r >> 3) & 1),
+//    so the chunk k of sixteen consecutive rows falls in sixteen distinct
+//    16-byte bank groups of the 256-byte bank cycle (k ^ (r & 7) alone puts
+//    rows r and r + 8 in the same one: a two-way conflict on every A read).
+//    The lane-to-chunk assignment of each load instruction makes the
+//    swizzle: LDS is written in lane order.
 //  * A wavefront's packed weights are its own (no other wavefront reads its
 //    rows), so they go from memory into a ring of registers a k-step pair at
 //    a time (two 16-byte loads per row half and k-step pair: the pair's 64
@@ -612,10 +615,34 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
 // arrive.  Here nothing but the weight ring competes for registers.
 //
 // LDS waits: the compiler does not track the LDS written by these loads, so
-// each k-step waits for its own stage by count before the block barrier:
-// the loads of the two later stages (eight instructions a wavefront) may
-// still be in flight, everything before them has landed.
+// each k-step waits for its own stage by count before the block barrier.
+// The count is exact: the vector loads a wavefront issued after its four of
+// stage ks.  Step s issues stage s + 3 (4 loads), then at s % 8 == 0 the next
+// scale/bias window (4), at odd s the weight pair (s >> 1) + 2 (4); the loads
+// after stage ks are those of steps ks - 3 (after its stage), ks - 2 and
+// ks - 1, so the count depends on ks % 8 only.  The prologue issues stages
+// 0..2 and pairs 0, 1 in the order steps -3..-1 would, so the first trip
+// counts the same.  (A flat count of 8 would also wait for stage ks + 1 and
+// the weights issued with it: two k-steps of lead instead of three.)
 constexpr int kDmaStages = 4;
+constexpr int kStageWait[8] = {16, 16, 20, 16, 16, 12, 16, 12};
+// Keeps the loads on either side in program order (the counts above rely on
+// it; left free, the compiler groups the prologue's stage loads first, and
+// its own waits for the window registers then assume them only eight loads
+// old on every trip).
+__device__ __forceinline__ void issue_order() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+__device__ __forceinline__ void wait_stage(int j) {
+  const int n = kStageWait[j & 7];
+  if (n <= 12)
+    asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+  else if (n <= 16)
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
+}
 constexpr int D_STAGE = BM * 128;                          // 16 KB
 constexpr int kGemmDmaLds = kDmaStages * D_STAGE + 4 * W_WAVE;  // 73 KB
 
@@ -717,13 +744,14 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(const GroupedArgs a, i
 
   // Activation loads: instruction j of wavefront wv fills rows 32 wv + 8 j +
   // (lane >> 3) of a stage; lane (lane & 7) of a row loads chunk
-  // (lane & 7) ^ (lane >> 3) (row & 7 = lane >> 3), which lands at slot
-  // lane & 7.
+  // (lane & 7) ^ (lane >> 3) ^ (j & 1) (row & 7 = lane >> 3, (row >> 3) & 1
+  // = j & 1), which lands at slot lane & 7.
   int a_voff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int ar = s_arow[32 * wv + 8 * j + (lane >> 3)];
-    a_voff[j] = ar >= 0 ? (int)(((int64_t)ar * a.act_ld) * 2) + 16 * ((lane & 7) ^ (lane >> 3))
+    a_voff[j] = ar >= 0 ? (int)(((int64_t)ar * a.act_ld) * 2) +
+                              16 * ((lane & 7) ^ (lane >> 3) ^ (j & 1))
                         : kMaskedOffset;
   }
   const int nk = a.K / BK;
@@ -807,10 +835,11 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(const GroupedArgs a, i
   const uint32_t nib_mask = sgpr_const(0x000F000Fu);
   const uint32_t magic = vgpr_const(0x64006400u);
   // this lane's A read offsets within a stage: row l32 (+ 32 i), chunk
-  // 4 h + c at slot (4 h + c) ^ (l32 & 7)
+  // 4 h + c at slot (4 h + c) ^ (l32 & 7) ^ ((l32 >> 3) & 1)
   int a_rd[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) a_rd[c] = l32 * 128 + 16 * ((4 * h + c) ^ (l32 & 7));
+  for (int c = 0; c < 4; ++c)
+    a_rd[c] = l32 * 128 + 16 * ((4 * h + c) ^ (l32 & 7) ^ ((l32 >> 3) & 1));
   // k-step ks from stage ks % kDmaStages and the weights bw (as gemm_kernel)
   auto compute = [&](int ks, const u32x4 (&bw)[2], auto NA) {
     constexpr int na = decltype(NA)::value;
@@ -872,18 +901,24 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(const GroupedArgs a, i
         }
       }
     };
-    // prologue: the first window, weight pairs 0 and 1, stages 0..2 (the
-    // window first: its wait at the first trip then counts as many later
-    // loads as on every other trip)
+    // prologue: the first window, then stages 0..2 and weight pairs 0 and 1
+    // in the order of steps -3 (stage 0, pair 0), -2 (stage 1) and -1
+    // (stage 2, pair 1), so that the first trip's waits count as every
+    // other trip's
     issue_w(wcur, 0);
+    issue_order();
+    dma_stage(0);
+    issue_order();
     issue_b(bq[0], 0);
+    issue_order();
+    dma_stage(1);
+    dma_stage(2);
+    issue_order();
     issue_b(bq[1], 1);
-#pragma unroll
-    for (int ks = 0; ks < kDmaStages - 1; ++ks) dma_stage(ks);
+    issue_order();
     // Trips of eight k-steps (one window).  k-step ks waits for this
-    // wavefront's loads of stage ks (the two later stages' eight loads may
-    // be in flight; whatever else was issued after them only makes the wait
-    // longer), then meets the block: every wavefront's loads of ks have
+    // wavefront's loads of stage ks (everything issued after them may be in
+    // flight), then meets the block: every wavefront's loads of ks have
     // landed, and every wavefront is done with ks - 1, whose stage the loads
     // of ks + 3 refill.  After an odd k-step its pair's slot takes the pair
     // two ahead.  Only the products are skipped past the end; the loads are
@@ -892,9 +927,10 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(const GroupedArgs a, i
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int ks = ks0 + j;
-        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        wait_stage(j);
         asm volatile("s_barrier" ::: "memory");
         dma_stage(ks + kDmaStages - 1);
+        issue_order();
         if (j == 0) new_window(ks0 >> 3);
         take_sb(j);
         if (ks < nk) {
@@ -906,6 +942,7 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(const GroupedArgs a, i
           compute(ks, bw, NA);
         }
         if (j & 1) issue_b(bq[(j >> 1) & 1], (ks >> 1) + 2);
+        issue_order();
       }
     }
     if constexpr (kSh) {
