@@ -269,6 +269,49 @@ def forward_stage_us(layers, xs, stage, n=64):
     return e0.elapsed_time(e1) * 1e3 / n
 
 
+def in_layer_stage_us(layers, xs, stage, n=64):
+    """Duration (us) of one stage where the layer runs it, after its own
+    earlier stages (their outputs just written, as in the layer): a HIP graph
+    of `n` runs of stages 0..stage minus a graph of `n` runs of stages
+    0..stage-1, over the same weight sets, timed with HIP events on the
+    stream the graphs' kernels run on."""
+    import torch
+
+    T = xs[0].shape[0]
+    fs = [ForwardStages(m, T, layers[0].w_gate.weight.device) for m in layers]
+
+    def graph_us(upto):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for i, f in enumerate(fs):
+                f.run(xs[i % len(xs)], upto=upto)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fs[i % len(fs)].run(xs[i % len(fs) % len(xs)], upto=upto)
+        g.replay()
+        torch.cuda.synchronize()
+        best = None
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            t = e0.elapsed_time(e1) * 1e3
+            best = t if best is None else min(best, t)
+        del g
+        return best
+
+    with_stage = graph_us(stage + 1)
+    before = graph_us(stage)
+    del fs
+    return (with_stage - before) / n
+
+
 # route = routing and dispatch (nvm_moe_route_dispatch)
 STAGE_NAMES = ["route", "gateup", "down", "combine"]
 
@@ -425,6 +468,7 @@ def decode_bench(layers, T, steps, warmup, dev, use_graph=True, shape=None, n_me
     graph_kernel_us = {n: stage_kernel_us(stages, xs, n) for n in ("gateup", "down")}
     del stages
     fwd_kernel_us = {n: forward_stage_us(layers, xs, i) for i, n in enumerate(STAGE_NAMES)}
+    in_layer_us = {n: in_layer_stage_us(layers, xs, i) for i, n in ((1, "gateup"), (2, "down"))}
     gu_b, dn_b = bytes_per_expert(H, I, gs)
     avg_touched = sum(touched) / len(touched)
     layer_bytes = avg_touched * (gu_b + dn_b) + router_bytes(H, E, gs) + 2 * T * H * 2
@@ -448,12 +492,17 @@ def decode_bench(layers, T, steps, warmup, dev, use_graph=True, shape=None, n_me
                                   "(nvm_moe_forward_stage: route = partial logits, gateup = "
                                   "gate/up with the routing finalised in its prologue), each a "
                                   "HIP graph of 64 back-to-back launches timed with events",
+        "in_layer_kernel_us": in_layer_us,
+        "in_layer_kernel_us_note": "the stage where the layer runs it, after its own earlier "
+                                   "stages: a HIP graph of 64 runs of stages 0..s minus one of "
+                                   "stages 0..s-1 (nvm_moe_forward_stage), timed with events",
         "touched_experts_avg": avg_touched,
         "layer_algorithmic_bytes": layer_bytes,
         "hbm_gbs": layer_bytes / (layer_us * 1e-6) / 1e9,
         "gateup_algorithmic_bytes": gateup_bytes,
         "gateup_gbs": gateup_bytes / (graph_kernel_us["gateup"] * 1e-6) / 1e9,
         "forward_gateup_gbs": gateup_bytes / (fwd_kernel_us["gateup"] * 1e-6) / 1e9,
+        "in_layer_gateup_gbs": gateup_bytes / (in_layer_us["gateup"] * 1e-6) / 1e9,
         "down_gbs": avg_touched * dn_b / (graph_kernel_us["down"] * 1e-6) / 1e9,
     }
 
@@ -469,6 +518,7 @@ def prefill_bench(layers, T, steps, warmup, dev, zipf, shape=None):
     stage_us, stage_layer_us, touched, ids = eager_stage_pass(layers, xs, steps, warmup, dev)
     layer_us = eager_fused_pass(layers, xs, steps, warmup, dev)
     fwd_us = {n: forward_stage_us(layers, xs, i, n=16) for i, n in enumerate(STAGE_NAMES)}
+    in_layer_us = {n: in_layer_stage_us(layers, xs, i, n=16) for i, n in ((1, "gateup"), (2, "down"))}
     N = T * k
     gateup_flops = 2.0 * N * H * 2 * I
     down_flops = 2.0 * N * I * H
@@ -489,6 +539,12 @@ def prefill_bench(layers, T, steps, warmup, dev, zipf, shape=None):
                                   "(nvm_moe_forward_stage; the GEMMs on the fp16 copies of x "
                                   "and h), each a HIP graph of 16 back-to-back launches timed "
                                   "with events",
+        "in_layer_kernel_us": in_layer_us,
+        "in_layer_kernel_us_note": "the stage where the layer runs it, after its own earlier "
+                                   "stages: a HIP graph of 16 runs of stages 0..s minus one of "
+                                   "stages 0..s-1 (nvm_moe_forward_stage), timed with events",
+        "in_layer_gateup_tflops": gateup_flops / (in_layer_us["gateup"] * 1e-6) / 1e12,
+        "in_layer_down_tflops": down_flops / (in_layer_us["down"] * 1e-6) / 1e12,
         "forward_gateup_tflops": gateup_flops / (fwd_us["gateup"] * 1e-6) / 1e12,
         "forward_down_tflops": down_flops / (fwd_us["down"] * 1e-6) / 1e12,
         "layer_tflops": layer_flops / (layer_us * 1e-6) / 1e12,
@@ -856,21 +912,21 @@ def read_rocprof_us(key, path=PROFILE_DECODE):
     return None, None
 
 
-def rocprof_check(key, algorithmic_bytes, achieved_gbs):
+def rocprof_check(key, work, achieved, peak, path=PROFILE_DECODE):
     """The roofline recomputed from the committed rocprof figures of the same
-    kernel at the same workload, beside the live figure.  The median stands
-    for the launches the live figure times (the back-to-back graph launches
-    are most of the profiled calls; the eager stage pass adds a few slower
-    ones to the average)."""
-    avg, med = read_rocprof_us(key)
+    kernel at the same workload, beside the live figure: the average over the
+    profiled launches that directly follow the layer's previous stage (the
+    `key@layer` line), the launches the live in-layer figure times.  `work`
+    is bytes (achieved in GB/s) or flops (achieved in TFLOP/s)."""
+    avg, med = read_rocprof_us(key + "@layer", path)
     if avg is None:
         return {"rocprof_avg_us": None}
-    ref = med if med is not None else avg
-    gbs = algorithmic_bytes / (ref * 1e-6) / 1e9
+    rate = work / (avg * 1e-6) / (1e9 if peak == HBM_PEAK_GBS else 1e12)
     return {"rocprof_avg_us": avg, "rocprof_median_us": med,
-            "rocprof_profile": str(PROFILE_DECODE.relative_to(ROOT)),
-            "frac_from_rocprof": gbs / HBM_PEAK_GBS,
-            "live_vs_rocprof": achieved_gbs / gbs}
+            "rocprof_calls": f"{key}@layer",
+            "rocprof_profile": str(path.relative_to(ROOT)),
+            "frac_from_rocprof": rate / peak,
+            "live_vs_rocprof": achieved / rate}
 
 
 def read_traffic(name):
@@ -906,12 +962,24 @@ def rocprof_summary(root: Path, write_traffic: bool) -> str:
     lines = []
     stats = {}
     durs = defaultdict(list)
+    # the layer's own launch of a product: the dispatch that directly follows
+    # the layer's previous stage (gate/up after the routing, down after gate/up)
+    in_layer = {"decode_gateup_fused": ("route_partial",),
+                "prefill_gateup": ("dispatch_hist",),
+                "decode_down": ("decode_gateup_fused",),
+                "prefill_down": ("prefill_gateup",)}
     for f in sorted(root.rglob("*kernel_trace.csv")):
         with open(f) as fh:
-            for r in csv.DictReader(fh):
-                k = key_of(r["Kernel_Name"])
-                if k and k != "copy":
-                    durs[k].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+            rows = sorted(csv.DictReader(fh), key=lambda r: int(r["Start_Timestamp"]))
+        prev = None
+        for r in rows:
+            k = key_of(r["Kernel_Name"])
+            if k and k != "copy":
+                d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+                durs[k].append(d)
+                if prev in in_layer.get(k, ()):
+                    durs[k + "@layer"].append(d)
+            prev = k
     for k, d in durs.items():
         stats[k] = {"calls": len(d), "avg_us": sum(d) / len(d), "med_us": statistics.median(d),
                     "min_us": min(d), "max_us": max(d)}
@@ -932,7 +1000,8 @@ def rocprof_summary(root: Path, write_traffic: bool) -> str:
             lines.append(f"{float(r['TotalDurationNs']) / 1e6:9.1f} {int(r['Calls']):7d} "
                          f"{float(r['AverageNs']) / 1e3:9.2f}  {name[:90]}")
     if stats:
-        lines.append("kernel trace (rocprofv3 --kernel-trace; per key: all calls):")
+        lines.append("kernel trace (rocprofv3 --kernel-trace; per key: all calls; key@layer: "
+                     "the calls that directly follow the layer's previous stage)")
         for k, s in stats.items():
             lines.append(f"  {k:16s} calls={s['calls']:5d} avg={s['avg_us']:8.2f} us "
                          f"med={s['med_us']:8.2f} us min={s['min_us']:8.2f} max={s['max_us']:8.2f}")
@@ -986,15 +1055,19 @@ def rocprof_summary(root: Path, write_traffic: bool) -> str:
                          f"(GRBM_GUI_ACTIVE / {MI355X_XCDS} XCDs x {MI355X_SIMDS} SIMDs); "
                          f"{cycles:.0f} cycles per dispatch")
     for k, rec in traffic.items():
-        if "fetch_size_bytes" in rec and "write_size_bytes" in rec:
-            rec["hbm_bytes_per_launch"] = rec["fetch_size_bytes"] + rec["write_size_bytes"]
         if k in stats:
             rec["avg_us"] = stats[k]["avg_us"]
     text = "\n".join(lines)
     if write_traffic and traffic:
+        # merged per kernel and counter: the FETCH_SIZE and WRITE_SIZE runs
+        # each add their own figure to the kernel's record
         old = json.loads(TRAFFIC_JSON.read_text()) if TRAFFIC_JSON.exists() else {}
-        old.update(traffic)
-        old["_factors"] = factors
+        for k, rec in traffic.items():
+            old.setdefault(k, {}).update(rec)
+            cur = old[k]
+            if "fetch_size_bytes" in cur and "write_size_bytes" in cur:
+                cur["hbm_bytes_per_launch"] = cur["fetch_size_bytes"] + cur["write_size_bytes"]
+        old["_factors"] = {**old.get("_factors", {}), **factors}
         TRAFFIC_JSON.parent.mkdir(exist_ok=True)
         TRAFFIC_JSON.write_text(json.dumps(old, indent=1, sort_keys=True) + "\n")
     return text
@@ -1092,7 +1165,7 @@ def main():
         f"{head['hbm_gbs']:.0f} GB/s, kernels {head['kernel_us']}")
 
     gu_b, _ = bytes_per_expert(H, I, gs)
-    achieved = head["forward_gateup_gbs"]
+    achieved = head["in_layer_gateup_gbs"]
     out = {
         "metric": METRIC,
         "value": head["tokens_per_s"],
@@ -1130,10 +1203,17 @@ def main():
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": read_traffic("decode_gateup_fused"),
             "algorithmic_bytes_per_launch": head["gateup_algorithmic_bytes"],
-            "avg_launch_us": head["forward_kernel_us"]["gateup"],
-            "timing": "HIP events around a graph of 64 back-to-back launches of the layer's "
-                      "gate/up stage (8 weight sets cycled), mean per launch",
-            **rocprof_check("decode_gateup_fused", head["gateup_algorithmic_bytes"], achieved),
+            "avg_launch_us": head["in_layer_kernel_us"]["gateup"],
+            "timing": "HIP events: a graph of 64 runs of the layer's routing and gate/up stages "
+                      "minus a graph of 64 runs of its routing stage (8 weight sets cycled), "
+                      "per launch",
+            # the same launch 64 times back to back (its routing partials
+            # written long before, so read from HBM rather than L2)
+            "back_to_back": {"avg_launch_us": head["forward_kernel_us"]["gateup"],
+                             "achieved": head["forward_gateup_gbs"],
+                             "frac": head["forward_gateup_gbs"] / HBM_PEAK_GBS},
+            **rocprof_check("decode_gateup_fused", head["gateup_algorithmic_bytes"], achieved,
+                            HBM_PEAK_GBS),
             # the same product without the routing in its prologue (the stage
             # entry point nvm_moe_expert_gateup), beside it
             "stage_entry_point": {
@@ -1184,21 +1264,25 @@ def main():
                 f"prefill {out['e2e']['prefill_tokens_per_s']:.0f} tok/s")
         u = out["prefill"]["uniform"]
         out["prefill_roofline"] = {
-            "kernel": "gemm_kernel<bf16, gate/up+SwiGLU, fp16 copy of x> (the layer's gate/up "
-                      "launch at 4096 tokens, nvm_moe_forward_stage 1)",
-            "bound": "mfma", "achieved": u["forward_gateup_tflops"],
+            "kernel": "gemm_dma_kernel<gate/up+SwiGLU, fp16 copy of x staged by direct-to-LDS "
+                      "loads> (the layer's gate/up launch at 4096 tokens, "
+                      "nvm_moe_forward_stage 1)",
+            "bound": "mfma", "achieved": u["in_layer_gateup_tflops"],
             "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": u["forward_gateup_tflops"] / MFMA_BF16_PEAK_TFLOPS,
-            "avg_launch_us": u["forward_kernel_us"]["gateup"],
+            "frac": u["in_layer_gateup_tflops"] / MFMA_BF16_PEAK_TFLOPS,
+            "avg_launch_us": u["in_layer_kernel_us"]["gateup"],
+            "timing": "HIP events: a graph of 16 runs of the layer's routing and gate/up stages "
+                      "minus a graph of 16 runs of its routing stage, per launch",
+            "back_to_back": {"avg_launch_us": u["forward_kernel_us"]["gateup"],
+                             "achieved": u["forward_gateup_tflops"],
+                             "frac": u["forward_gateup_tflops"] / MFMA_BF16_PEAK_TFLOPS},
             "traffic": read_traffic("prefill_gateup"),
             "layer_frac": u["layer_mfma_frac"],
         }
-        avg, med = read_rocprof_us("prefill_gateup", PROFILE_PREFILL)
-        if avg is not None:
-            fl = 2.0 * 4096 * SHAPE["k"] * SHAPE["H"] * 2 * SHAPE["I"]
-            out["prefill_roofline"]["rocprof"] = {
-                "avg_us": avg, "median_us": med, "frac_from_avg": fl / (avg * 1e-6) / 1e12
-                / MFMA_BF16_PEAK_TFLOPS, "profile": str(PROFILE_PREFILL.relative_to(ROOT))}
+        fl = 2.0 * 4096 * SHAPE["k"] * SHAPE["H"] * 2 * SHAPE["I"]
+        out["prefill_roofline"].update(rocprof_check(
+            "prefill_gateup", fl, u["in_layer_gateup_tflops"], MFMA_BF16_PEAK_TFLOPS,
+            PROFILE_PREFILL))
     if not args.no_cpu:
         log(f"[bench] CPU baseline (~{args.cpu_seconds:.0f} s)")
         out["cpu_baseline"] = cpu_baseline(layers[0], args.batch, args.cpu_seconds, dev)
