@@ -28,9 +28,12 @@
 // to bf16 it would carry a 2^-9 relative error, which at the 235B-A22B shape
 // alone makes a mean output error above 1e-3 against the exact products;
 // rounded to fp16 (one v_pk_fma_f16, single rounding) the error is 2^-12 and
-// the outputs are those of exact weights.  bf16 activations convert to fp16
-// exactly in fp16's range (|x| <= 65504; post-norm activations are far
-// inside it), and the fp16 MFMA runs at the bf16 rate.
+// the outputs are those of exact weights.  The fp16 MFMA runs at the bf16
+// rate.  bf16 activations convert to fp16 exactly within fp16's range; the
+// fp16 copies of x and h that the forward hands these GEMMs (act_h) carry a
+// power-of-two shift per row and 64-value group (act_sh), which the k-loop
+// undoes on its float32 sums, so there bf16's whole range is kept.  Rows
+// converted here (the stage entry points) saturate beyond 65504.
 //
 // k-order inside a k-step: MFMA chunk c (16 wide) and lane half h cover
 // the eight k = 8*(4h + c) + i, i = 0..7, in both operands, in the slot
