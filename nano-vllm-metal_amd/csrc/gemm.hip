@@ -660,28 +660,38 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(const GroupedArgs a, i
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_arow[BM];
   __shared__ int s_orow[BM];
+  // the m-tile prefix and the expert offsets, in the first stage's LDS until
+  // the tile's rows are known (the first stage loads come after the barrier
+  // that follows)
   int *const s_tiles = (int *)smem;
-  static_assert((kMaxExperts + 1) * 4 <= D_STAGE, "m-tile list exceeds an activation stage");
+  int *const s_offs = s_tiles + kMaxExperts + 1;
+  static_assert(2 * (kMaxExperts + 1) * 4 <= D_STAGE, "m-tile list exceeds an activation stage");
 
   hoist_args(a.act, a.act_ld, a.act_rows, a.a_map, a.a_div, a.offsets, a.w0, a.s0, a.b0, a.w1,
              a.s1, a.b1, a.R, a.K, a.gs, a.E, a.out, a.o_map, a.out_ld, n_tiles);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int l32 = lane & 31, h = lane >> 5;
 
-  // m-tile list (as gemm_kernel)
+  // m-tile list (as gemm_kernel); the offsets stay in LDS, so the tile's
+  // rows need no second round trip to memory
   auto offs = [&](int i) { return a.offsets ? a.offsets[i] : (i == 0 ? 0 : (int)a.act_rows); };
   if (wv == 0) {
     int carry = 0;
     for (int c0 = 0; c0 < a.E; c0 += 64) {
       const int e = c0 + lane;
-      const int tv = e < a.E ? (offs(e + 1) - offs(e) + BM - 1) / BM : 0;
+      const int o0 = e < a.E ? offs(e) : 0, o1 = e < a.E ? offs(e + 1) : 0;
+      const int tv = e < a.E ? (o1 - o0 + BM - 1) / BM : 0;
       int inc = tv;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
         const int u = __shfl_up(inc, o);
         if (lane >= o) inc += u;
       }
-      if (e < a.E) s_tiles[e] = carry + inc - tv;
+      if (e < a.E) {
+        s_tiles[e] = carry + inc - tv;
+        s_offs[e + 1] = o1;
+        if (e == 0) s_offs[0] = o0;
+      }
       carry += __shfl(inc, 63);
     }
     if (lane == 0) s_tiles[a.E] = carry;
@@ -703,8 +713,8 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(const GroupedArgs a, i
       hi = mid - 1;
   }
   const int e = lo;
-  const int m0 = offs(e) + (mt - s_tiles[e]) * BM;
-  const int mcnt = min(BM, offs(e + 1) - m0);
+  const int m0 = s_offs[e] + (mt - s_tiles[e]) * BM;
+  const int mcnt = min(BM, s_offs[e + 1] - m0);
   const int R = a.R, KW = a.K >> 3, GPR = a.K / a.gs;
   const int n0 = nt * (DUAL ? WROWS / 2 : WROWS);
 
@@ -714,28 +724,8 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(const GroupedArgs a, i
     s_orow[i] = i < mcnt ? (a.o_map ? a.o_map[slot] : slot) : -1;
   }
   __syncthreads();
-  // fp16 copies stored with group shifts (as gemm_kernel)
-  const int KSG = a.K >> 6;
-  bool shifted = false;
-  {
-    uint32_t any = 0;
-    if (a.act_sh) {
-      if ((KSG & 3) == 0) {
-        const int W = KSG >> 2;
-        for (int j = tid; j < BM * W; j += 256) {
-          const int r = s_arow[j / W];
-          if (r >= 0) any |= *(const uint32_t *)(a.act_sh + (int64_t)r * KSG + 4 * (j % W));
-        }
-      } else {
-        for (int j = tid; j < BM * KSG; j += 256) {
-          const int r = s_arow[j / KSG];
-          if (r >= 0) any |= a.act_sh[(int64_t)r * KSG + j % KSG];
-        }
-      }
-    }
-    shifted = __syncthreads_or(any != 0);
-  }
 
+  const int KSG = a.K >> 6;
   const rsrc_t ra = make_rsrc(a.act, (uint32_t)(a.act_rows * a.act_ld * 2));
   const int64_t eoff = (int64_t)e * R;
   const rsrc_t rw0 = make_rsrc(a.w0 + eoff * KW, (uint32_t)R * KW * 4);
@@ -904,21 +894,6 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(const GroupedArgs a, i
         }
       }
     };
-    // prologue: the first window, then stages 0..2 and weight pairs 0 and 1
-    // in the order of steps -3 (stage 0, pair 0), -2 (stage 1) and -1
-    // (stage 2, pair 1), so that the first trip's waits count as every
-    // other trip's
-    issue_w(wcur, 0);
-    issue_order();
-    dma_stage(0);
-    issue_order();
-    issue_b(bq[0], 0);
-    issue_order();
-    dma_stage(1);
-    dma_stage(2);
-    issue_order();
-    issue_b(bq[1], 1);
-    issue_order();
     // Trips of eight k-steps (one window).  k-step ks waits for this
     // wavefront's loads of stage ks (everything issued after them may be in
     // flight), then meets the block: every wavefront's loads of ks have
@@ -961,6 +936,42 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(const GroupedArgs a, i
     // the zero-filling loads past the end land before LDS is reused
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   };
+  // prologue: the first window, then stages 0..2 and weight pairs 0 and 1
+  // in the order of steps -3 (stage 0, pair 0), -2 (stage 1) and -1
+  // (stage 2, pair 1), so that the first trip's waits count as every other
+  // trip's (the scan below waits for all of them, which only adds margin)
+  issue_w(wcur, 0);
+  issue_order();
+  dma_stage(0);
+  issue_order();
+  issue_b(bq[0], 0);
+  issue_order();
+  dma_stage(1);
+  dma_stage(2);
+  issue_order();
+  issue_b(bq[1], 1);
+  issue_order();
+  // fp16 copies stored with group shifts (as gemm_kernel); scanned after the
+  // first loads are out, so that its round trip overlaps theirs
+  bool shifted = false;
+  {
+    uint32_t any = 0;
+    if (a.act_sh) {
+      if ((KSG & 3) == 0) {
+        const int W = KSG >> 2;
+        for (int j = tid; j < BM * W; j += 256) {
+          const int r = s_arow[j / W];
+          if (r >= 0) any |= *(const uint32_t *)(a.act_sh + (int64_t)r * KSG + 4 * (j % W));
+        }
+      } else {
+        for (int j = tid; j < BM * KSG; j += 256) {
+          const int r = s_arow[j / KSG];
+          if (r >= 0) any |= a.act_sh[(int64_t)r * KSG + j % KSG];
+        }
+      }
+    }
+    shifted = __syncthreads_or(any != 0);
+  }
   using NoSh = std::false_type;
   if (shifted)
     k_loop(std::integral_constant<int, 4>{}, std::true_type{});
