@@ -618,33 +618,27 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const GroupedArgs a, int n
 // arrive.  Here nothing but the weight ring competes for registers.
 //
 // LDS waits: the compiler does not track the LDS written by these loads, so
-// each k-step waits for its own stage by count before the block barrier.
-// The count is exact: the vector loads a wavefront issued after its four of
-// stage ks.  Step s issues stage s + 3 (4 loads), then at s % 8 == 0 the next
-// scale/bias window (4), at odd s the weight pair (s >> 1) + 2 (4); the loads
-// after stage ks are those of steps ks - 3 (after its stage), ks - 2 and
-// ks - 1, so the count depends on ks % 8 only.  The prologue issues stages
-// 0..2 and pairs 0, 1 in the order steps -3..-1 would, so the first trip
-// counts the same.  (A flat count of 8 would also wait for stage ks + 1 and
-// the weights issued with it: two k-steps of lead instead of three.)
+// each k-step waits for its own stage by count before the block barrier:
+// s_waitcnt vmcnt(8), the eight loads of the two later stages.  The count
+// holds whatever order the register loads (weights, windows, shift scan)
+// complete in, as long as the direct-to-LDS loads complete in order among
+// themselves: while stage ks is in flight, so are stages ks + 1 and ks + 2,
+// nine or more loads outstanding.  (Counting the register loads issued after
+// stage ks as well, 12 to 20 by the step's position, would assume that every
+// vector memory operation completes in issue order.)  The wait thus also
+// drains the register loads issued before the later stages; exact counts
+// measured the same.
 constexpr int kDmaStages = 4;
-constexpr int kStageWait[8] = {16, 16, 20, 16, 16, 12, 16, 12};
-// Keeps the loads on either side in program order (the counts above rely on
-// it; left free, the compiler groups the prologue's stage loads first, and
-// its own waits for the window registers then assume them only eight loads
-// old on every trip).
+// Keeps the loads on either side in program order (left free, the compiler
+// groups the prologue's stage loads first, and its own waits for the window
+// registers then assume them only eight loads old on every trip).
 __device__ __forceinline__ void issue_order() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 }
-__device__ __forceinline__ void wait_stage(int j) {
-  const int n = kStageWait[j & 7];
-  if (n <= 12)
-    asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-  else if (n <= 16)
-    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
+__device__ __forceinline__ void wait_stage() {
+  static_assert(kDmaStages == 4, "two later stages of four loads each");
+  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
 }
 constexpr int D_STAGE = BM * 128;                          // 16 KB
 constexpr int kGemmDmaLds = kDmaStages * D_STAGE + 4 * W_WAVE;  // 73 KB
@@ -895,8 +889,8 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(const GroupedArgs a, i
       }
     };
     // Trips of eight k-steps (one window).  k-step ks waits for this
-    // wavefront's loads of stage ks (everything issued after them may be in
-    // flight), then meets the block: every wavefront's loads of ks have
+    // wavefront's loads of stage ks (those of stages ks + 1 and ks + 2 may be
+    // in flight), then meets the block: every wavefront's loads of ks have
     // landed, and every wavefront is done with ks - 1, whose stage the loads
     // of ks + 3 refill.  After an odd k-step its pair's slot takes the pair
     // two ahead.  Only the products are skipped past the end; the loads are
@@ -905,7 +899,7 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(const GroupedArgs a, i
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int ks = ks0 + j;
-        wait_stage(j);
+        wait_stage();
         asm volatile("s_barrier" ::: "memory");
         dma_stage(ks + kDmaStages - 1);
         issue_order();
@@ -938,8 +932,7 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(const GroupedArgs a, i
   };
   // prologue: the first window, then stages 0..2 and weight pairs 0 and 1
   // in the order of steps -3 (stage 0, pair 0), -2 (stage 1) and -1
-  // (stage 2, pair 1), so that the first trip's waits count as every other
-  // trip's (the scan below waits for all of them, which only adds margin)
+  // (stage 2, pair 1), as the trips issue them
   issue_w(wcur, 0);
   issue_order();
   dma_stage(0);
