@@ -15,8 +15,10 @@ permutation itself can be checked).
 
 Differences a caller can observe, all deliberate:
 
-* expert ids are ``int32`` (the reference's are ``uint32``; torch has no
-  general uint32 tensors);
+* ``route_topk`` returns ``uint32`` ids, as the reference's
+  ``argpartition`` does; this module's own additions (``route_and_dispatch``,
+  ``Moe.forward(..., return_routing=True)``) return ``int32`` ids, the same
+  bits, since torch indexes with signed integers;
 * top-k slots are in (probability desc, expert index asc) order; the
   reference's ``argpartition`` leaves slot order unspecified;
 * the block is one call into the library (route, dispatch, fused gate/up +
@@ -58,7 +60,11 @@ def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
 
 def route_topk(x: torch.Tensor, w_router: QuantizedWeights, top_k: int,
                norm_topk_prob: bool = False):
-    """Router (moe.py:37-49) -> ``(probs [..., E], ids [..., k] int32, scores [..., k])``."""
+    """Router (moe.py:37-49) -> ``(probs [..., E], ids [..., k] uint32, scores [..., k])``.
+
+    The ids are uint32, as ``mx.argpartition`` returns them (moe.py:45); the
+    other entry points take them as they are (or as int32 / int64).
+    """
     lib = _lib.load()
     dev = _lib.require_device(x, w_router.weight, w_router.scales, w_router.biases)
     *lead, H = x.shape
@@ -67,7 +73,7 @@ def route_topk(x: torch.Tensor, w_router: QuantizedWeights, top_k: int,
     E = w_router.weight.shape[0]
     wr = _i32(w_router.weight)
     probs = torch.empty((T, E), dtype=x.dtype, device=dev)
-    ids = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    ids = torch.empty((T, top_k), dtype=torch.uint32, device=dev)
     scores = torch.empty((T, top_k), dtype=x.dtype, device=dev)
     size = ctypes.c_size_t()
     _lib.check(lib.nvm_route_workspace_size(T, H, E, ctypes.byref(size)))
