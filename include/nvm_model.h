@@ -72,6 +72,19 @@ int nvm_moe_forward_residual_norm(const void *x, int64_t T, int64_t H, int64_t I
                                   void *x_out, int regime, void *workspace,
                                   size_t workspace_bytes, nvm_stream_t stream);
 
+/*
+ * Embedding lookup of a 4-bit affine-quantised table (MLX layout, as the
+ * expert weights): out[t] = rnd(q * s + b) over row tokens[t], the value
+ * computed in float32 and rounded once to the activation dtype.  Replaces
+ * `QuantizedEmbedding.__call__` (layers/embed_head.py:21-36: mx.dequantize of
+ * the gathered rows).  tokens [T] int32; wq [V, D/8] uint32; scales, biases
+ * [V, D/group] act; out [T, D] act (16-byte aligned).  Ids outside [0, V)
+ * give zero rows (the reference reads out of bounds there).
+ */
+int nvm_embedding(const int32_t *tokens, int64_t T, const uint32_t *wq, const void *scales,
+                  const void *biases, int64_t V, int64_t D, int group_size, int bits, int dtype,
+                  void *out, nvm_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -75,10 +75,16 @@ struct Act<DT_F16> {
   }
   __device__ static __forceinline__ float lo(uint32_t d) { return to_f32(d & 0xFFFFu); }
   __device__ static __forceinline__ float hi(uint32_t d) { return to_f32(d >> 16); }
+  // The float32 operand is kept as such (empty asm): left free, the compiler
+  // fuses a preceding fma or multiply and this conversion into one
+  // v_fma_mixlo_f16, which rounds the exact result straight to fp16 and
+  // parts from the float32 value rounded to fp16 where that is an fp16 tie.
   __device__ static __forceinline__ uint16_t from_f32(float f) {
+    asm volatile("" : "+v"(f));
     return __builtin_bit_cast(uint16_t, (_Float16)f);
   }
   __device__ static __forceinline__ uint32_t pack2(float a, float b) {
+    asm volatile("" : "+v"(a), "+v"(b));
     f16x2 v = {(_Float16)a, (_Float16)b};
     return __builtin_bit_cast(uint32_t, v);
   }

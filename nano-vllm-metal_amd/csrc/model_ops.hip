@@ -259,6 +259,57 @@ hipError_t launch_combine_residual_norm(int dtype, const void *down, const void 
   return hipGetLastError();
 }
 
+// Embedding rows of a 4-bit affine-quantised table: out[t, c] =
+// rnd(q * s + b) for the row of token t, one packed word (eight values) per
+// thread.  q * s is exact in float32 (at most 4 + 11 significant bits); the
+// sum is rounded to float32 and then to the activation dtype (Act's
+// conversions keep the float32 value), as a float32 dequantisation followed
+// by a cast.  Ids outside [0, V) give zero rows.
+template <int DT>
+__global__ __launch_bounds__(256) void embedding_kernel(const int32_t *__restrict__ tokens,
+                                                        const uint32_t *__restrict__ wq,
+                                                        const uint16_t *__restrict__ sc,
+                                                        const uint16_t *__restrict__ bi, int V,
+                                                        int D8, int G, int gs8,
+                                                        uint16_t *__restrict__ out, int64_t T) {
+  using A = Act<DT>;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // packed word
+  if (i >= T * D8) return;
+  const int64_t t = i / D8;
+  const int w = (int)(i - t * D8);
+  const int id = tokens[t];
+  u32x4 o = {0u, 0u, 0u, 0u};
+  if (id >= 0 && id < V) {
+    const uint32_t q = wq[(int64_t)id * D8 + w];
+    const int g = w / gs8;
+    const float s = A::to_f32(sc[(int64_t)id * G + g]);
+    const float b = A::to_f32(bi[(int64_t)id * G + g]);
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf((float)((q >> (4 * j)) & 15u), s, b);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = A::pack2(v[2 * j], v[2 * j + 1]);
+  }
+  *(u32x4 *)(out + i * 8) = o;
+}
+
+hipError_t launch_embedding(int dtype, const int32_t *tokens, int64_t T, const uint32_t *wq,
+                            const void *sc, const void *bi, int64_t V, int64_t D, int gs,
+                            void *out, hipStream_t st) {
+  if (T == 0) return hipSuccess;
+  const int64_t words = T * (D / 8);
+  const unsigned grid = (unsigned)((words + 255) / 256);
+  if (dtype == DT_BF16)
+    hipLaunchKernelGGL(embedding_kernel<DT_BF16>, dim3(grid), dim3(256), 0, st, tokens, wq,
+                       (const uint16_t *)sc, (const uint16_t *)bi, (int)V, (int)(D / 8),
+                       (int)(D / gs), gs / 8, (uint16_t *)out, T);
+  else
+    hipLaunchKernelGGL(embedding_kernel<DT_F16>, dim3(grid), dim3(256), 0, st, tokens, wq,
+                       (const uint16_t *)sc, (const uint16_t *)bi, (int)V, (int)(D / 8),
+                       (int)(D / gs), gs / 8, (uint16_t *)out, T);
+  return hipGetLastError();
+}
+
 bool combine_residual_norm_supports(int64_t H) { return H % 8 == 0 && H <= 8 * kNormThreads * kCombChunks; }
 
 }  // namespace nvm
@@ -344,6 +395,33 @@ int nvm_qk_norm_rope_store(const void *qkv, int64_t T, int Hq, int Hkv, int64_t 
     hipLaunchKernelGGL(qk_norm_rope_store_kernel<DT_F16>, dim3(grid), dim3(256), 0, st, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(NVM_ERR_HIP, "qk_norm_rope_store: %s", hipGetErrorString(e));
+  return NVM_OK;
+}
+
+int nvm_embedding(const int32_t *tokens, int64_t T, const uint32_t *wq, const void *scales,
+                  const void *biases, int64_t V, int64_t D, int group_size, int bits, int dtype,
+                  void *out, nvm_stream_t stream) {
+  using namespace nvm;
+  if (dtype != NVM_DTYPE_F16 && dtype != NVM_DTYPE_BF16)
+    return set_error(NVM_ERR_INVALID, "embedding: dtype must be f16 or bf16");
+  if (bits != 4) return set_error(NVM_ERR_UNSUPPORTED, "embedding: only 4-bit weights");
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return set_error(NVM_ERR_UNSUPPORTED, "embedding: group_size %d not in {32, 64, 128}",
+                     group_size);
+  if (T < 0 || V <= 0 || D <= 0 || D % group_size)
+    return set_error(NVM_ERR_INVALID, "embedding: bad shape T=%lld V=%lld D=%lld", (long long)T,
+                     (long long)V, (long long)D);
+  if (V > INT32_MAX || T * (D / 8) > (int64_t)UINT32_MAX * 256)
+    return set_error(NVM_ERR_UNSUPPORTED, "embedding: table or batch too large");
+  if (T == 0) return NVM_OK;
+  if (!tokens || !wq || !scales || !biases || !out)
+    return set_error(NVM_ERR_INVALID, "embedding: null pointer");
+  if (((uintptr_t)out & 15) != 0)
+    return set_error(NVM_ERR_INVALID, "embedding: out must be 16-byte aligned");
+  const hipError_t e = launch_embedding(dtype == NVM_DTYPE_BF16 ? DT_BF16 : DT_F16, tokens, T, wq,
+                                        scales, biases, V, D, group_size, out,
+                                        (hipStream_t)stream);
+  if (e != hipSuccess) return set_error(NVM_ERR_HIP, "embedding: %s", hipGetErrorString(e));
   return NVM_OK;
 }
 

@@ -57,6 +57,7 @@ SIGNATURES = {
                             _P, ctypes.c_float, _I, _I, _I, _I, _P, _P, _SZ, _P],
     "nvm_causal_attention": [_P, _P, _P, _I64, _I64, _I, _I, _I64, ctypes.c_float, _I, _I, _P, _P],
     "nvm_residual_rms_norm": [_P, _P, _P, _I64, _I64, ctypes.c_float, _I, _P, _P, _P],
+    "nvm_embedding": [_P, _I64, _P, _P, _P, _I64, _I64, _I, _I, _I, _P, _P],
     "nvm_qk_norm_rope_store": [_P, _I64, _I, _I, _I64, _P, _P, ctypes.c_float, _P, _P, _P, _I64,
                                _P, _P, _P, _P, _I64, _I64, _I, _P, _P, _P, _P],
     "nvm_moe_forward_residual_norm": [_P, _I64, _I64, _I64, _I64, _I, _I, _I, _I, _I,

@@ -16,6 +16,31 @@ import torch
 from . import _lib
 
 
+def embedding(tokens: torch.Tensor, table, dtype: torch.dtype) -> torch.Tensor:
+    """``QuantizedEmbedding.__call__`` (layers/embed_head.py:21-36): the rows of
+    ``table`` (a 4-bit ``QuantizedWeights`` of shape ``[V, D/8]``) for
+    ``tokens``, dequantised (``q * s + b`` in float32, rounded once to
+    ``dtype``, the dtype of the table's scales); shape ``[*tokens.shape, D]``.
+    Ids outside ``[0, V)`` give zero rows."""
+    lib = _lib.load()
+    dev = _lib.require_device(tokens, table.weight, table.scales, table.biases)
+    if table.scales.dtype != dtype or table.biases.dtype != dtype:
+        raise ValueError("embedding: scales and biases must have the output dtype")
+    V, D8 = table.weight.shape
+    D = D8 * 8
+    ids = tokens.reshape(-1).to(torch.int32).contiguous()
+    out = torch.empty((ids.numel(), D), dtype=dtype, device=dev)
+    wq = table.weight.contiguous()
+    if wq.dtype == torch.uint32:
+        wq = wq.view(torch.int32)
+    _lib.check(lib.nvm_embedding(ids.data_ptr(), ids.numel(), wq.data_ptr(),
+                                 table.scales.contiguous().data_ptr(),
+                                 table.biases.contiguous().data_ptr(), V, D, table.group_size,
+                                 table.bits, _lib.dtype_code(dtype), out.data_ptr(),
+                                 _lib.stream_of(dev)))
+    return out.reshape(*tokens.shape, D)
+
+
 def residual_rms_norm(h: torch.Tensor, r: Optional[torch.Tensor], weight: torch.Tensor,
                       eps: float) -> Tuple[torch.Tensor, torch.Tensor]:
     """``(h + r, rms_norm(h + r) * weight)``; with ``r`` None, ``(h, rms_norm(h) * weight)``."""

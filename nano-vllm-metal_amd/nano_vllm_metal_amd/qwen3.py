@@ -32,9 +32,9 @@ from typing import List, Optional, Sequence
 import torch
 
 from .attention import causal_attention, causal_attention_supports, paged_attention
-from .fused import moe_residual_rms_norm, qk_norm_rope_store, residual_rms_norm
+from .fused import embedding, moe_residual_rms_norm, qk_norm_rope_store, residual_rms_norm
 from .kv_cache import PagedKVCache
-from .linear import QuantizedWeights, dequantize, quantized_linear
+from .linear import QuantizedWeights, quantized_linear
 from .moe import Moe
 
 
@@ -169,11 +169,12 @@ class Qwen3Model:
                             page_size, self.dtype, self.device)
 
     def embed(self, tokens: torch.Tensor) -> torch.Tensor:
-        """``QuantizedEmbedding`` (layers/embed_head.py:21-36): dequantised rows."""
+        """``QuantizedEmbedding`` (layers/embed_head.py:21-36): dequantised rows
+        (``nvm_embedding``)."""
+        # (mx.dequantize returns the scales' dtype; a table stored in another
+        # dtype than the model's is then cast, as the reference's next op does)
         w = self.embed_w
-        rows = dequantize(w.weight[tokens], w.scales[tokens], w.biases[tokens], w.group_size,
-                          w.bits)
-        return rows.to(self.dtype)
+        return embedding(tokens, w, w.scales.dtype).to(self.dtype)
 
     def _attention(self, li: int, layer: Qwen3Layer, x: torch.Tensor, step: "StepInputs",
                    cache: PagedKVCache) -> torch.Tensor:

@@ -119,3 +119,39 @@ def test_moe_combine_residual_norm(T, dt):
     h2, x2 = moe_residual_rms_norm(moe, x, h, w, 1e-6)
     assert torch.equal(h2, h_ref)
     _near(x2, x_ref, dt, "norm of the residual")
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_embedding(dt, gs):
+    """nvm_embedding against the float32 dequantisation of the gathered rows,
+    bit for bit (QuantizedEmbedding.__call__, layers/embed_head.py:21-36);
+    ids outside the table give zero rows."""
+    import numpy as np
+
+    from nano_vllm_metal_amd import QuantizedWeights
+    from nano_vllm_metal_amd.fused import embedding
+    from nano_vllm_metal_amd.linear import dequantize
+
+    g = torch.Generator().manual_seed(gs)
+    V, D = 1000, 1024
+    wq = torch.randint(-2 ** 31, 2 ** 31 - 1, (V, D // 8), generator=g, dtype=torch.int64)
+    wq = wq.to(torch.int32).to(DEV)
+    # scales and biases over many binades, both signs
+    sc = (torch.randn(V, D // gs, generator=g) * 2.0 ** torch.randint(-20, 8, (V, D // gs),
+                                                                     generator=g)).to(dt).to(DEV)
+    bi = (torch.randn(V, D // gs, generator=g) * 2.0 ** torch.randint(-20, 8, (V, D // gs),
+                                                                     generator=g)).to(dt).to(DEV)
+    table = QuantizedWeights(sc, bi, gs, 4, wq)
+    tokens = torch.tensor([[0, 999, 17, 17, 500], [3, -1, 1000, 2 ** 30, 42]], dtype=torch.int32,
+                          device=DEV)
+    got = embedding(tokens, table, dt)
+    torch.cuda.synchronize()
+    assert got.shape == (2, 5, D) and got.dtype == dt
+    valid = (tokens >= 0) & (tokens < V)
+    ids = torch.where(valid, tokens, torch.zeros_like(tokens)).long()
+    want = dequantize(wq[ids], sc[ids], bi[ids], gs, 4).to(dt)
+    want = torch.where(valid[..., None], want, torch.zeros_like(want))
+    g_bits = got.view(torch.int16).cpu().numpy()
+    w_bits = want.view(torch.int16).cpu().numpy()
+    assert np.array_equal(g_bits, w_bits)
