@@ -414,6 +414,41 @@ def test_moe_decode_is_batch_invariant(H, I, T_full):
         assert torch.equal(part, full[:T]), f"T={T} differs from the first rows of T={T_full}"
 
 
+@pytest.mark.parametrize("T", [1, 5, 8, 12])
+@pytest.mark.parametrize("act", ["bfloat16", "float16"])
+def test_moe_decode_routing_ties(T, act):
+    """The routing that the decode products finalise (one token a wavefront
+    up to eight tokens, four a wavefront above): an all-zero router gives
+    every expert probability 1/E, so top-k is experts 0..k-1 and each score
+    1/k; router rows equal in threes tie each token's experts in groups of
+    three at distinct levels, where the lower index must win inside a group."""
+    E, H, I, k, gs = 128, 256, 128, 8, 64
+    x, w = _moe_case(170 + T, T, H, E, I, act)
+    wq, s, b = w["router"]
+    w0 = dict(w, router=(np.zeros_like(wq), np.zeros_like(s), np.zeros_like(b)))
+    moe = make_moe(w0, act, gs, k, True, DEV)
+    moe.regime = "decode"
+    _, ids, scores = moe.forward(to_act(x, act, DEV), return_routing=True)
+    torch.cuda.synchronize()
+    assert ids.cpu().tolist() == [list(range(k))] * T
+    assert torch.all(scores.float() == 1.0 / k).item()
+    _check_moe(x, w0, k, True, act, gs, "decode")
+    # levels 2^-6 .. apart so their probabilities stay distinct after rounding
+    lv = O.round_act(np.random.default_rng(171).permutation(np.arange(E // 3 + 1)) * 2.0 ** -6, act)
+    rb = np.repeat(lv[np.arange(E) // 3][:, None], b.shape[1], axis=1)
+    w3 = dict(w, router=(np.zeros_like(wq), np.zeros_like(s), rb.astype(b.dtype)))
+    _check_moe(x, w3, k, True, act, gs, "decode")
+    moe3 = make_moe(w3, act, gs, k, True, DEV)
+    moe3.regime = "decode"
+    _, ids3, _ = moe3.forward(to_act(x, act, DEV), return_routing=True)
+    ids3 = ids3.cpu().numpy()
+    for t in range(T):
+        g = ids3[t] // 3
+        for j in range(k - 1):
+            if g[j] == g[j + 1]:
+                assert ids3[t, j] < ids3[t, j + 1], f"token {t}: tie inside group {g[j]} misordered"
+
+
 def test_moe_235b_decode():
     """H4096 I1536: gate/up through the eight-group slice GEMV (KS 8), down
     through six-group slices in four k-slices."""
