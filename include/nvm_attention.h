@@ -80,8 +80,9 @@ int nvm_paged_attention(const float *q, int64_t N, int64_t L, int64_t D, const v
  * j <= i of its request, query head h reads kv head h / (num_heads /
  * num_kv_heads).  q, k and v must hold values of the activation dtype `dtype`
  * (NVM_DTYPE_BF16 or NVM_DTYPE_F16; the model's q/k norm and RoPE round
- * them): the products are then exact, the sums float32.  D of 64 or 128 and
- * 1, 2, 4, 8 or 16 query heads per kv head (else NVM_ERR_UNSUPPORTED).
+ * them): the products are then exact, the sums float32.  D of 64 or 128,
+ * 1, 2, 4, 8 or 16 query heads per kv head, and a positive finite scale (the
+ * model's head_dim ** -0.5) (else NVM_ERR_UNSUPPORTED).
  */
 int nvm_causal_attention(const float *q, const float *k, const float *v, int64_t B, int64_t L,
                          int num_heads, int num_kv_heads, int64_t D, float scale, int dtype,

@@ -8,11 +8,14 @@
 // rounds them like the reference), so each product of two of them is exact in
 // float32.
 //
-// A block owns (request b, kv head h, 16 columns per wavefront): a column is
-// one (query position, query head) of the heads that share kv head h, so the
-// grouped-query heads read each key and value row once, from LDS.  Columns
-// are 16 / R positions x the R = Hq / Hkv heads; the block's eight
-// wavefronts take consecutive positions.  Per 64-key tile:
+// A block owns (request b, kv head h, two 16-column tiles per wavefront): a
+// column is one (query position, query head) of the heads that share kv
+// head h, so the grouped-query heads read each key and value row once, from
+// LDS.  A column tile is 16 / R positions x the R = Hq / Hkv heads; the
+// block's eight wavefronts take consecutive positions.  Every key or value
+// operand a wavefront reads from LDS feeds the MFMAs of both its column
+// tiles (with one tile per wavefront, the LDS reads per tile took as many
+// cycles as the MFMAs).  Per 64-key tile:
 //   * the tile's keys (act dtype, key-major) and values (act dtype,
 //     transposed: dim-major, key pairs per dword) are staged in LDS by the
 //     whole block, double-buffered, the next tile's rows loaded into
@@ -30,6 +33,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "internal.h"
@@ -40,7 +44,8 @@ namespace nvm {
 namespace {
 
 constexpr float kLog2eC = 1.4426950408889634f;
-constexpr int kCW = 8;      // wavefronts (column tiles) per block
+constexpr int kCW = 8;      // wavefronts per block
+constexpr int kCT = 2;      // 16-column tiles per wavefront
 constexpr int kKT = 64;     // keys per tile
 
 struct CausalArgs {
@@ -60,32 +65,54 @@ __device__ __forceinline__ void store_out_c(void *out, int dt, int64_t i, float 
     ((uint16_t *)out)[i] = Act<DT_F16>::from_f32(v);
 }
 
-// x = p0 + p1 + p2 in the act dtype, for four pairs of values.
+// x = p0 + p1 + p2 in the act dtype, for four pairs of values (x >= 0 and
+// normal or zero, as the probabilities are).  bf16: each part is the upper
+// half of what is left (truncation: x - trunc(x) is exact and has at most 16
+// significant bits, its remainder at most 8, a bf16 value), the pairs packed
+// with one v_perm_b32 a part.  f16: each part rounded to nearest, the packed
+// word pinned so that the compiler takes its halves back instead of
+// converting again.
 template <int DT>
 __device__ __forceinline__ void split3c(const float (&x)[8], u32x4 &p0, u32x4 &p1, u32x4 &p2) {
   using A = Act<DT>;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     float a0 = x[2 * i], a1 = x[2 * i + 1];
-    const uint32_t h = A::pack2(a0, a1);
-    a0 -= A::lo(h);
-    a1 -= A::hi(h);
-    const uint32_t m = A::pack2(a0, a1);
-    a0 -= A::lo(m);
-    a1 -= A::hi(m);
-    p0[i] = h;
-    p1[i] = m;
-    p2[i] = A::pack2(a0, a1);
+    if constexpr (DT == DT_BF16) {
+      const uint32_t h0 = __float_as_uint(a0), h1 = __float_as_uint(a1);
+      a0 -= __uint_as_float(h0 & 0xFFFF0000u);
+      a1 -= __uint_as_float(h1 & 0xFFFF0000u);
+      const uint32_t m0 = __float_as_uint(a0), m1 = __float_as_uint(a1);
+      a0 -= __uint_as_float(m0 & 0xFFFF0000u);
+      a1 -= __uint_as_float(m1 & 0xFFFF0000u);
+      // upper halves of (lo, hi) into one word, lo first
+      p0[i] = perm_b32(h1, h0, 0x07060302u);
+      p1[i] = perm_b32(m1, m0, 0x07060302u);
+      p2[i] = perm_b32(__float_as_uint(a1), __float_as_uint(a0), 0x07060302u);
+    } else {
+      uint32_t h = A::pack2(a0, a1);
+      asm volatile("" : "+v"(h));
+      a0 -= A::lo(h);
+      a1 -= A::hi(h);
+      uint32_t m = A::pack2(a0, a1);
+      asm volatile("" : "+v"(m));
+      a0 -= A::lo(m);
+      a1 -= A::hi(m);
+      p0[i] = h;
+      p1[i] = m;
+      p2[i] = A::pack2(a0, a1);
+    }
   }
 }
 
-template <int DT, int DH, int R>
+template <int DT, int DH, int R, int CT>
 __global__ __launch_bounds__(64 * kCW) void causal_prefill_kernel(CausalArgs a) {
   using A = Act<DT>;
   constexpr int NC = DH / 32;       // 32-dim steps of a score MFMA
   constexpr int NT = DH / 16;       // 16-dim tiles of the output
   constexpr int PPC = 16 / R;       // query positions per column tile
-  constexpr int QB = kCW * PPC;     // query positions per block
+  constexpr int PPW = CT * PPC;     // query positions per wavefront
+  constexpr int QB = kCW * PPW;     // query positions per block
   constexpr int KP = DH + 8;        // LDS pitch of a key row (16-bit elements)
   constexpr int VP = kKT / 2 + 4;   // LDS pitch of a transposed value row (dwords)
   constexpr int DG = DH / 8;        // 8-dim groups of a row
@@ -103,29 +130,38 @@ __global__ __launch_bounds__(64 * kCW) void causal_prefill_kernel(CausalArgs a) 
   const int qb = a.n_qb - 1 - blockIdx.x / (a.B * a.Hkv);
   const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
   const int q0 = qb * QB;
-  // this lane's column: position and query head
-  const int pos = q0 + wv * PPC + c16 / R;
+  const int wp0 = q0 + wv * PPW;  // the wavefront's first query position
+  // this lane's columns: positions (one per column tile) and query head
+  int pos[CT];
+  bool col_ok[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    pos[ct] = wp0 + ct * PPC + c16 / R;
+    col_ok[ct] = pos[ct] < a.L;
+  }
   const int head = kvh * R + c16 % R;
-  const bool col_ok = pos < a.L;
   const int64_t tok0 = (int64_t)b * a.L;  // the request's first token row
 
-  // B operand of the score MFMAs: query (pos, head), dims 32kk + 8G .. +7
-  u32x4 qop[NC];
-  {
-    const float *qp = a.q + ((tok0 + (col_ok ? pos : 0)) * a.Hq + head) * DH;
+  // B operands of the score MFMAs: query (pos, head), dims 32kk + 8G .. +7
+  u32x4 qop[CT][NC];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const float *qp = a.q + ((tok0 + (col_ok[ct] ? pos[ct] : 0)) * a.Hq + head) * DH;
 #pragma unroll
     for (int kk = 0; kk < NC; ++kk) {
       const int d0 = 32 * kk + 8 * G;
-      const f32x4 x0 = col_ok ? *(const f32x4 *)(qp + d0) : f32x4{0.f, 0.f, 0.f, 0.f};
-      const f32x4 x1 = col_ok ? *(const f32x4 *)(qp + d0 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
-      qop[kk] = u32x4{A::pack2(x0[0], x0[1]), A::pack2(x0[2], x0[3]), A::pack2(x1[0], x1[1]),
-                      A::pack2(x1[2], x1[3])};
+      const f32x4 x0 = col_ok[ct] ? *(const f32x4 *)(qp + d0) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 x1 = col_ok[ct] ? *(const f32x4 *)(qp + d0 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      qop[ct][kk] = u32x4{A::pack2(x0[0], x0[1]), A::pack2(x0[2], x0[3]),
+                          A::pack2(x1[0], x1[1]), A::pack2(x1[2], x1[3])};
     }
   }
 
   // keys of the block: every position below q0 + QB (and below L)
   const int kend = min(q0 + QB, a.L);
   const int ntile = (kend + kKT - 1) / kKT;
+  // the wavefront's columns all exist and see every key below wp0 + 1
+  const bool all_cols = wp0 + PPW <= a.L;
 
   // staging loads of tile kt into registers (rows past kend read as zeros)
   f32x4 kreg[KI][2], vreg[VI][4];
@@ -178,10 +214,17 @@ __global__ __launch_bounds__(64 * kCW) void causal_prefill_kernel(CausalArgs a) 
     }
   };
 
-  float m_run = -INFINITY, l_run = 0.f;  // column c16; l_run is this lane's share
-  f32x4 oacc[NT];                        // O^T: column c16, dims 16t + 4G + i
+  // per column tile: running maximum (base 2, scaled) and this lane's share
+  // of the column's sum; O^T: column c16, dims 16t + 4G + i
+  float m_run[CT], l_run[CT];
+  f32x4 oacc[CT][NT];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) oacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int ct = 0; ct < CT; ++ct) {
+    m_run[ct] = -INFINITY;
+    l_run[ct] = 0.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) oacc[ct][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   stage_load(0);
   stage_store(0);
@@ -190,55 +233,91 @@ __global__ __launch_bounds__(64 * kCW) void causal_prefill_kernel(CausalArgs a) 
     const int buf = kt & 1;
     if (kt + 1 < ntile) stage_load(kt + 1);  // uniform
 
-    // S^T: keys 16u + c16 as the A operand (dims 32kk + 8G .. +7)
-    f32x4 acc[4];
+    // S^T: keys 16u + c16 as the A operand (dims 32kk + 8G .. +7), each key
+    // operand read once for the column tiles
+    f32x4 acc[CT][4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < NC; ++kk)
-        acc[u] = A::mfma16(*(const u32x4 *)&s_k[buf][16 * u + c16][32 * kk + 8 * G], qop[kk],
-                           acc[u]);
+      for (int ct = 0; ct < CT; ++ct) acc[ct][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < NC; ++kk) {
+        const u32x4 kop = *(const u32x4 *)&s_k[buf][16 * u + c16][32 * kk + 8 * G];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[ct][u] = A::mfma16(kop, qop[ct][kk], acc[ct][u]);
+      }
     }
-    // causal mask (key j <= position, j < L), base-2 scores, online softmax
-    float sc[4][4];
-    float tmax = -INFINITY;
+    // causal mask (key j <= position, j < L) unless every key of the tile is
+    // visible to every column of the wavefront (uniform), base-2 scores,
+    // online softmax
+    // Causal mask (key j <= position, j < L), base-2 scores, online softmax.
+    // Interior tiles (every key of the tile visible to every column of the
+    // wavefront, all columns real: uniform) take a path without the mask and
+    // without the guard for a column that has seen no key yet.  scale2 > 0:
+    // the maximum of the raw scores scaled is the maximum of the scaled
+    // scores, and exp2(s * scale2 - m) is one fma into v_exp_f32, whose
+    // results below 2^-126 (terms that far below the column maximum) flush to
+    // zero, which the float32 sum cannot tell.
+    float pv[CT][4][4];
+    bool rescale = false;
+    float alpha[CT];
+    auto softmax = [&](auto interior) {
+      constexpr bool kIn = decltype(interior)::value;
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+      for (int ct = 0; ct < CT; ++ct) {
+        float tmax = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int j = kt * kKT + 16 * u + 4 * G + i;
-        const bool valid = col_ok && j <= pos;
-        sc[u][i] = valid ? acc[u][i] * a.scale2 : -INFINITY;
-        tmax = fmaxf(tmax, sc[u][i]);
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j = kt * kKT + 16 * u + 4 * G + i;
+            pv[ct][u][i] = kIn || (col_ok[ct] && j <= pos[ct]) ? acc[ct][u][i] : -INFINITY;
+            tmax = fmaxf(tmax, pv[ct][u][i]);
+          }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float m_new = fmaxf(m_run[ct], tmax * a.scale2);
+        const bool any = kIn || m_new != -INFINITY;
+        alpha[ct] = any ? __builtin_amdgcn_exp2f(m_run[ct] - m_new) : 1.f;
+        rescale |= alpha[ct] != 1.f;
+        float psum = 0.f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            pv[ct][u][i] =
+                any ? __builtin_amdgcn_exp2f(__builtin_fmaf(pv[ct][u][i], a.scale2, -m_new)) : 0.f;
+            psum += pv[ct][u][i];
+          }
+        l_run[ct] = l_run[ct] * alpha[ct] + psum;
+        m_run[ct] = m_new;
       }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    const bool any = m_new != -INFINITY;
-    const float alpha = any ? exp2f(m_run - m_new) : 1.f;
-    float psum = 0.f;
-    float pv[4][4];
+    };
+    if (all_cols && kt * kKT + kKT - 1 <= wp0)
+      softmax(std::true_type{});
+    else
+      softmax(std::false_type{});
+    // O^T *= alpha, skipped when no column's maximum moved (the factors are
+    // then all 1)
+    if (__builtin_amdgcn_ballot_w64(rescale)) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+      for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pv[u][i] = any ? exp2f(sc[u][i] - m_new) : 0.f;
-        psum += pv[u][i];
-      }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
+        for (int t = 0; t < NT; ++t) oacc[ct][t] *= alpha[ct];
+    }
 
-    // O^T += V^T . P^T per 32-key chunk
+    // O^T += V^T . P^T per 32-key chunk, each value operand read once for the
+    // column tiles
 #pragma unroll
     for (int kc = 0; kc < 2; ++kc) {
-      const float x[8] = {pv[2 * kc][0], pv[2 * kc][1], pv[2 * kc][2], pv[2 * kc][3],
-                          pv[2 * kc + 1][0], pv[2 * kc + 1][1], pv[2 * kc + 1][2],
-                          pv[2 * kc + 1][3]};
-      u32x4 pb[3];
-      split3c<DT>(x, pb[0], pb[1], pb[2]);
+      u32x4 pb[CT][3];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const float x[8] = {pv[ct][2 * kc][0],     pv[ct][2 * kc][1],     pv[ct][2 * kc][2],
+                            pv[ct][2 * kc][3],     pv[ct][2 * kc + 1][0], pv[ct][2 * kc + 1][1],
+                            pv[ct][2 * kc + 1][2], pv[ct][2 * kc + 1][3]};
+        split3c<DT>(x, pb[ct][0], pb[ct][1], pb[ct][2]);
+      }
       // key pairs (4G, 4G+1), (4G+2, 4G+3) and the same + 16 of the chunk
       const int kp0 = 16 * kc + 2 * G, kp1 = 16 * kc + 8 + 2 * G;
 #pragma unroll
@@ -248,7 +327,10 @@ __global__ __launch_bounds__(64 * kCW) void causal_prefill_kernel(CausalArgs a) 
         const u32x2 hi = *(const u32x2 *)&row[kp1];
         const u32x4 va{lo.x, lo.y, hi.x, hi.y};
 #pragma unroll
-        for (int part = 0; part < 3; ++part) oacc[t] = A::mfma16(va, pb[part], oacc[t]);
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int part = 0; part < 3; ++part)
+            oacc[ct][t] = A::mfma16(va, pb[ct][part], oacc[ct][t]);
       }
     }
     // the next tile's rows into the other buffer (every wavefront passed the
@@ -257,17 +339,21 @@ __global__ __launch_bounds__(64 * kCW) void causal_prefill_kernel(CausalArgs a) 
     __syncthreads();
   }
 
-  // the column's sum (four lane shares), then O = O^T / l
-  l_run += __shfl_xor(l_run, 16);
-  l_run += __shfl_xor(l_run, 32);
-  if (col_ok) {
-    const int64_t o0 = ((tok0 + pos) * a.Hq + head) * DH;
+  // each column's sum (four lane shares), then O = O^T / l
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+  for (int ct = 0; ct < CT; ++ct) {
+    float l = l_run[ct];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (col_ok[ct]) {
+      const int64_t o0 = ((tok0 + pos[ct]) * a.Hq + head) * DH;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        store_out_c(a.out, a.out_dt, o0 + 16 * t + 4 * G + i,
-                    l_run > 0.f ? oacc[t][i] / l_run : 0.f);
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          store_out_c(a.out, a.out_dt, o0 + 16 * t + 4 * G + i,
+                      l > 0.f ? oacc[ct][t][i] / l : 0.f);
+    }
   }
 }
 
@@ -281,11 +367,11 @@ hipError_t launch_causal_r(const CausalArgs &a0, int R, hipStream_t st) {
     return hipGetLastError();
   };
   switch (R) {
-    case 1: return go(causal_prefill_kernel<DT, DH, 1>, kCW * 16);
-    case 2: return go(causal_prefill_kernel<DT, DH, 2>, kCW * 8);
-    case 4: return go(causal_prefill_kernel<DT, DH, 4>, kCW * 4);
-    case 8: return go(causal_prefill_kernel<DT, DH, 8>, kCW * 2);
-    case 16: return go(causal_prefill_kernel<DT, DH, 16>, kCW);
+    case 1: return go(causal_prefill_kernel<DT, DH, 1, kCT>, kCW * kCT * 16);
+    case 2: return go(causal_prefill_kernel<DT, DH, 2, kCT>, kCW * kCT * 8);
+    case 4: return go(causal_prefill_kernel<DT, DH, 4, kCT>, kCW * kCT * 4);
+    case 8: return go(causal_prefill_kernel<DT, DH, 8, kCT>, kCW * kCT * 2);
+    case 16: return go(causal_prefill_kernel<DT, DH, 16, kCT>, kCW * kCT);
     default: return hipErrorInvalidValue;
   }
 }
@@ -310,6 +396,9 @@ extern "C" int nvm_causal_attention(const float *q, const float *k, const float 
     return set_error(NVM_ERR_UNSUPPORTED,
                      "causal_attention: head dim 64 or 128 and 1, 2, 4, 8 or 16 query heads "
                      "per kv head (got D=%lld, %d)", (long long)D, R);
+  if (!(scale > 0.f) || !(scale <= 1.0e15f))
+    return set_error(NVM_ERR_UNSUPPORTED,
+                     "causal_attention: scale must be positive and finite (got %g)", (double)scale);
   if (B * L == 0) return NVM_OK;
   if (!q || !k || !v || !out) return set_error(NVM_ERR_INVALID, "causal_attention: null pointer");
   if (B * L * num_heads * D >= (1ll << 31) || B * num_kv_heads > (1 << 20))

@@ -250,6 +250,33 @@ def test_paged_attention_validation(kw, code, msg):
     assert msg in _err(lib)
 
 
+def _causal(lib, **kw):
+    a = dict(q=1, k=1, v=1, B=2, L=16, hq=32, hkv=4, D=128, scale=0.088, dt=1, odt=1, out=1)
+    a.update(kw)
+    return lib.nvm_causal_attention(a["q"], a["k"], a["v"], a["B"], a["L"], a["hq"], a["hkv"],
+                                    a["D"], a["scale"], a["dt"], a["odt"], a["out"], None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    ({"scale": 0.0}, -2, "scale must be positive"),
+    ({"scale": -0.1}, -2, "scale must be positive"),
+    ({"scale": float("nan")}, -2, "scale must be positive"),
+    ({"scale": float("inf")}, -2, "scale must be positive"),
+    ({"D": 96}, -2, "head dim"),
+    ({"hq": 24, "hkv": 8}, -2, "query heads per kv head"),
+    ({"hq": 30}, -1, "bad shape"),
+    ({"dt": 7}, -1, "dtype must be f16 or bf16"),
+    ({"q": None}, -1, "null pointer"),
+])
+def test_causal_attention_validation(kw, code, msg):
+    """Argument checks of nvm_causal_attention return before device work.  The
+    kernel's softmax takes the maximum of the raw scores and scales it, so the
+    scale must be positive (the model passes head_dim ** -0.5)."""
+    _, lib = _lib()
+    assert _causal(lib, **kw) == code
+    assert msg in _err(lib)
+
+
 def test_paged_attention_workspace_size():
     _, lib = _lib()
     sz = ctypes.c_size_t()
