@@ -206,7 +206,9 @@ int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, i
  * stages 0..3 in order compute exactly what nvm_moe_forward computes (the
  * Moe.__call__ steps of layers/moe.py:77-86, one at a time).  ids_out and
  * scores_out, when given, must be the same in every stage; y is written by
- * stage 3 only.
+ * stage 3 only.  (For decode batches of at most 16 pairs nvm_moe_forward
+ * runs stages 2 and 3 as one launch, the down product with the combine in
+ * its epilogue; its y is bit-identical to stages 2 and 3 run apart.)
  */
 int nvm_moe_forward_stage(int stage, const void *x, int64_t T, int64_t H, int64_t I, int64_t E,
                           int top_k, int norm_topk_prob, int group_size, int bits, int dtype,

@@ -2,6 +2,7 @@
 // workspace layout and the launch sequence of the MoE block.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <algorithm>
 #include <mutex>
@@ -271,6 +272,38 @@ nvm::GroupedArgs down_args(const void *h, int64_t n_pairs, int64_t H, int64_t I,
   d.o_map = sorted;
   d.out_ld = H;
   return d;
+}
+
+// The forward's decode down product with the combine in its epilogue (one
+// block per 16 columns of y over every pair), for batches of at most
+// kDownCombinePairs pairs: y is bit-identical to the down product followed
+// by the combine, so the choice by batch size keeps every token's output
+// independent of its batch.  It saves the combine launch, but its 128 blocks
+// (H 2048) each stream every touched expert's 16 rows with one unit of ring
+// per wavefront: one token's layer took 28.6 against 30.5 us, eight tokens'
+// 62.7 against 56.9 us.  NVM_DOWN_COMBINE=0/1 overrides the choice.
+constexpr int64_t kDownCombinePairs = 16;
+bool use_down_combine(int regime, int64_t T, int64_t H, int64_t I, int64_t E, int top_k,
+                      int group_size) {
+  const int64_t N = T * top_k;
+  if (!use_decode(regime, N, E, I) ||
+      !nvm::gemv3_down_combine_supports((int)I, (int)H, (int)E, group_size, N, top_k))
+    return false;
+  const char *v = getenv("NVM_DOWN_COMBINE");
+  if (v && (v[0] == '0' || v[0] == '1')) return v[0] == '1';
+  return N <= kDownCombinePairs;
+}
+
+int run_down_combine(int dtype, const MoeWs &ws, const uint16_t *scores, int64_t T, int64_t H,
+                     int64_t I, int64_t E, int top_k, int group_size, const uint32_t *wd,
+                     const void *sd, const void *bd, void *y, nvm_stream_t stream) {
+  nvm::GroupedArgs d = down_args(ws.h, T * top_k, H, I, E, group_size, wd, sd, bd, ws.offsets,
+                                 ws.sorted, nullptr);
+  d.c_scores = scores;
+  d.c_y = (uint16_t *)y;
+  d.c_k = top_k;
+  NVM_TRY_HIP(nvm::launch_gemv3_down_combine(dtype, d, (hipStream_t)stream));
+  return NVM_OK;
 }
 
 // Routing, dispatch and both expert products of the block (everything but
@@ -580,11 +613,14 @@ int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, i
   NVM_REQUIRE(y || T == 0, "moe: null pointer");
   MoeWs ws{};
   uint16_t *scores = nullptr;
+  const bool fdc = T > 0 && use_down_combine(regime, T, H, I, E, top_k, group_size);
   if (int r = moe_stages(x, T, H, I, E, top_k, norm_topk_prob, group_size, bits, dtype, wr, sr,
                          br, wg, sg, bg, wu, su, bu, wd, sd, bd, ids_out, scores_out, regime,
-                         workspace, workspace_bytes, stream, ws, scores))
+                         workspace, workspace_bytes, stream, ws, scores, 0, fdc ? 1 : 2))
     return r;
   if (T == 0) return NVM_OK;
+  if (fdc) return run_down_combine(dtype, ws, scores, T, H, I, E, top_k, group_size, wd, sd, bd, y,
+                                   stream);
   return nvm_moe_combine(ws.down, scores, T, top_k, H, dtype, y, stream);
 }
 

@@ -33,6 +33,7 @@
 //   turn.
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 #include "common.h"
 #include "finalize.h"
@@ -93,15 +94,27 @@ __device__ __forceinline__ uint32_t sb_val(const u32x2 &v, int j) {
 // whose expert no token chose ends there.  Its units are the (tile, chunk)
 // pairs of its tiles and its expert's chunks, tile-major, so that an expert
 // of more than 16 rows reads a tile's weights again from the cache.
-template <int DT, bool DUAL, int NS, bool FUSED, bool STATIC>
+//
+// TILE: the down product with the combine in its epilogue (decode batches of
+// at most kTilePairs pairs).  Block b owns the 16 weight rows [16 b, 16 b +
+// 16), i.e. 16 columns of y, and every chunk of every expert the batch
+// touches: its units are (chunk, its tile), in chunk order, dealt over its
+// wavefronts phase by phase.  A unit's outputs are the ones the dealt down
+// product computes for those rows (the same steps in the same order), and
+// go, rounded to the act dtype, into LDS by sorted slot; after the last
+// phase the block sums each token's k slots for its 16 columns as
+// combine_kernel does (act-rounded terms rnd(down * score), float32, slot
+// order, rounded once) and stores y.  No partial result leaves the block.
+template <int DT, bool DUAL, int NS, bool FUSED, bool STATIC, bool TILE = false>
 __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, int RT, int SPE) {
   using A = Act<DT>;
   constexpr int D = NS % 4 == 0 ? 4 : 3;  // ring slots
   static_assert(NS % D == 0, "the ring must divide the steps of a unit");
+  static_assert(!TILE || (!DUAL && !FUSED && !STATIC), "TILE is a mode of the down product");
   constexpr int K = 256 * NS, KW = K / 8, G64 = K / 64;
   constexpr int ROWB = row_bytes(K);
-  constexpr int NM = 2;                    // gate and up, or two row tiles
-  constexpr int RU = DUAL ? kRows : 2 * kRows;  // weight rows per unit
+  constexpr int NM = TILE ? 1 : 2;         // gate and up, or one or two row tiles
+  constexpr int RU = DUAL ? kRows : NM * kRows;  // weight rows per unit
   // 16-byte windows per lane of a weight row's scales (or biases): lane
   // group G holds groups 8G..8G+7 of window j, 32j + 8G.. of the row
   constexpr int SBW = (G64 + 31) / 32;
@@ -114,13 +127,18 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
   __shared__ int s_cb[kMaxExperts + 1];   // first chunk index of each expert
   __shared__ int s_round[kMaxRounds][4];  // expert, first slot, rows, first staged row
   __shared__ int s_nph, s_nrows;          // chunks and staged rows of the current phase
-  __shared__ int s_orow[DUAL ? 1 : kMaxRounds][kRows];  // output rows (single product)
+  __shared__ int s_orow[DUAL || TILE ? 1 : kMaxRounds][kRows];  // output rows (single product)
   static_assert(!FUSED || DUAL, "only the gate/up product finalises the routing");
   // routing finalised here (route_part): ids, scores and the sorted pairs
   __shared__ int s_rids[FUSED ? kFusedPairs : 1];
   __shared__ uint16_t s_rsc[FUSED ? kFusedPairs : 1];
   __shared__ int s_sorted[FUSED ? kFusedPairs : 1];
   __shared__ uint64_t s_mask[FUSED ? kRowExperts : 1];  // token set of each expert
+  // TILE: the tile's down outputs [slot][16] (act bits), the slot of each
+  // pair and each pair's score (act bits)
+  __shared__ uint16_t s_y[TILE ? kTilePairs * kRows : 1];
+  __shared__ int s_inv[TILE ? kTilePairs : 1];
+  __shared__ uint16_t s_csc[TILE ? kTilePairs : 1];
 
   hoist_args(a.act, a.act_ld, a.act_rows, a.a_map, a.a_div, a.offsets, a.w0, a.s0, a.b0, a.w1,
              a.s1, a.b1, a.R, a.gs, a.E, a.out, a.o_map, a.out_ld, RT, SPE);
@@ -147,12 +165,15 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
   // whole-tensor descriptors: every expert's rows are reached through 32-bit
   // offsets (the host keeps E * R * K / 2 below 2 GiB)
   const int64_t ER = (int64_t)E * R;
-  const rsrc_t w_r[NM] = {make_rsrc(a.w0, (uint32_t)(ER * KW * 4)),
-                          make_rsrc(DUAL ? a.w1 : a.w0, (uint32_t)(ER * KW * 4))};
-  const rsrc_t s_r[NM] = {make_rsrc(a.s0, (uint32_t)(ER * G64 * 2)),
-                          make_rsrc(DUAL ? a.s1 : a.s0, (uint32_t)(ER * G64 * 2))};
-  const rsrc_t b_r[NM] = {make_rsrc(a.b0, (uint32_t)(ER * G64 * 2)),
-                          make_rsrc(DUAL ? a.b1 : a.b0, (uint32_t)(ER * G64 * 2))};
+  rsrc_t w_r[NM], s_r[NM], b_r[NM];
+  w_r[0] = make_rsrc(a.w0, (uint32_t)(ER * KW * 4));
+  s_r[0] = make_rsrc(a.s0, (uint32_t)(ER * G64 * 2));
+  b_r[0] = make_rsrc(a.b0, (uint32_t)(ER * G64 * 2));
+  if constexpr (NM > 1) {
+    w_r[NM - 1] = make_rsrc(DUAL ? a.w1 : a.w0, (uint32_t)(ER * KW * 4));
+    s_r[NM - 1] = make_rsrc(DUAL ? a.s1 : a.s0, (uint32_t)(ER * G64 * 2));
+    b_r[NM - 1] = make_rsrc(DUAL ? a.b1 : a.b0, (uint32_t)(ER * G64 * 2));
+  }
   const rsrc_t act_r = make_rsrc(a.act, (uint32_t)(a.act_rows * a.act_ld * 2));
 
   // ring: the weights, two 16-byte loads per matrix and step
@@ -237,6 +258,17 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
     // (no offsets: one expert over all act_rows rows, the dense product)
     for (int i = tid; i <= E; i += 64 * kW)
       s_off[i] = a.offsets ? a.offsets[i] : (i == 0 ? 0 : (int)a.act_rows);
+    if constexpr (TILE) {
+      // the slot of every pair (inverse of o_map) and its score, for the
+      // combine after the last phase
+      for (int i = tid; i < (int)a.act_rows; i += 64 * kW) s_inv[i] = 0;
+      __syncthreads();
+      for (int i = tid; i < (int)a.act_rows; i += 64 * kW) {
+        const int p = a.o_map[i];
+        if ((unsigned)p < (unsigned)a.act_rows) s_inv[p] = i;
+        s_csc[i] = a.c_scores[i];
+      }
+    }
     __syncthreads();
     if (wv == 0) {
       // chunk bases: exclusive prefix over experts of ceil(rows / 16)
@@ -267,6 +299,13 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
     }
     c_first = 0;
     c_last = (n_e + kRows - 1) / kRows - 1;
+  } else if constexpr (TILE) {
+    // every chunk, for this block's tile
+    u0 = 0;
+    u1 = s_cb[E];
+    if (u1 <= u0) return;  // uniform over the block, before any further barrier
+    c_first = 0;
+    c_last = u1 - 1;
   } else {
     const int U = s_cb[E] * RT;
     if ((int64_t)U * gridDim.x < (1ll << 31)) {
@@ -363,7 +402,7 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
     }
     __syncthreads();
     const int n = s_nph, tot = s_nrows * G64;
-    if constexpr (!DUAL) {
+    if constexpr (!DUAL && !TILE) {
       // output rows of the phase's routed rows (single product)
       for (int i = tid; i < n * kRows; i += 64 * kW) {
         const int r = i / kRows, c = i - r * kRows;
@@ -380,8 +419,9 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
       p0 = 0;
       p1 = (tw1 - tw0) * n;
     } else {
-      ua = max(u0, cb * RT);
-      const int ub = min(u1, (cb + n) * RT);
+      const int upc = TILE ? 1 : RT;  // units per chunk (TILE: the block's tile only)
+      ua = max(u0, cb * upc);
+      const int ub = min(u1, (cb + n) * upc);
       const int P = ub - ua;
       auto range_start = [&](int i) { return ua + (int)((unsigned)(i * P) / kW); };
       p0 = range_start(ri);
@@ -393,6 +433,9 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
         const int q = n == 1 ? u : u / n;
         r = u - q * n;
         rt = tw0 + q;
+      } else if constexpr (TILE) {
+        r = u - cb;
+        rt = blockIdx.x;
       } else {
         const int ci = u / RT;
         r = ci - cb;
@@ -452,7 +495,9 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
           for (int v = 0; v < 4; ++v) {
             const int t = 4 * G + v;
             if (t < cnt) {
-              if constexpr (DUAL) {
+              if constexpr (TILE) {
+                s_y[(slot0 + t) * kRows + col] = A::from_f32(o[0][v]);
+              } else if constexpr (DUAL) {
                 // reference rounding points: gate and up outputs are act
                 // tensors, silu's ops each round (silu_act), and silu(gate) *
                 // up rounds once more (its float32 product is exact)
@@ -566,6 +611,27 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
     __syncthreads();
     cb += n;
   }
+
+  if constexpr (TILE) {
+    // y[t][16 b + c] = rnd(sum over slots j in order of rnd(down * score)),
+    // combine_kernel's arithmetic (the last phase's barrier has passed)
+    const int k = a.c_k, T = (int)a.act_rows / k;
+    for (int i = tid; i < T * kRows; i += 64 * kW) {
+      const int t = i / kRows, c = i - t * kRows;
+      const int row = (int)blockIdx.x * kRows + c;
+      float acc = 0.f;
+      for (int j = 0; j < k; ++j) {
+        const int p = t * k + j;
+        const float s = A::to_f32(s_csc[p]);
+        // (a slot outside the batch, from sorted pairs that are not a
+        // permutation, reads slot 0 rather than past the array)
+        const int sl = s_inv[p];
+        const int slc = (unsigned)sl < (unsigned)a.act_rows ? sl : 0;
+        acc += round_act<DT>(A::to_f32(s_y[slc * kRows + c]) * s);
+      }
+      if (row < R) a.c_y[(int64_t)t * a.out_ld + row] = A::from_f32(acc);
+    }
+  }
 }
 
 }  // namespace
@@ -591,24 +657,25 @@ bool use_static(const GroupedArgs &a) {
   return a.act_rows * a.a_div >= 2 * (int64_t)a.E;
 }
 
-template <int DT, bool DUAL, int NS, bool FUSED, bool STATIC>
+template <int DT, bool DUAL, int NS, bool FUSED, bool STATIC, bool TILE = false>
 hipError_t launch_v3(const GroupedArgs &a, hipStream_t st) {
-  const int RU = DUAL ? kRows : 2 * kRows;
+  const int RU = DUAL || TILE ? kRows : 2 * kRows;
   const int RT = (a.R + RU - 1) / RU;
   // more than 64 KB of dynamic LDS (once per device; a failure here shows up
   // as a failed launch below)
   static bool attr_set[64] = {false};
   int dev = 0;
   if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !attr_set[dev]) {
-    (void)hipFuncSetAttribute((const void *)&gemv3_kernel<DT, DUAL, NS, FUSED, STATIC>,
+    (void)hipFuncSetAttribute((const void *)&gemv3_kernel<DT, DUAL, NS, FUSED, STATIC, TILE>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, kActLds);
     attr_set[dev] = true;
   }
   // STATIC: SPE blocks per expert, about one block per compute unit in all
   // (and at least one tile a block)
+  // TILE: one block per 16-row tile
   const int spe = STATIC ? std::max(1, std::min(cu_count() / a.E, RT)) : 1;
-  const int grid = STATIC ? a.E * spe : cu_count();
-  hipLaunchKernelGGL((gemv3_kernel<DT, DUAL, NS, FUSED, STATIC>), dim3(grid), dim3(64 * kW),
+  const int grid = TILE ? RT : STATIC ? a.E * spe : cu_count();
+  hipLaunchKernelGGL((gemv3_kernel<DT, DUAL, NS, FUSED, STATIC, TILE>), dim3(grid), dim3(64 * kW),
                      kActLds, st, a, RT, spe);
   return hipGetLastError();
 }
@@ -643,6 +710,29 @@ hipError_t launch_gemv3(int dtype, bool dual, const GroupedArgs &a, hipStream_t 
   if (dtype == DT_BF16)
     return dual ? launch_v3_ns<DT_BF16, true>(a, st) : launch_v3_ns<DT_BF16, false>(a, st);
   return dual ? launch_v3_ns<DT_F16, true>(a, st) : launch_v3_ns<DT_F16, false>(a, st);
+}
+
+bool gemv3_down_combine_supports(int K, int R, int E, int gs, int64_t pairs, int k) {
+  return gemv3_supports(K, R, E, gs) && k >= 1 && pairs >= 1 && pairs <= kTilePairs &&
+         pairs % k == 0;
+}
+
+hipError_t launch_gemv3_down_combine(int dtype, const GroupedArgs &a, hipStream_t st) {
+  if (!gemv3_down_combine_supports(a.K, a.R, a.E, a.gs, a.act_rows, a.c_k) || !a.offsets ||
+      !a.o_map || !a.c_scores || !a.c_y || a.route_part)
+    return hipErrorInvalidValue;
+  auto go = [&](auto dt) -> hipError_t {
+    constexpr int D = decltype(dt)::value;
+    switch (a.K / 256) {
+      case 3: return launch_v3<D, false, 3, false, false, true>(a, st);
+      case 6: return launch_v3<D, false, 6, false, false, true>(a, st);
+      case 8: return launch_v3<D, false, 8, false, false, true>(a, st);
+      case 16: return launch_v3<D, false, 16, false, false, true>(a, st);
+      default: return hipErrorInvalidValue;
+    }
+  };
+  return dtype == DT_BF16 ? go(std::integral_constant<int, DT_BF16>{})
+                          : go(std::integral_constant<int, DT_F16>{});
 }
 
 }  // namespace nvm

@@ -57,12 +57,26 @@ struct GroupedArgs {
   // the shifts of the h it stores into out_sh [rows, R / 64] (may be NULL).
   const uint8_t *act_sh;
   uint8_t *out_sh;
+  // Down product with the combine in its epilogue (launch_gemv3_down_combine,
+  // act_rows = T * c_k pairs in sorted order, o_map = sorted): the scores
+  // [pairs] (act bits, pair order) and y [T, out_ld] it writes.
+  const uint16_t *c_scores;
+  uint16_t *c_y;
+  int c_k;
 };
 
 // Decode batches whose routing the gate/up product can finalise: at most
 // kFusedPairs pairs, E <= 128 experts, top-k <= 16.
 constexpr int kFusedPairs = 1024;
 bool fused_route_supports(int64_t T, int64_t E, int k);
+
+// Decode down product with the combine in its epilogue (gemv3.hip): one
+// block per 16 rows of y, each over every pair of the batch (at most
+// kTilePairs), y bit-identical to the down product followed by
+// launch_combine.
+constexpr int kTilePairs = 256;
+bool gemv3_down_combine_supports(int K, int R, int E, int gs, int64_t pairs, int k);
+hipError_t launch_gemv3_down_combine(int dtype, const GroupedArgs &a, hipStream_t st);
 
 // Router.  Partial float64 logits over hidden splits, then per-token finalise.
 // With final_act the logits are rounded and stored as act [T, E] directly.

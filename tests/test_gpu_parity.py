@@ -449,6 +449,33 @@ def test_moe_decode_routing_ties(T, act):
                 assert ids3[t, j] < ids3[t, j + 1], f"token {t}: tie inside group {g[j]} misordered"
 
 
+@pytest.mark.parametrize("T,H,I,act", [(1, 2048, 768, "bfloat16"), (3, 2048, 768, "bfloat16"),
+                                       (8, 2048, 768, "float16"), (16, 2048, 768, "bfloat16"),
+                                       (32, 2048, 768, "bfloat16"), (1, 4096, 1536, "bfloat16"),
+                                       (8, 4096, 1536, "bfloat16")])
+def test_moe_decode_down_combine_is_bit_identical(T, H, I, act, monkeypatch):
+    """The down product with the combine in its epilogue (one block per 16
+    columns of y over every pair) against the down product followed by the
+    combine launch: the same y bits, routing and scores, forced both ways
+    (NVM_DOWN_COMBINE) at batch sizes up to its 256-pair limit, both dtypes
+    and the 235B shape; the fused output also checked against the oracle."""
+    x, w = _moe_case(900 + T + H, T, H, 128, I, act)
+    moe = make_moe(w, act, 64, 8, True, DEV)
+    moe.regime = "decode"
+    xs = to_act(x, act, DEV)
+    outs = []
+    for fused in ("0", "1"):
+        monkeypatch.setenv("NVM_DOWN_COMBINE", fused)
+        y, ids, sc = moe.forward(xs, return_routing=True)
+        torch.cuda.synchronize()
+        outs.append((y.clone(), ids.clone(), sc.clone()))
+    print(f"down+combine T={T} H={H} {act}", flush=True)
+    for a, b, what in zip(outs[0], outs[1], ("y", "ids", "scores")):
+        assert torch.equal(a, b), f"{what}: fused down+combine differs from down then combine"
+    y_ref, _, _ = O.moe_forward(x, w, 8, True, act, 64)
+    assert_moe_close(to_np(outs[1][0]), y_ref, act, "moe down+combine")
+
+
 def test_moe_235b_decode():
     """H4096 I1536: gate/up through the eight-group slice GEMV (KS 8), down
     through six-group slices in four k-slices."""
