@@ -11,8 +11,10 @@
 // Decode kernel (L = 1, f16/bf16 pages, D = 64 or 128).  A block owns one
 // (request, kv head, group of up to RP query heads, context split): the query
 // heads that share a kv head read each key and value row once (grouped-query
-// sharing; the reference reads them once per query head).  Its four
-// wavefronts take 64-position tiles of the split in turn.
+// sharing; the reference reads them once per query head).  Its eight
+// wavefronts take 64-position tiles of the split in turn, each with its
+// tile's keys and values in registers (one memory round trip a tile; eight
+// wavefronts keep twice the tiles in flight that four did).
 //   * Scores on the matrix cores, S^T = K . Q^T with v_mfma_f32_16x16x32 in
 //     the page dtype: the key rows are the A operand straight from memory
 //     (lane (c, G) loads 16 bytes: position c of a 16-row subtile, dims
@@ -27,7 +29,7 @@
 //     (its head's probabilities at the chunk's k-slots), split into three
 //     page-dtype parts like q; the value rows (16-byte loads issued with the
 //     key loads) are staged in LDS and read back transposed as the A operand.
-//   * The four wavefronts' (max, sum, output) partials meet in LDS; with more
+//   * The wavefronts' (max, sum, output) partials meet in LDS; with more
 //     than one split per row they go to the workspace and a second launch
 //     combines them.
 // Other shapes (L > 1, f32 or int8 pages, other head dims) run one wavefront
@@ -47,6 +49,7 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kTile = 64;           // context positions per wavefront step
 constexpr int kTargetBlocks = 256;  // decode: split the context until about this many blocks
+constexpr int kDecodeWaves = 8;     // decode: wavefronts per block (tiles in flight per block)
 constexpr int kMaxRowDim = 256;     // head dim of the row kernel (4 values per lane)
 constexpr int kMaxSplits = 64;      // context splits of a decode row
 
@@ -101,8 +104,8 @@ __device__ __forceinline__ void split3(const float (&x)[8], u32x4 &p0, u32x4 &p1
   }
 }
 
-template <int DT, int DH, int RP>
-__global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
+template <int DT, int DH, int RP, int NW>
+__global__ __launch_bounds__(64 * NW) void paged_decode_kernel(PagedArgs a) {
   using A = Act<DT>;
   constexpr int NC = DH / 32;        // 32-dim chunks of a score MFMA
   constexpr int NT = DH / 16;        // 16-dim output tiles of a P.V MFMA
@@ -112,13 +115,13 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
   constexpr int VP = DH + 8;         // LDS pitch of a staged value row (16-bit elements)
   // one 32-position chunk of values per wavefront during the tile loop; the
   // wavefronts' output partials afterwards (the same LDS)
-  constexpr int kVBytes = 4 * 32 * VP * 2, kOBytes = 4 * RP * DH * 4;
+  constexpr int kVBytes = NW * 32 * VP * 2, kOBytes = NW * RP * DH * 4;
   __shared__ __attribute__((aligned(16))) char s_buf[kVBytes > kOBytes ? kVBytes : kOBytes];
   auto s_v = reinterpret_cast<uint16_t(*)[32][VP]>(s_buf);
   auto s_o = reinterpret_cast<float(*)[RP][DH]>(s_buf);
   __shared__ u32x4 s_q[NC][3][64];  // the score MFMAs' B operand, per lane
-  __shared__ int s_row[4][kTile];
-  __shared__ float s_m[4][RP], s_l[4][RP];
+  __shared__ int s_row[NW][kTile];
+  __shared__ float s_m[NW][RP], s_l[NW][RP];
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int c16 = lane & 15, G = lane >> 4;
@@ -177,7 +180,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
   };
   int pg_next[4];
   page_ids(p0 + kTile * wv, pg_next);
-  for (int t0 = p0 + kTile * wv; t0 < p1; t0 += 4 * kTile) {
+  for (int t0 = p0 + kTile * wv; t0 < p1; t0 += NW * kTile) {
     // element offsets of the key/value rows of positions t0 + 16u + c16
     int rowoff[4];
 #pragma unroll
@@ -188,7 +191,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
                       ? ((pg * a.Hkv + kvh) * a.page_size + pos % a.page_size) * DH
                       : -1;
     }
-    page_ids(t0 + 4 * kTile, pg_next);
+    page_ids(t0 + NW * kTile, pg_next);
     u32x4 kop[4][NC];
 #pragma unroll
     for (int u = 0; u < 4; ++u)
@@ -300,15 +303,15 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(PagedArgs a) {
   }
   __syncthreads();
 
-  for (int e = threadIdx.x; e < RP * DH; e += 256) {
+  for (int e = threadIdx.x; e < RP * DH; e += 64 * NW) {
     const int r = e / DH, d = e % DH;
     if (r >= nh) continue;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_m[w][r]);
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][r]);
     float Ls = 0.f, Os = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float mw = s_m[w][r];
       if (mw != -INFINITY) {
         const float f = exp2f(mw - M);
@@ -465,7 +468,6 @@ AttnPlan attn_plan(int64_t N, int64_t L, int64_t D, int64_t max_pages, int64_t p
   const int64_t base = N / Hq * Hkv * p.HG;
   const int64_t s0 = std::max<int64_t>(1, (kTargetBlocks + base - 1) / base);
   int64_t tps = std::max<int64_t>(1, (tiles + s0 - 1) / s0);
-  if (tps >= 4) tps = (tps + 3) / 4 * 4;  // whole rounds of the four wavefronts
   tps = std::max<int64_t>(tps, (tiles + kMaxSplits - 1) / kMaxSplits);
   p.S = (int)std::max<int64_t>(1, (tiles + tps - 1) / tps);
   p.span = (int)(tps * kTile);
@@ -482,14 +484,18 @@ template <int DT>
 void launch_decode(const PagedArgs &a, int RP, int D, unsigned grid, hipStream_t st) {
   if (D == 128) {
     if (RP == 8)
-      hipLaunchKernelGGL((paged_decode_kernel<DT, 128, 8>), dim3(grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((paged_decode_kernel<DT, 128, 8, kDecodeWaves>), dim3(grid),
+                         dim3(64 * kDecodeWaves), 0, st, a);
     else
-      hipLaunchKernelGGL((paged_decode_kernel<DT, 128, 16>), dim3(grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((paged_decode_kernel<DT, 128, 16, kDecodeWaves>), dim3(grid),
+                         dim3(64 * kDecodeWaves), 0, st, a);
   } else {
     if (RP == 8)
-      hipLaunchKernelGGL((paged_decode_kernel<DT, 64, 8>), dim3(grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((paged_decode_kernel<DT, 64, 8, kDecodeWaves>), dim3(grid),
+                         dim3(64 * kDecodeWaves), 0, st, a);
     else
-      hipLaunchKernelGGL((paged_decode_kernel<DT, 64, 16>), dim3(grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((paged_decode_kernel<DT, 64, 16, kDecodeWaves>), dim3(grid),
+                         dim3(64 * kDecodeWaves), 0, st, a);
   }
 }
 
