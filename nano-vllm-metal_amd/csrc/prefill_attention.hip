@@ -247,9 +247,6 @@ __global__ __launch_bounds__(64 * kCW) void causal_prefill_kernel(CausalArgs a) 
         for (int ct = 0; ct < CT; ++ct) acc[ct][u] = A::mfma16(kop, qop[ct][kk], acc[ct][u]);
       }
     }
-    // causal mask (key j <= position, j < L) unless every key of the tile is
-    // visible to every column of the wavefront (uniform), base-2 scores,
-    // online softmax
     // Causal mask (key j <= position, j < L), base-2 scores, online softmax.
     // Interior tiles (every key of the tile visible to every column of the
     // wavefront, all columns real: uniform) take a path without the mask and
