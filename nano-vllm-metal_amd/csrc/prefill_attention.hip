@@ -105,6 +105,13 @@ __device__ __forceinline__ void split3c(const float (&x)[8], u32x4 &p0, u32x4 &p
   }
 }
 
+// Column of key pair kp in row r of the transposed values in LDS: rows in
+// groups of 16 XOR the column with a multiple of 4, so that the staging
+// stores (16 lanes on 16 rows 8 apart, one key pair) fall on 16 banks, not
+// 2; the P.V reads (16 lanes on one group's 16 rows) keep their pattern,
+// and a key pair's two dwords stay adjacent.
+__device__ __forceinline__ int vt_col(int r, int kp) { return kp ^ (4 * ((r >> 4) & 7)); }
+
 template <int DT, int DH, int R, int CT>
 __global__ __launch_bounds__(64 * kCW) void causal_prefill_kernel(CausalArgs a) {
   using A = Act<DT>;
@@ -209,7 +216,7 @@ __global__ __launch_bounds__(64 * kCW) void causal_prefill_kernel(CausalArgs a) 
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
         const float lo = vreg[i][d >> 2][d & 3], hi = vreg[i][2 + (d >> 2)][d & 3];
-        s_vt[buf][8 * dg + d][kp2] = A::pack2(lo, hi);
+        s_vt[buf][8 * dg + d][vt_col(8 * dg + d, kp2)] = A::pack2(lo, hi);
       }
     }
   };
@@ -320,8 +327,8 @@ __global__ __launch_bounds__(64 * kCW) void causal_prefill_kernel(CausalArgs a) 
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const uint32_t *row = s_vt[buf][16 * t + c16];
-        const u32x2 lo = *(const u32x2 *)&row[kp0];
-        const u32x2 hi = *(const u32x2 *)&row[kp1];
+        const u32x2 lo = *(const u32x2 *)&row[vt_col(16 * t, kp0)];
+        const u32x2 hi = *(const u32x2 *)&row[vt_col(16 * t, kp1)];
         const u32x4 va{lo.x, lo.y, hi.x, hi.y};
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct)
