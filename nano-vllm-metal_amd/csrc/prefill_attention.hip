@@ -105,12 +105,18 @@ __device__ __forceinline__ void split3c(const float (&x)[8], u32x4 &p0, u32x4 &p
   }
 }
 
-// Column of key pair kp in row r of the transposed values in LDS: rows in
-// groups of 16 XOR the column with a multiple of 4, so that the staging
-// stores (16 lanes on 16 rows 8 apart, one key pair) fall on 16 banks, not
-// 2; the P.V reads (16 lanes on one group's 16 rows) keep their pattern,
-// and a key pair's two dwords stay adjacent.
-__device__ __forceinline__ int vt_col(int r, int kp) { return kp ^ (4 * ((r >> 4) & 7)); }
+// Column of key pair kp in row r of the transposed values in LDS.  A lane's
+// P.V operand is key pairs kp0 = 16 kc + 2 G, kp0 + 1, kp0 + 8, kp0 + 9:
+// they sit in columns 16 kc + 4 G .. + 3, one 16-byte read (the two 8-byte
+// reads it replaces collided on banks).  Rows in groups of 16 XOR the column
+// with vt_swz of the group (bits 1, 3 and 4), which spreads the staging
+// stores (16 lanes on 16 rows 8 apart, one key pair) over 8 columns instead
+// of 1; bit 1 swaps the two pairs inside a read, which the read undoes.
+__device__ __forceinline__ constexpr int vt_swz(int g) { return ((g & 1) << 1) | ((g & 6) << 2); }
+__device__ __forceinline__ int vt_col(int r, int kp) {
+  const int pc = (kp & 16) | (((kp >> 1) & 3) << 2) | (((kp >> 3) & 1) << 1) | (kp & 1);
+  return pc ^ vt_swz((r >> 4) & 7);
+}
 
 template <int DT, int DH, int R, int CT>
 __global__ __launch_bounds__(64 * kCW) void causal_prefill_kernel(CausalArgs a) {
@@ -120,8 +126,12 @@ __global__ __launch_bounds__(64 * kCW) void causal_prefill_kernel(CausalArgs a) 
   constexpr int PPC = 16 / R;       // query positions per column tile
   constexpr int PPW = CT * PPC;     // query positions per wavefront
   constexpr int QB = kCW * PPW;     // query positions per block
-  constexpr int KP = DH + 8;        // LDS pitch of a key row (16-bit elements)
-  constexpr int VP = kKT / 2 + 4;   // LDS pitch of a transposed value row (dwords)
+  // LDS pitches (the LDS serves a 16-byte access 32 lanes at a time over
+  // 128 banks): key rows of DH + 16 elements (72 or 40 dwords) and value
+  // rows of 40 dwords put the 32 lanes of a score or P.V read on distinct
+  // banks (pitches of 68 or 36 dwords collide on one bank pair)
+  constexpr int KP = DH + 16;       // LDS pitch of a key row (16-bit elements)
+  constexpr int VP = kKT / 2 + 8;   // LDS pitch of a transposed value row (dwords)
   constexpr int DG = DH / 8;        // 8-dim groups of a row
   // staging items of a tile: keys (key, 8 dims), values (key pair, 8 dims),
   // and per thread
@@ -322,14 +332,14 @@ __global__ __launch_bounds__(64 * kCW) void causal_prefill_kernel(CausalArgs a) 
                             pv[ct][2 * kc + 1][2], pv[ct][2 * kc + 1][3]};
         split3c<DT>(x, pb[ct][0], pb[ct][1], pb[ct][2]);
       }
-      // key pairs (4G, 4G+1), (4G+2, 4G+3) and the same + 16 of the chunk
-      const int kp0 = 16 * kc + 2 * G, kp1 = 16 * kc + 8 + 2 * G;
+      // key pairs 2G, 2G + 1 and 2G + 8, 2G + 9 of the chunk (keys 4G .. 4G + 3 and
+      // the same + 16): the 16 bytes at vt_col
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const uint32_t *row = s_vt[buf][16 * t + c16];
-        const u32x2 lo = *(const u32x2 *)&row[vt_col(16 * t, kp0)];
-        const u32x2 hi = *(const u32x2 *)&row[vt_col(16 * t, kp1)];
-        const u32x4 va{lo.x, lo.y, hi.x, hi.y};
+        const int sw = vt_swz(t & 7);
+        u32x4 va = *(const u32x4 *)&row[(16 * kc + 4 * G) ^ (sw & ~3)];
+        if (sw & 2) va = u32x4{va[2], va[3], va[0], va[1]};  // (t unrolled: no branch)
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
