@@ -872,6 +872,9 @@ COPY_PROBE_BYTES = 256 << 20
 KERNEL_KEYS = (
     ("decode_gateup_fused", r"gemv3_kernel<1, true, \d+, true,"),
     ("decode_gateup", r"gemv3_kernel<1, true, \d+, false,|gemv_kernel<1, true"),
+    # the down product with the combine in its epilogue (decode batches of at
+    # most 16 pairs)
+    ("decode_down_combine", r"gemv3_kernel<1, false, \d+, false, false, true>"),
     ("decode_down", r"gemv3_kernel<1, false|gemv_kernel<1, false"),
     # prefill GEMMs of the forward (activations converted to fp16 once, by
     # act_to_f16) and of the stage entry points (converting their own rows)
@@ -889,6 +892,11 @@ KERNEL_KEYS = (
     ("dispatch_scatter", r"dispatch_scatter_kernel"),
     ("dispatch", r"dispatch_kernel"),
     ("combine", r"combine_kernel<1"),
+    # attention (the model port)
+    ("attn_causal_prefill", r"causal_prefill_kernel<"),
+    ("attn_paged_prefill", r"paged_prefill_kernel<"),
+    ("attn_paged_decode", r"paged_decode_kernel<"),
+    ("attn_paged_combine", r"paged_combine_kernel"),
 )
 
 
