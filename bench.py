@@ -225,14 +225,29 @@ class ForwardStages:
             L.dtype_code(x.dtype), *flat, self.y.data_ptr(), None, None,
             L.REGIME_AUTO, self.ws.data_ptr(), self.ws.numel(), L.stream_of(self.dev)))
 
-    def run(self, x, upto=4):
-        """Stages 0 .. upto-1."""
-        for s in range(upto):
+    def run(self, x, upto=4, seq=None):
+        """Stages 0 .. upto-1, or the stages of `seq` in order."""
+        for s in (range(upto) if seq is None else seq):
             self.launch(s, x)
         return self.y
 
 
-def forward_stage_us(layers, xs, stage, n=64):
+def forward_plan(moe, T, regime=0):
+    """1 when nvm_moe_forward runs both products of this batch as one launch
+    (stage 4 of nvm_moe_forward_stage), else 0."""
+    from nano_vllm_metal_amd import _lib
+
+    lib = _lib.load()
+    E = moe.w_router.weight.shape[0]
+    H = moe.w_router.weight.shape[1] * 8
+    I = moe.w_gate.weight.shape[1]
+    out = ctypes.c_int(0)
+    _lib.check(lib.nvm_moe_forward_plan(T, H, I, E, moe.num_experts_per_tok,
+                                        moe.w_gate.group_size, regime, ctypes.byref(out)))
+    return out.value
+
+
+def forward_stage_us(layers, xs, stage, n=64, before=None):
     """Duration (us) of one stage of the layer's own launch sequence: a HIP
     graph of `n` back-to-back launches of that stage (weight sets cycled, each
     set's earlier stages run beforehand), timed with HIP events on the stream
@@ -245,7 +260,7 @@ def forward_stage_us(layers, xs, stage, n=64):
     # (each set's stages before this one: a later stage may overwrite what
     # this one reads, as the down product overwrites the fp16 copy of x)
     for i, f in enumerate(fs):
-        f.run(xs[i % len(xs)], upto=stage)
+        f.run(xs[i % len(xs)], upto=stage, seq=before)
     torch.cuda.synchronize()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -269,29 +284,31 @@ def forward_stage_us(layers, xs, stage, n=64):
     return e0.elapsed_time(e1) * 1e3 / n
 
 
-def in_layer_stage_us(layers, xs, stage, n=64):
+def in_layer_stage_us(layers, xs, stage, n=64, seq=None):
     """Duration (us) of one stage where the layer runs it, after its own
     earlier stages (their outputs just written, as in the layer): a HIP graph
     of `n` runs of stages 0..stage minus a graph of `n` runs of stages
-    0..stage-1, over the same weight sets, timed with HIP events on the
-    stream the graphs' kernels run on."""
+    0..stage-1 (with `seq`: of the stages seq[:stage + 1] minus seq[:stage]),
+    over the same weight sets, timed with HIP events on the stream the
+    graphs' kernels run on."""
     import torch
 
     T = xs[0].shape[0]
     fs = [ForwardStages(m, T, layers[0].w_gate.weight.device) for m in layers]
 
     def graph_us(upto):
+        sq = None if seq is None else seq[:upto]
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             for i, f in enumerate(fs):
-                f.run(xs[i % len(xs)], upto=upto)
+                f.run(xs[i % len(xs)], upto=upto, seq=sq)
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for i in range(n):
-                fs[i % len(fs)].run(xs[i % len(fs) % len(xs)], upto=upto)
+                fs[i % len(fs)].run(xs[i % len(fs) % len(xs)], upto=upto, seq=sq)
         g.replay()
         torch.cuda.synchronize()
         best = None
@@ -469,10 +486,16 @@ def decode_bench(layers, T, steps, warmup, dev, use_graph=True, shape=None, n_me
     del stages
     fwd_kernel_us = {n: forward_stage_us(layers, xs, i) for i, n in enumerate(STAGE_NAMES)}
     in_layer_us = {n: in_layer_stage_us(layers, xs, i) for i, n in ((1, "gateup"), (2, "down"))}
+    # both products as the layer launches them (stage 4: one launch where the
+    # forward fuses them)
+    fused_products = forward_plan(layers[0], T)
+    in_layer_us["products"] = in_layer_stage_us(layers, xs, 1, seq=[0, 4])
+    fwd_kernel_us["products"] = forward_stage_us(layers, xs, 4, before=[0])
     gu_b, dn_b = bytes_per_expert(H, I, gs)
     avg_touched = sum(touched) / len(touched)
     layer_bytes = avg_touched * (gu_b + dn_b) + router_bytes(H, E, gs) + 2 * T * H * 2
     gateup_bytes = avg_touched * gu_b + T * H * 2
+    products_bytes = avg_touched * (gu_b + dn_b) + T * H * 2
     return {
         "tokens": T,
         "tokens_per_s": T / (layer_us * 1e-6),
@@ -495,11 +518,17 @@ def decode_bench(layers, T, steps, warmup, dev, use_graph=True, shape=None, n_me
         "in_layer_kernel_us": in_layer_us,
         "in_layer_kernel_us_note": "the stage where the layer runs it, after its own earlier "
                                    "stages: a HIP graph of 64 runs of stages 0..s minus one of "
-                                   "stages 0..s-1 (nvm_moe_forward_stage), timed with events",
+                                   "stages 0..s-1 (nvm_moe_forward_stage), timed with events; "
+                                   "products = both products as the layer launches them "
+                                   "(stages 0, 4 minus stage 0)",
+        "fused_products": bool(fused_products),
         "touched_experts_avg": avg_touched,
         "layer_algorithmic_bytes": layer_bytes,
         "hbm_gbs": layer_bytes / (layer_us * 1e-6) / 1e9,
         "gateup_algorithmic_bytes": gateup_bytes,
+        "products_algorithmic_bytes": products_bytes,
+        "in_layer_products_gbs": products_bytes / (in_layer_us["products"] * 1e-6) / 1e9,
+        "forward_products_gbs": products_bytes / (fwd_kernel_us["products"] * 1e-6) / 1e9,
         "gateup_gbs": gateup_bytes / (graph_kernel_us["gateup"] * 1e-6) / 1e9,
         "forward_gateup_gbs": gateup_bytes / (fwd_kernel_us["gateup"] * 1e-6) / 1e9,
         "in_layer_gateup_gbs": gateup_bytes / (in_layer_us["gateup"] * 1e-6) / 1e9,
@@ -870,6 +899,10 @@ COPY_PROBE_BYTES = 256 << 20
 # finalises the routing in its prologue (inside nvm_moe_forward);
 # decode_gateup is the product alone (nvm_moe_expert_gateup).
 KERNEL_KEYS = (
+    # both decode products in one launch (expert-major blocks, each over one
+    # half of the down reduction): the layer's products launch from two
+    # routed rows per expert on average
+    ("decode_products", r"gemv3_kernel<1, true, \d+, true, true, false, [1-9]"),
     ("decode_gateup_fused", r"gemv3_kernel<1, true, \d+, true,"),
     ("decode_gateup", r"gemv3_kernel<1, true, \d+, false,|gemv_kernel<1, true"),
     # the down product with the combine in its epilogue (decode batches of at
@@ -973,6 +1006,7 @@ def rocprof_summary(root: Path, write_traffic: bool) -> str:
     # the layer's own launch of a product: the dispatch that directly follows
     # the layer's previous stage (gate/up after the routing, down after gate/up)
     in_layer = {"decode_gateup_fused": ("route_partial",),
+                "decode_products": ("route_partial",),
                 "prefill_gateup": ("dispatch_hist",),
                 "decode_down": ("decode_gateup_fused",),
                 "prefill_down": ("prefill_gateup",)}
@@ -1173,7 +1207,24 @@ def main():
         f"{head['hbm_gbs']:.0f} GB/s, kernels {head['kernel_us']}")
 
     gu_b, _ = bytes_per_expert(H, I, gs)
-    achieved = head["in_layer_gateup_gbs"]
+    fused = head["fused_products"]
+    # the dominant kernel of the layer: both products in one launch where the
+    # forward fuses them (B = 32 at this shape), else the gate/up product
+    achieved = head["in_layer_products_gbs"] if fused else head["in_layer_gateup_gbs"]
+    gateup_alone = {
+        "kernel": "gemv3_kernel<bf16, gate/up+SwiGLU, routing finalised in the prologue, "
+                  "K=2048> (nvm_moe_forward_stage 1)",
+        "avg_launch_us": head["in_layer_kernel_us"]["gateup"],
+        "algorithmic_bytes_per_launch": head["gateup_algorithmic_bytes"],
+        "achieved": head["in_layer_gateup_gbs"],
+        "frac": head["in_layer_gateup_gbs"] / HBM_PEAK_GBS,
+        "traffic": read_traffic("decode_gateup_fused"),
+        "back_to_back": {"avg_launch_us": head["forward_kernel_us"]["gateup"],
+                         "achieved": head["forward_gateup_gbs"],
+                         "frac": head["forward_gateup_gbs"] / HBM_PEAK_GBS},
+        **rocprof_check("decode_gateup_fused", head["gateup_algorithmic_bytes"],
+                        head["in_layer_gateup_gbs"], HBM_PEAK_GBS),
+    }
     out = {
         "metric": METRIC,
         "value": head["tokens_per_s"],
@@ -1201,27 +1252,38 @@ def main():
                             "hbm_gbs": head["layer_algorithmic_bytes"]
                             / (head["layer_us_median"] * 1e-6) / 1e9
                             if head["layer_us_median"] else None},
-        "roofline": {
-            "kernel": "gemv3_kernel<bf16, gate/up+SwiGLU, routing finalised in the prologue, "
-                      "K=2048> (the layer's gate/up launch, nvm_moe_forward_stage 1)",
+        "roofline": ({
+            "kernel": "gemv3_kernel<bf16, gate/up+SwiGLU then down over one half of its "
+                      "reduction, routing finalised in the prologue, K=2048> (the layer's "
+                      "products launch, nvm_moe_forward_stage 4)",
             "bound": "hbm",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": read_traffic("decode_gateup_fused"),
-            "algorithmic_bytes_per_launch": head["gateup_algorithmic_bytes"],
-            "avg_launch_us": head["in_layer_kernel_us"]["gateup"],
+            "traffic": read_traffic("decode_products"),
+            "algorithmic_bytes_per_launch": head["products_algorithmic_bytes"],
+            "avg_launch_us": head["in_layer_kernel_us"]["products"],
+            "timing": "HIP events: a graph of 64 runs of the layer's routing and products "
+                      "stages minus a graph of 64 runs of its routing stage (8 weight sets "
+                      "cycled), per launch",
+            "back_to_back": {"avg_launch_us": head["forward_kernel_us"]["products"],
+                             "achieved": head["forward_products_gbs"],
+                             "frac": head["forward_products_gbs"] / HBM_PEAK_GBS},
+            **rocprof_check("decode_products", head["products_algorithmic_bytes"], achieved,
+                            HBM_PEAK_GBS),
+            # the gate/up product alone as the forward's stage 1 runs it
+            # (the layer's launch at batches that do not fuse the products)
+            "gateup_alone": gateup_alone,
+        } if fused else {
+            **gateup_alone,
+            "bound": "hbm",
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
             "timing": "HIP events: a graph of 64 runs of the layer's routing and gate/up stages "
                       "minus a graph of 64 runs of its routing stage (8 weight sets cycled), "
                       "per launch",
-            # the same launch 64 times back to back (its routing partials
-            # written long before, so read from HBM rather than L2)
-            "back_to_back": {"avg_launch_us": head["forward_kernel_us"]["gateup"],
-                             "achieved": head["forward_gateup_gbs"],
-                             "frac": head["forward_gateup_gbs"] / HBM_PEAK_GBS},
-            **rocprof_check("decode_gateup_fused", head["gateup_algorithmic_bytes"], achieved,
-                            HBM_PEAK_GBS),
+        }) | {
             # the same product without the routing in its prologue (the stage
             # entry point nvm_moe_expert_gateup), beside it
             "stage_entry_point": {

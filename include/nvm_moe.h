@@ -209,6 +209,14 @@ int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, i
  * stage 3 only.  (For decode batches of at most 16 pairs nvm_moe_forward
  * runs stages 2 and 3 as one launch, the down product with the combine in
  * its epilogue; its y is bit-identical to stages 2 and 3 run apart.)
+ *
+ * Stages 4 and 5 are the forward's own grouping where it runs both products
+ * in one launch (nvm_moe_forward_plan): 4 = gate/up and down products as
+ * nvm_moe_forward launches them (one launch where it fuses them, leaving the
+ * down output in the workspace as float32 sums of the two halves of its
+ * reduction; else stages 1 and 2), 5 = the combine that follows stage 4.
+ * Stages 0, 4, 5 in order compute exactly what nvm_moe_forward computes; y
+ * is bit-identical to stages 0..3.
  */
 int nvm_moe_forward_stage(int stage, const void *x, int64_t T, int64_t H, int64_t I, int64_t E,
                           int top_k, int norm_topk_prob, int group_size, int bits, int dtype,
@@ -218,6 +226,19 @@ int nvm_moe_forward_stage(int stage, const void *x, int64_t T, int64_t H, int64_
                           const uint32_t *wd, const void *sd, const void *bd,
                           void *y, int32_t *ids_out, void *scores_out, int regime,
                           void *workspace, size_t workspace_bytes, nvm_stream_t stream);
+
+/*
+ * Which launches nvm_moe_forward makes for these arguments (no device work):
+ * *fused_products = 1 when it runs the gate/up and down products of a decode
+ * batch as one launch (expert-major blocks, two per expert, each over one
+ * half of the down reduction; the combine then adds the halves), else 0.  The
+ * choice depends on the shapes, T, top_k, regime and the NVM_FUSED_DOWN /
+ * NVM_GEMV_STATIC environment overrides; y is bit-identical either way.  No
+ * counterpart in the reference: for callers that time or profile the block's
+ * kernels (stages 4 and 5 of nvm_moe_forward_stage).
+ */
+int nvm_moe_forward_plan(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, int group_size,
+                         int regime, int *fused_products);
 
 /*
  * nvm_moe_forward without a workspace argument, for callers that cannot

@@ -122,6 +122,11 @@ struct MoeWs {
   unsigned *done;
   uint16_t *h, *down;
   uint8_t *xsh, *hsh;  // group shifts of the prefill GEMMs' fp16 copies of x and h
+  // the float32 half sums of the down reduction [2][T*k][H] (decode batches
+  // of at most 64 tokens), and whether the products left the down output
+  // there (launch_gemv3_fused_down) instead of in `down`
+  float *dpart;
+  bool split;
   size_t bytes;
 };
 
@@ -142,6 +147,10 @@ MoeWs carve_moe(void *base, int64_t T, int64_t H, int64_t I, int64_t E, int k) {
   w.down = c.take<uint16_t>((size_t)N * H);
   w.xsh = c.take<uint8_t>((size_t)T * (H / 64));
   w.hsh = c.take<uint8_t>((size_t)N * (I / 64));
+  // (forward_fuses_products needs them; T <= 64)
+  w.dpart = T <= 64 && nvm::fused_route_supports(T, E, k) ? c.take<float>((size_t)2 * N * H)
+                                                          : nullptr;
+  w.split = false;
   w.bytes = c.bytes();
   return w;
 }
@@ -306,9 +315,36 @@ int run_down_combine(int dtype, const MoeWs &ws, const uint16_t *scores, int64_t
   return NVM_OK;
 }
 
+// The decode gate/up and down products in one launch (expert-major blocks,
+// two per expert, each over one half of the down reduction): taken where
+// the expert-major products would be (at least two routed rows per expert
+// on average) at the shapes it supports.  y is bit-identical either way, so
+// the choice keeps every token's output independent of its batch.
+// NVM_FUSED_DOWN=0/1 overrides the choice (within the shapes it supports);
+// NVM_GEMV_STATIC=0 turns it off with the other expert-major products.
+bool use_fused_down(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, int group_size) {
+  if (!nvm::gemv3_fused_down_supports((int)H, (int)I, (int)H, (int)E, group_size, T, top_k))
+    return false;
+  const char *v = getenv("NVM_FUSED_DOWN");
+  if (v && (v[0] == '0' || v[0] == '1')) return v[0] == '1';
+  const char *st = getenv("NVM_GEMV_STATIC");
+  if (st && st[0] == '0') return false;
+  return T * top_k >= 2 * E;
+}
+
+// nvm_moe_forward runs the decode products as one launch (the decode branch
+// of moe_stages with the half sums carved in the workspace).
+bool forward_fuses_products(int64_t T, int64_t H, int64_t I, int64_t E, int top_k,
+                            int group_size, int regime) {
+  return T > 0 && T <= 64 && nvm::fused_route_supports(T, E, top_k) &&
+         use_decode(regime, T * top_k, E, H) &&
+         use_fused_down(T, H, I, E, top_k, group_size);
+}
+
 // Routing, dispatch and both expert products of the block (everything but
 // the combine), on the caller's workspace; `scores` is where the routing
-// scores went.
+// scores went; with ws.split the down output is left as the float32 half
+// sums ws.dpart (launch_combine_split).
 int moe_stages(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int top_k,
                int norm_topk_prob, int group_size, int bits, int dtype, const uint32_t *wr,
                const void *sr, const void *br, const uint32_t *wg, const void *sg,
@@ -621,6 +657,11 @@ int nvm_moe_forward(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, i
   if (T == 0) return NVM_OK;
   if (fdc) return run_down_combine(dtype, ws, scores, T, H, I, E, top_k, group_size, wd, sd, bd, y,
                                    stream);
+  if (ws.split) {
+    NVM_TRY_HIP(nvm::launch_combine_split(dtype, ws.dpart, scores, T, top_k, H, y,
+                                          (hipStream_t)stream));
+    return NVM_OK;
+  }
   return nvm_moe_combine(ws.down, scores, T, top_k, H, dtype, y, stream);
 }
 
@@ -632,16 +673,32 @@ int nvm_moe_forward_stage(int stage, const void *x, int64_t T, int64_t H, int64_
                           const uint32_t *wd, const void *sd, const void *bd, void *y,
                           int32_t *ids_out, void *scores_out, int regime, void *workspace,
                           size_t workspace_bytes, nvm_stream_t stream) {
-  NVM_REQUIRE(stage >= 0 && stage <= 3, "moe_stage: stage %d outside [0, 3]", stage);
-  NVM_REQUIRE(y || T == 0 || stage < 3, "moe_stage: null pointer");
+  NVM_REQUIRE(stage >= 0 && stage <= 5, "moe_stage: stage %d outside [0, 5]", stage);
+  NVM_REQUIRE(y || T == 0 || (stage != 3 && stage != 5), "moe_stage: null pointer");
   MoeWs ws{};
   uint16_t *scores = nullptr;
+  // stage 4: both products as the forward launches them; 5: its combine
+  const int first = stage == 4 ? 1 : stage == 5 ? 3 : stage;
+  const int last = stage == 4 ? 2 : stage == 5 ? 3 : stage;
   if (int r = moe_stages(x, T, H, I, E, top_k, norm_topk_prob, group_size, bits, dtype, wr, sr,
                          br, wg, sg, bg, wu, su, bu, wd, sd, bd, ids_out, scores_out, regime,
-                         workspace, workspace_bytes, stream, ws, scores, stage, stage))
+                         workspace, workspace_bytes, stream, ws, scores, first, last))
     return r;
-  if (T == 0 || stage < 3) return NVM_OK;
+  if (T == 0 || (stage != 3 && stage != 5)) return NVM_OK;
+  if (stage == 5 && ws.dpart && forward_fuses_products(T, H, I, E, top_k, group_size, regime)) {
+    NVM_TRY_HIP(nvm::launch_combine_split(dtype, ws.dpart, scores, T, top_k, H, y,
+                                          (hipStream_t)stream));
+    return NVM_OK;
+  }
   return nvm_moe_combine(ws.down, scores, T, top_k, H, dtype, y, stream);
+}
+
+int nvm_moe_forward_plan(int64_t T, int64_t H, int64_t I, int64_t E, int top_k, int group_size,
+                         int regime, int *fused_products) {
+  NVM_REQUIRE(fused_products, "moe_forward_plan: null output");
+  NVM_REQUIRE(T >= 0 && H > 0 && I > 0 && E > 0 && top_k > 0, "moe_forward_plan: bad shape");
+  *fused_products = forward_fuses_products(T, H, I, E, top_k, group_size, regime) ? 1 : 0;
+  return NVM_OK;
 }
 
 int nvm_moe_scratch_bytes(size_t *bytes) {
@@ -704,8 +761,9 @@ int nvm_moe_forward_residual_norm(const void *x, int64_t T, int64_t H, int64_t I
                          workspace, workspace_bytes, stream, ws, scores))
     return r;
   if (T == 0) return NVM_OK;
-  NVM_TRY_HIP(nvm::launch_combine_residual_norm(dtype, ws.down, scores, T, top_k, H, h, norm_w,
-                                                eps, h_out, x_out, (hipStream_t)stream));
+  NVM_TRY_HIP(nvm::launch_combine_residual_norm(
+      dtype, ws.split ? (const void *)ws.dpart : (const void *)ws.down, scores, T, top_k, H, h,
+      norm_w, eps, h_out, x_out, (hipStream_t)stream, ws.split));
   return NVM_OK;
 }
 
@@ -777,6 +835,17 @@ int moe_stages(const void *x, int64_t T, int64_t H, int64_t I, int64_t E, int to
       g.r_scores = scores;
       g.r_offsets = ws.offsets;
       g.r_sorted = ws.sorted;
+      if (runs(2) && ws.dpart && forward_fuses_products(T, H, I, E, top_k, group_size, regime)) {
+        // both products in one launch; the combine adds the down halves
+        g.d_w = wd;
+        g.d_s = (const uint16_t *)sd;
+        g.d_b = (const uint16_t *)bd;
+        g.d_part = ws.dpart;
+        g.d_R = (int)H;
+        NVM_TRY_HIP(nvm::launch_gemv3_fused_down(dtype, g, st));
+        ws.split = true;
+        return NVM_OK;
+      }
       if (int r = run_products(dtype, true, true, g, N, st)) return r;
     }
   } else {

@@ -237,6 +237,54 @@ __device__ __forceinline__ void hoist_args(const T &...v) {
 }
 
 __device__ __forceinline__ u32x4 ldg16(const void *p) { return *(const u32x4 *)p; }
+
+// The down outputs of pairs t k + j0 .. t k + j0 + NB - 1 (those below k) at
+// columns 8c .. 8c + 7, as float32 values of the act dtype: from the act
+// tensor down [pairs][H], or (SPLIT) from the float32 sums of the two halves
+// of the down reduction, part [2][TK][H], as rnd(lo + hi) (the down
+// product's own output rounding).  Pairs past k read as zero.
+template <int DT, bool SPLIT, int NB>
+__device__ __forceinline__ void down_vals(const void *down, int64_t TK, int64_t t, int k, int j0,
+                                          int64_t H, int64_t c, float (&dv)[NB][8]) {
+  using A = Act<DT>;
+  if constexpr (SPLIT) {
+    const float *part = (const float *)down;
+    u32x4 lo[NB][2], hi[NB][2];
+#pragma unroll
+    for (int jj = 0; jj < NB; ++jj) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      lo[jj][0] = lo[jj][1] = hi[jj][0] = hi[jj][1] = z;
+      if (j0 + jj < k) {  // uniform
+        const int64_t p = t * k + j0 + jj;
+        lo[jj][0] = ldg16(part + p * H + 8 * c);
+        lo[jj][1] = ldg16(part + p * H + 8 * c + 4);
+        hi[jj][0] = ldg16(part + (TK + p) * H + 8 * c);
+        hi[jj][1] = ldg16(part + (TK + p) * H + 8 * c + 4);
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < NB; ++jj)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        dv[jj][i] = round_act<DT>(__uint_as_float(lo[jj][i >> 2][i & 3]) +
+                                  __uint_as_float(hi[jj][i >> 2][i & 3]));
+  } else {
+    const uint16_t *dn = (const uint16_t *)down;
+    u32x4 v[NB];
+#pragma unroll
+    for (int jj = 0; jj < NB; ++jj) {
+      v[jj] = u32x4{0u, 0u, 0u, 0u};
+      if (j0 + jj < k) v[jj] = ldg16(dn + ((t * k + j0 + jj) * H + 8 * c));  // uniform
+    }
+#pragma unroll
+    for (int jj = 0; jj < NB; ++jj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dv[jj][2 * i] = A::lo(v[jj][i]);
+        dv[jj][2 * i + 1] = A::hi(v[jj][i]);
+      }
+  }
+}
 __device__ __forceinline__ u32x2 ldg8(const void *p) { return *(const u32x2 *)p; }
 
 // Raw buffer loads: a uniform descriptor (base, size in bytes) plus a 32-bit

@@ -53,6 +53,9 @@ constexpr int kActLds = 136 * 1024;
 // offset of a masked row: with the 4 KB of step offsets added it stays below
 // 2^31 and at or beyond the end of every tensor (gemv3_supports)
 constexpr int kMasked = 0x7FFF0000;
+// FDOWN: rows of the h stage (a routed row per token at most: the fused
+// routing's token limit)
+constexpr int kFdRows = 64;
 
 // Bytes per staged routed row: the A operands (2K) and the group sums (K/16),
 // padded to an odd multiple of 16 bytes, so that the 16 rows one lane group
@@ -75,10 +78,73 @@ __device__ __forceinline__ constexpr int a_offset(int s, int h, int st, int G) {
   return (((s * 2 + h) * 4 + st) * 4 + G) * 16;
 }
 
+// Byte offset of column k's 16-bit value inside a staged row: stage_store's
+// placement (group g = k / 64 of half-step g / 2, chunk i = k % 64 / 8 at
+// MFMA step 2 (g % 2) + i % 2 and lane group G_i, each chunk in pair order).
+__device__ __forceinline__ int h_pos(int k) {
+  const int g = k >> 6, i = (k >> 3) & 7, e = k & 7;
+  const int Gi = ((i >> 2) & 1) | (((i >> 1) & 1) << 1);
+  return a_offset(g >> 2, (g >> 1) & 1, 2 * (g & 1) + (i & 1), Gi) + 4 * (e & 3) + 2 * (e >> 2);
+}
+
 // Value j (0..3) of a step's scale or bias window (four 16-bit values).
 __device__ __forceinline__ uint32_t sb_val(const u32x2 &v, int j) {
   const uint32_t d = (j & 2) ? v.y : v.x;
   return (j & 1) ? (d >> 16) : (d & 0xFFFFu);
+}
+
+// One 128-column half-step h (0, 1) of a unit's step: the codes of the
+// NM weight-row tiles (wh: this lane's 16 bytes of each) expanded to exact
+// M+q values, their MFMAs against the four A operands af, and the scale
+// FMAs of the half-step's two groups (values 2h and 2h + 1 of the step's
+// scale window sv) into o.
+template <int DT, int NM>
+__device__ __forceinline__ void halfstep_products(const u32x4 (&wh)[NM], const u32x2 (&sv)[NM],
+                                                  const u32x4 (&af)[4], int h, uint32_t nib_mask,
+                                                  uint32_t magic, f32x4 (&o)[NM]) {
+  using A = Act<DT>;
+  u32x4 bop[NM][4];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    const u32x4 w = swap_pairs3(wh[m]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bop[m][j] = nibble_pairs_v<A::kCodeShift>(w[j], nib_mask, magic);
+  }
+  f32x4 acc[NM][2];
+#pragma unroll
+  for (int step2 = 0; step2 < 2; ++step2)
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        acc[m][q] = A::mfma16(af[2 * q + step2], bop[m][2 * q + step2],
+                              step2 ? acc[m][q] : f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float sc = A::to_f32(sb_val(sv[m], 2 * h + q));
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[m][v] = fmaf(sc, acc[m][q][v], o[m][v]);
+    }
+}
+
+// The bias terms of half-step h's two groups: lane (c, G) with G < 2
+// supplies the group sum xg of routed row c (group 2h + G of the step) and
+// (b - M s) of weight row c; lanes with G >= 2 supply zeros.
+template <int DT, int NM>
+__device__ __forceinline__ void halfstep_bias(const u32x2 (&sv)[NM], const u32x2 (&bv)[NM],
+                                              float xg, int h, int G, f32x4 (&o)[NM]) {
+  using A = Act<DT>;
+  const bool gl = G < 2;
+  const int j = 2 * h + (G & 1);
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    const float scv = A::to_f32(sb_val(sv[m], j));
+    const float bvv = A::to_f32(sb_val(bv[m], j));
+    o[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(gl ? xg : 0.f, gl ? fmaf(-A::kMagic, scv, bvv) : 0.f,
+                                                o[m], 0, 0, 0);
+  }
 }
 
 // FUSED: the gate/up product that finalises the routing in its prologue
@@ -105,7 +171,22 @@ __device__ __forceinline__ uint32_t sb_val(const u32x2 &v, int j) {
 // phase the block sums each token's k slots for its 16 columns as
 // combine_kernel does (act-rounded terms rnd(down * score), float32, slot
 // order, rounded once) and stores y.  No partial result leaves the block.
-template <int DT, bool DUAL, int NS, bool FUSED, bool STATIC, bool TILE = false>
+//
+// FDOWN (NSD > 0, with FUSED and STATIC, two blocks per expert): the down
+// product of the block's expert follows its gate/up product in the same
+// launch.  Block part p's gate/up tiles are h's columns [p KH, (p + 1) KH),
+// KH = 128 NSD = I / 2: its wavefronts write their SwiGLU outputs into LDS
+// (as staged rows of K = KH) instead of memory, and after a barrier the
+// block computes the down product over that half of the reduction for all
+// of the expert's rows and every down row: the sum the single product forms
+// from zero over the same half-steps (o = lo + hi), stored in float32 to
+// d_part[p][pair][row].  The combine adds the halves (lo + hi, rounded to
+// the act dtype as the down product's output) before weighting them, so y
+// is bit-identical to the separate down product and combine.  The
+// block's down units are (32-row tile, chunk of the expert's rows): each
+// wavefront's first one is requested before the barrier, and the rest are
+// taken from a block counter as the wavefronts finish theirs.
+template <int DT, bool DUAL, int NS, bool FUSED, bool STATIC, bool TILE = false, int NSD = 0>
 __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, int RT, int SPE) {
   using A = Act<DT>;
   constexpr int D = NS % 4 == 0 ? 4 : 3;  // ring slots
@@ -118,8 +199,13 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
   // 16-byte windows per lane of a weight row's scales (or biases): lane
   // group G holds groups 8G..8G+7 of window j, 32j + 8G.. of the row
   constexpr int SBW = (G64 + 31) / 32;
+  constexpr bool FDOWN = NSD > 0;
+  static_assert(!FDOWN || (DUAL && FUSED && STATIC), "FDOWN follows the expert-major gate/up");
+  constexpr int KH = 128 * NSD;                     // reduction columns of a down half
+  constexpr int HROWB = FDOWN ? row_bytes(KH) : 0;  // bytes per h row in LDS
+  constexpr int HST = FDOWN ? kFdRows * HROWB : 0;  // the h rows, at the top of the LDS
   // staged rows per phase
-  constexpr int kMaxStagedRows = kActLds / ROWB;
+  constexpr int kMaxStagedRows = (kActLds - HST) / ROWB;
   static_assert(kMaxStagedRows >= kRows, "one chunk must fit the staging LDS");
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -139,6 +225,7 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
   __shared__ uint16_t s_y[TILE ? kTilePairs * kRows : 1];
   __shared__ int s_inv[TILE ? kTilePairs : 1];
   __shared__ uint16_t s_csc[TILE ? kTilePairs : 1];
+  __shared__ int s_dctr;  // FDOWN: the next down unit
 
   hoist_args(a.act, a.act_ld, a.act_rows, a.a_map, a.a_div, a.offsets, a.w0, a.s0, a.b0, a.w1,
              a.s1, a.b1, a.R, a.gs, a.E, a.out, a.o_map, a.out_ld, RT, SPE);
@@ -153,11 +240,20 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
   const int ri = (wv & 3) * 2 + (wv >> 2);
 
   // STATIC: the block's expert and this wavefront's tiles [tw0, tw1)
-  int e_s = 0, tw0 = 0, tw1 = 0;
+  int e_s = 0, tw0 = 0, tw1 = 0, part = 0, b0 = 0;
   if constexpr (STATIC) {
     e_s = blockIdx.x / SPE;
-    const int part = blockIdx.x - e_s * SPE;
-    const int b0 = part * RT / SPE, b1 = (part + 1) * RT / SPE;
+    part = blockIdx.x - e_s * SPE;
+    if (FDOWN && E % 8 == 0) {
+      // the two blocks of an expert on one XCD (blocks are dealt to the
+      // eight XCDs round-robin by id), so that the 128-byte line of each
+      // down row that both halves read comes from its L2 the second time
+      const int b = blockIdx.x;
+      e_s = (b >> 4) * 8 + (b & 7);
+      part = (b >> 3) & 1;
+    }
+    b0 = part * RT / SPE;
+    const int b1 = (part + 1) * RT / SPE;
     tw0 = b0 + ri * (b1 - b0) / kW;
     tw1 = b0 + (ri + 1) * (b1 - b0) / kW;
   }
@@ -288,9 +384,9 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
   // ---- the block's chunks [c_first, c_last] and, dynamic, its share of
   // units [u0, u1); unit u = (chunk u / RT, tile u % RT).  STATIC chunk
   // indices are the expert's own (0 .. its chunk count - 1).
-  int u0 = 0, u1 = 0, c_first, c_last;
+  int u0 = 0, u1 = 0, c_first, c_last, n_e = 0;
   if constexpr (STATIC) {
-    const int n_e = s_off[e_s + 1] - s_off[e_s];
+    n_e = s_off[e_s + 1] - s_off[e_s];
     if (n_e == 0) {
       // no token chose this expert: the prefetched ring is not used (its
       // requests complete before the wavefront ends)
@@ -319,6 +415,60 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
     c_first = u0 / RT;
     c_last = (u1 - 1) / RT;
   }
+
+  // ---- FDOWN: the down product's state (used after the gate/up phases)
+  [[maybe_unused]] uint8_t *const hst = smem + (kActLds - HST);
+  constexpr int NSDR = FDOWN ? NSD : 1;
+  constexpr int KWD = 2 * KH / 8, G64D = 2 * KH / 64;  // down row: words, groups
+  constexpr int SBWD = FDOWN ? (G64D + 31) / 32 : 1;
+  // a down unit: NMD 16-row tiles of the down weights; the ring holds one
+  constexpr int NMD = 2;
+  struct DAddr {
+    int w[NMD], sb[NMD];
+  };
+  const int Rd = FDOWN ? a.d_R : 0;
+  const int64_t ERd = (int64_t)E * Rd;
+  const rsrc_t dw_r = make_rsrc(a.d_w, (uint32_t)(ERd * KWD * 4));
+  const rsrc_t ds_r = make_rsrc(a.d_s, (uint32_t)(ERd * G64D * 2));
+  const rsrc_t db_r = make_rsrc(a.d_b, (uint32_t)(ERd * G64D * 2));
+  u32x4 dq[NSDR][NMD];                      // down ring: a half-step (16 bytes a tile) a slot
+  u32x4 dsu[NMD][SBWD], dbu[NMD][SBWD];    // the current unit's scale/bias windows
+  u32x4 dsu_n[NMD][SBWD], dbu_n[NMD][SBWD];  // the next unit's
+  // the block's down units: (tile, chunk of the expert's rows), tile-major
+  int dnch = 1, dnu = 0;
+  if constexpr (FDOWN) {
+    dnch = (n_e + kRows - 1) / kRows;
+    dnu = Rd / (NMD * kRows) * dnch;
+  }
+  // down unit u: row offsets of its tiles (masked past the block's units)
+  auto setup_d = [&](int u, DAddr &ad) {
+    const bool ok = u < dnu;
+    const int tile = ok ? u / dnch : 0;
+#pragma unroll
+    for (int m = 0; m < NMD; ++m) {
+      const int er = e_s * Rd + tile * NMD * kRows + kRows * m + col;
+      ad.w[m] = ok ? er * (KWD * 4) + NSD * 64 * part + 16 * G : kMasked;
+      ad.sb[m] = ok ? er * (G64D * 2) : kMasked;
+    }
+  };
+  auto issue_d = [&](int slot, int hsl, const DAddr &ad) {
+#pragma unroll
+    for (int m = 0; m < NMD; ++m) dq[slot][m] = bload16(dw_r, ad.w[m] + 64 * hsl, 0);
+  };
+  // (a lane group's window of groups 32j + 8G .. + 7 is requested only where
+  // it meets the half's groups [2 NSD part, 2 NSD (part + 1)))
+  auto sb_issue_d = [&](u32x4 (&su)[NMD][SBWD], u32x4 (&bu)[NMD][SBWD], const DAddr &ad) {
+#pragma unroll
+    for (int m = 0; m < NMD; ++m)
+#pragma unroll
+      for (int j = 0; j < SBWD; ++j) {
+        const int g0 = 32 * j + 8 * G;
+        const bool need = g0 < 2 * NSD * (part + 1) && g0 + 8 > 2 * NSD * part;
+        const int off = need ? ad.sb[m] + 16 * G + 64 * j : kMasked;
+        su[m][j] = bload16(ds_r, off, 0);
+        bu[m][j] = bload16(db_r, off, 0);
+      }
+  };
 
   // the staged rows' activation rows (and, single product, output rows)
   auto act_row = [&](int sl) {
@@ -503,7 +653,12 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
                 // up rounds once more (its float32 product is exact)
                 const float gv = round_act<DT>(o[0][v]);
                 const float uv = round_act<DT>(o[1][v]);
-                a.out[(int64_t)(slot0 + t) * a.out_ld + row] = A::from_f32(silu_act<DT>(gv) * uv);
+                const uint16_t hv = A::from_f32(silu_act<DT>(gv) * uv);
+                if constexpr (FDOWN)
+                  *(uint16_t *)(hst + (slot0 - s_off[e_s] + t) * HROWB +
+                                h_pos(row - b0 * kRows)) = hv;
+                else
+                  a.out[(int64_t)(slot0 + t) * a.out_ld + row] = hv;
               } else {
                 a.out[(int64_t)s_orow[r][t] * a.out_ld + row] = A::from_f32(o[m][v]);
               }
@@ -523,9 +678,17 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
       const float *gsum = (const float *)(arow + 2 * K);
       // the next unit's scales and biases, ahead of its first ring slots
       sb_issue(su_nxt, bu_nxt, nxt);
-      f32x4 o[NM];
+      // The single product sums its reduction in two halves, half-steps
+      // [0, NS) and [NS, 2 NS) (128 columns each), each from zero, and adds
+      // them at the end: the order a block that owns one half of the
+      // reduction also follows (FDOWN).  Per half-step: its MFMAs, the scale
+      // FMAs of its two groups, then the bias MFMA of its two groups.
+      constexpr int NP = DUAL ? 1 : 2;
+      f32x4 op[NP][NM];
 #pragma unroll
-      for (int m = 0; m < NM; ++m) o[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int P = 0; P < NP; ++P)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) op[P][m] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
@@ -549,43 +712,30 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int st = 0; st < 4; ++st) af[h][st] = *(const u32x4 *)(ab + a_offset(s, h, st, 0));
-        const float xb = gsum[4 * s + G];
+        // group sums: the step's four groups (lane group G: group 4s + G),
+        // or per half-step its two (lane groups 0 and 1)
+        const float xb = gsum[4 * s + (DUAL ? G : (G & 1))];
+        const float xb2 = DUAL ? 0.f : gsum[4 * s + 2 + (G & 1)];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          u32x4 bop[NM][4];
+          const int P = !DUAL && 2 * s + h >= NS ? 1 : 0;
+          u32x4 wh[NM];
+#pragma unroll
+          for (int m = 0; m < NM; ++m) wh[m] = wq[d][m][h];
+          halfstep_products<DT, NM>(wh, sv, af[h], h, nib_mask, magic, op[P]);
+          if constexpr (!DUAL) halfstep_bias<DT, NM>(sv, bv, h ? xb2 : xb, h, G, op[P]);
+        }
+        if constexpr (DUAL) {
+          // bias terms of the step's four groups: lane (c, G) supplies the
+          // group sum of routed row c and (b - M s) of weight row c, group
+          // 4s + G
 #pragma unroll
           for (int m = 0; m < NM; ++m) {
-            const u32x4 w = swap_pairs3(wq[d][m][h]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              bop[m][j] = nibble_pairs_v<A::kCodeShift>(w[j], nib_mask, magic);
+            const float scv = A::to_f32(sb_val(sv[m], G));
+            const float bvv = A::to_f32(sb_val(bv[m], G));
+            op[0][m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xb, fmaf(-A::kMagic, scv, bvv),
+                                                            op[0][m], 0, 0, 0);
           }
-          f32x4 acc[NM][2];
-#pragma unroll
-          for (int step2 = 0; step2 < 2; ++step2)
-#pragma unroll
-            for (int m = 0; m < NM; ++m)
-#pragma unroll
-              for (int q = 0; q < 2; ++q)
-                acc[m][q] = A::mfma16(af[h][2 * q + step2], bop[m][2 * q + step2],
-                                      step2 ? acc[m][q] : f32x4{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-          for (int m = 0; m < NM; ++m)
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-              const float sc = A::to_f32(sb_val(sv[m], 2 * h + q));
-#pragma unroll
-              for (int v = 0; v < 4; ++v) o[m][v] = fmaf(sc, acc[m][q][v], o[m][v]);
-            }
-        }
-        // bias terms of the step's four groups: lane (c, G) supplies the group
-        // sum of routed row c and (b - M s) of weight row c, group 4s + G
-#pragma unroll
-        for (int m = 0; m < NM; ++m) {
-          const float scv = A::to_f32(sb_val(sv[m], G));
-          const float bvv = A::to_f32(sb_val(bv[m], G));
-          o[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xb, fmaf(-A::kMagic, scv, bvv), o[m], 0, 0,
-                                                      0);
         }
         // refill the slot D steps ahead: this unit, or the next one.  The
         // scheduling barrier keeps each step's requests in that step (the
@@ -595,6 +745,9 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
         else issue(d, s + D - NS, nxt);
         __builtin_amdgcn_sched_barrier(0);
       }
+      f32x4 o[NM];
+#pragma unroll
+      for (int m = 0; m < NM; ++m) o[m] = DUAL ? op[0][m] : op[0][m] + op[NP - 1][m];
       epilogue(u, o);
       cur = nxt;
       setup(u + 2, nxt);
@@ -607,9 +760,127 @@ __global__ __launch_bounds__(64 * kW, 2) void gemv3_kernel(const GroupedArgs a, 
         }
     }
 
-    // every wavefront is done with the staged rows
-    __syncthreads();
+    // every wavefront is done with the staged rows (FDOWN: the last phase's
+    // barrier follows the first down requests, below)
+    if (!FDOWN || cb + n <= c_last) __syncthreads();
     cb += n;
+  }
+
+  if constexpr (FDOWN) {
+    // the first down unit's ring and windows, requested before the barrier
+    // that ends the gate/up product
+    {
+      // (the wavefronts' first units are units 0 .. 7; the rest are taken
+      // from a block counter as the wavefronts finish, so that the younger
+      // wavefront of each SIMD, which the SIMD serves second, takes fewer)
+      DAddr d0;
+      setup_d(ri, d0);
+      sb_issue_d(dsu, dbu, d0);
+#pragma unroll
+      for (int hsl = 0; hsl < NSDR; ++hsl) issue_d(hsl, hsl, d0);
+      if (tid == 0) s_dctr = kW;
+    }
+    __syncthreads();
+    // group sums of the h rows, formed as stage_store forms them for the
+    // down product's staged rows (eight 16-byte chunks in column order, each
+    // dword's pair in column order)
+    for (int it = tid; it < n_e * (KH / 64); it += 64 * kW) {
+      const int er = it / (KH / 64), lg = it - er * (KH / 64);
+      uint8_t *hrow = hst + er * HROWB;
+      float gs = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int Gi = ((i >> 2) & 1) | (((i >> 1) & 1) << 1);
+        const u32x4 pv = *(const u32x4 *)(hrow + a_offset(lg >> 2, (lg >> 1) & 1,
+                                                           2 * (lg & 1) + (i & 1), Gi));
+        // undo pair_order: (x0,x4)(x1,x5)(x2,x6)(x3,x7) -> (x0,x1)(x2,x3)(x4,x5)(x6,x7)
+        const u32x4 v = {perm_b32(pv.y, pv.x, 0x05040100u), perm_b32(pv.w, pv.z, 0x05040100u),
+                         perm_b32(pv.y, pv.x, 0x07060302u), perm_b32(pv.w, pv.z, 0x07060302u)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gs = A::dot2(v[j], A::kOne2, gs);
+      }
+      *(float *)(hrow + 2 * KH + 4 * lg) = gs;
+    }
+    __syncthreads();
+    const int TK = (int)a.act_rows * a.a_div;
+    // half P of the reduction: half-steps NSD P .. NSD P + NSD - 1 of the
+    // single product's unit (compile-time, so are the window picks)
+    auto down_phase = [&](auto pc) {
+      constexpr int P = decltype(pc)::value;
+      // the next unit from the block counter (one lane's LDS atomic)
+      auto grab = [&]() {
+        int v = 0;
+        if (lane == 0)
+          v = __hip_atomic_fetch_add(&s_dctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        return __builtin_amdgcn_readfirstlane(v);
+      };
+      int u = ri;        // in the ring
+      int un = grab();   // requested into the ring during unit u
+      while (u < dnu) {  // uniform over the wavefront
+        const int q = u / dnch, c = u - q * dnch;
+        const int cnt = min(kRows, n_e - kRows * c);
+        const uint8_t *arow = hst + (kRows * c + min(col, cnt - 1)) * HROWB;
+        const uint8_t *ab = arow + G * 16;
+        const float *gsum = (const float *)(arow + 2 * KH);
+        // the next unit's scales and biases, ahead of its first use
+        DAddr an;
+        setup_d(un, an);
+        sb_issue_d(dsu_n, dbu_n, an);
+        f32x4 o[NMD];
+#pragma unroll
+        for (int m = 0; m < NMD; ++m) o[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int hsl = 0; hsl < NSDR; ++hsl) {
+          const int hsg = NSDR * P + hsl, sg = hsg >> 1, h = hsg & 1;
+          u32x2 sv[NMD], bv[NMD];
+#pragma unroll
+          for (int m = 0; m < NMD; ++m) {
+            const int j = sg / 8, Gp = (sg % 8) / 2, w0 = 2 * (sg % 2);
+            const int src = (Gp * 16 + col) * 4;
+            sv[m] = u32x2{(uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)dsu[m][j][w0]),
+                          (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)dsu[m][j][w0 + 1])};
+            bv[m] = u32x2{(uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)dbu[m][j][w0]),
+                          (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)dbu[m][j][w0 + 1])};
+          }
+          u32x4 af[4];
+#pragma unroll
+          for (int st = 0; st < 4; ++st)
+            af[st] = *(const u32x4 *)(ab + a_offset(hsl >> 1, hsl & 1, st, 0));
+          const float xg = gsum[2 * hsl + (G & 1)];
+          halfstep_products<DT, NMD>(dq[hsl], sv, af, h, nib_mask, magic, o);
+          halfstep_bias<DT, NMD>(sv, bv, xg, h, G, o);
+          // refill the slot with the next unit's half-step
+          issue_d(hsl, hsl, an);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        // this half's float32 sums, by pair
+#pragma unroll
+        for (int m = 0; m < NMD; ++m) {
+          const int row = q * NMD * kRows + kRows * m + col;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int t = 4 * G + v;
+            if (t < cnt) {
+              const int pair = s_sorted[s_off[e_s] + kRows * c + t];
+              a.d_part[((int64_t)P * TK + pair) * Rd + row] = o[m][v];
+            }
+          }
+        }
+#pragma unroll
+        for (int m = 0; m < NMD; ++m)
+#pragma unroll
+          for (int j = 0; j < SBWD; ++j) {
+            dsu[m][j] = dsu_n[m][j];
+            dbu[m][j] = dbu_n[m][j];
+          }
+        u = un;
+        un = grab();
+      }
+    };
+    if (part == 0)
+      down_phase(std::integral_constant<int, 0>{});
+    else
+      down_phase(std::integral_constant<int, 1>{});
   }
 
   if constexpr (TILE) {
@@ -657,26 +928,28 @@ bool use_static(const GroupedArgs &a) {
   return a.act_rows * a.a_div >= 2 * (int64_t)a.E;
 }
 
-template <int DT, bool DUAL, int NS, bool FUSED, bool STATIC, bool TILE = false>
+template <int DT, bool DUAL, int NS, bool FUSED, bool STATIC, bool TILE = false, int NSD = 0>
 hipError_t launch_v3(const GroupedArgs &a, hipStream_t st) {
   const int RU = DUAL || TILE ? kRows : 2 * kRows;
   const int RT = (a.R + RU - 1) / RU;
+  auto *const kern = &gemv3_kernel<DT, DUAL, NS, FUSED, STATIC, TILE, NSD>;
   // more than 64 KB of dynamic LDS (once per device; a failure here shows up
   // as a failed launch below)
   static bool attr_set[64] = {false};
   int dev = 0;
   if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !attr_set[dev]) {
-    (void)hipFuncSetAttribute((const void *)&gemv3_kernel<DT, DUAL, NS, FUSED, STATIC, TILE>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kActLds);
+    (void)hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              kActLds);
     attr_set[dev] = true;
   }
   // STATIC: SPE blocks per expert, about one block per compute unit in all
-  // (and at least one tile a block)
+  // (and at least one tile a block); FDOWN: two, one per half of the down
+  // reduction
   // TILE: one block per 16-row tile
-  const int spe = STATIC ? std::max(1, std::min(cu_count() / a.E, RT)) : 1;
+  const int spe =
+      NSD > 0 ? 2 : STATIC ? std::max(1, std::min(cu_count() / a.E, RT)) : 1;
   const int grid = TILE ? RT : STATIC ? a.E * spe : cu_count();
-  hipLaunchKernelGGL((gemv3_kernel<DT, DUAL, NS, FUSED, STATIC, TILE>), dim3(grid), dim3(64 * kW),
-                     kActLds, st, a, RT, spe);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kW), kActLds, st, a, RT, spe);
   return hipGetLastError();
 }
 
@@ -710,6 +983,24 @@ hipError_t launch_gemv3(int dtype, bool dual, const GroupedArgs &a, hipStream_t 
   if (dtype == DT_BF16)
     return dual ? launch_v3_ns<DT_BF16, true>(a, st) : launch_v3_ns<DT_BF16, false>(a, st);
   return dual ? launch_v3_ns<DT_F16, true>(a, st) : launch_v3_ns<DT_F16, false>(a, st);
+}
+
+// The fused gate/up + down launch: the 30B-A3B decode shape (K 2048, I 768:
+// a down half of three half-steps), down rows in 32-row tiles (d_R a
+// multiple of 256: a whole number a wavefront), at most
+// kFdRows tokens (one h row each per expert) and the fused routing's limits.
+bool gemv3_fused_down_supports(int K, int R, int dR, int E, int gs, int64_t T, int k) {
+  return K == 2048 && R == 2 * 128 * 3 && gemv3_supports(K, R, E, gs) &&
+         gemv3_supports(R, dR, E, gs) && dR % 256 == 0 && T >= 1 && T <= kFdRows &&
+         T * k <= kFusedPairs && E <= kRowExperts && k <= kRowTopK;
+}
+
+hipError_t launch_gemv3_fused_down(int dtype, const GroupedArgs &a, hipStream_t st) {
+  if (!gemv3_fused_down_supports(a.K, a.R, a.d_R, a.E, a.gs, a.act_rows, a.a_div) ||
+      !a.route_part || !a.d_w || !a.d_s || !a.d_b || !a.d_part)
+    return hipErrorInvalidValue;
+  return dtype == DT_BF16 ? launch_v3<DT_BF16, true, 8, true, true, false, 3>(a, st)
+                          : launch_v3<DT_F16, true, 8, true, true, false, 3>(a, st);
 }
 
 bool gemv3_down_combine_supports(int K, int R, int E, int gs, int64_t pairs, int k) {

@@ -63,6 +63,14 @@ struct GroupedArgs {
   const uint16_t *c_scores;
   uint16_t *c_y;
   int c_k;
+  // Gate/up product followed by the down product in the same launch
+  // (launch_gemv3_fused_down): the down weights d_w/d_s/d_b [E, d_R, R]
+  // (d_R rows over the R = I columns of h) and the float32 sums of each
+  // half of its reduction, d_part [2][act_rows * a_div][d_R] by pair.
+  const uint32_t *d_w;
+  const uint16_t *d_s, *d_b;
+  float *d_part;
+  int d_R;
 };
 
 // Decode batches whose routing the gate/up product can finalise: at most
@@ -77,6 +85,18 @@ bool fused_route_supports(int64_t T, int64_t E, int k);
 constexpr int kTilePairs = 256;
 bool gemv3_down_combine_supports(int K, int R, int E, int gs, int64_t pairs, int k);
 hipError_t launch_gemv3_down_combine(int dtype, const GroupedArgs &a, hipStream_t st);
+
+// Decode gate/up product with the down product of the same expert-major
+// blocks (gemv3.hip, FDOWN): two blocks per expert, each over one half of
+// the down reduction, writing float32 half sums to d_part; combined by
+// launch_combine_split.  Shapes: K = 2048, R = 768, d_R a multiple of 256,
+// at most 64 tokens; the routing finalised in the launch (route_part).
+bool gemv3_fused_down_supports(int K, int R, int dR, int E, int gs, int64_t T, int k);
+hipError_t launch_gemv3_fused_down(int dtype, const GroupedArgs &a, hipStream_t st);
+// y[t] = rnd(sum_j rnd(rnd(part[0][t k + j] + part[1][t k + j]) * score[t k + j])):
+// combine_kernel's arithmetic on the down output rnd(lo + hi).
+hipError_t launch_combine_split(int dtype, const float *part, const void *scores, int64_t T, int k,
+                                int64_t H, void *y, hipStream_t st);
 
 // Router.  Partial float64 logits over hidden splits, then per-token finalise.
 // With final_act the logits are rounded and stored as act [T, E] directly.
@@ -167,11 +187,12 @@ hipError_t launch_gemm(int dtype, bool dual, const GroupedArgs &a, int64_t max_m
 hipError_t launch_act_to_f16(const void *x, int64_t n, void *out, uint8_t *sh, hipStream_t st);
 
 // Combine fused with the residual add and RMSNorm that follow the MoE block
-// in the model (rows of H <= 8192, a multiple of 8).
+// in the model (rows of H <= 8192, a multiple of 8).  split: `down` holds the
+// float32 half sums [2][T * k][H] of launch_gemv3_fused_down.
 hipError_t launch_combine_residual_norm(int dtype, const void *down, const void *scores,
                                         int64_t T, int k, int64_t H, const void *h,
                                         const void *w, float eps, void *h_out, void *x_out,
-                                        hipStream_t st);
+                                        hipStream_t st, bool split = false);
 bool combine_residual_norm_supports(int64_t H);
 
 // Multi-query paged attention on the matrix cores (paged_prefill.hip): L > 1

@@ -79,9 +79,11 @@ __global__ __launch_bounds__(kNormThreads) void residual_rms_norm_kernel(
 // x_out = rnd(rms_norm(h_out) * w).  Eight pairs' loads are in flight at once.
 constexpr int kCombChunks = 4;  // 8-value chunks per thread: H <= 256 * 4 * 8
 
-template <int DT>
+// SPLIT: the down outputs come as the float32 sums of the two halves of the
+// down reduction (down_vals).
+template <int DT, bool SPLIT>
 __global__ __launch_bounds__(kNormThreads) void moe_combine_residual_norm_kernel(
-    const uint16_t *__restrict__ down, const uint16_t *__restrict__ scores, int k, int H8,
+    const void *__restrict__ down, const uint16_t *__restrict__ scores, int k, int H8,
     const uint16_t *__restrict__ h, const uint16_t *__restrict__ w, float eps,
     uint16_t *__restrict__ h_out, uint16_t *__restrict__ x_out) {
   using A = Act<DT>;
@@ -96,27 +98,19 @@ __global__ __launch_bounds__(kNormThreads) void moe_combine_residual_norm_kernel
     const int c = tid + kNormThreads * q;
     if (c >= H8) continue;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j0 = 0; j0 < k; j0 += 8) {
-      u32x4 v[8];
-      uint32_t sv[8];
+    constexpr int NB = SPLIT ? 4 : 8;  // pairs whose loads are in flight together
+    for (int j0 = 0; j0 < k; j0 += NB) {
+      float dv[NB][8];
+      uint32_t sv[NB];
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        v[jj] = u32x4{0u, 0u, 0u, 0u};
-        sv[jj] = 0u;
-        if (j0 + jj < k) {
-          v[jj] = ldg16(down + ((t * k + j0 + jj) * H + 8 * c));
-          sv[jj] = scores[t * k + j0 + jj];
-        }
-      }
+      for (int jj = 0; jj < NB; ++jj) sv[jj] = j0 + jj < k ? scores[t * k + j0 + jj] : 0u;
+      down_vals<DT, SPLIT, NB>(down, (int64_t)gridDim.x * k, t, k, j0, H, c, dv);
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
+      for (int jj = 0; jj < NB; ++jj) {
         if (j0 + jj >= k) break;
         const float sc = A::to_f32(sv[jj]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc[2 * i] += round_act<DT>(A::lo(v[jj][i]) * sc);
-          acc[2 * i + 1] += round_act<DT>(A::hi(v[jj][i]) * sc);
-        }
+        for (int i = 0; i < 8; ++i) acc[i] += round_act<DT>(dv[jj][i] * sc);
       }
     }
     const u32x4 hh = ldg16(h + t * H + 8 * c);
@@ -244,18 +238,19 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(QkvArgs a) {
 hipError_t launch_combine_residual_norm(int dtype, const void *down, const void *scores,
                                         int64_t T, int k, int64_t H, const void *h,
                                         const void *w, float eps, void *h_out, void *x_out,
-                                        hipStream_t st) {
+                                        hipStream_t st, bool split) {
   if (T == 0) return hipSuccess;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)T), dim3(kNormThreads), 0, st, down,
+                       (const uint16_t *)scores, k, (int)(H / 8), (const uint16_t *)h,
+                       (const uint16_t *)w, eps, (uint16_t *)h_out, (uint16_t *)x_out);
+  };
   if (dtype == DT_BF16)
-    hipLaunchKernelGGL(moe_combine_residual_norm_kernel<DT_BF16>, dim3((unsigned)T),
-                       dim3(kNormThreads), 0, st, (const uint16_t *)down, (const uint16_t *)scores,
-                       k, (int)(H / 8), (const uint16_t *)h, (const uint16_t *)w, eps,
-                       (uint16_t *)h_out, (uint16_t *)x_out);
+    split ? go(moe_combine_residual_norm_kernel<DT_BF16, true>)
+          : go(moe_combine_residual_norm_kernel<DT_BF16, false>);
   else
-    hipLaunchKernelGGL(moe_combine_residual_norm_kernel<DT_F16>, dim3((unsigned)T),
-                       dim3(kNormThreads), 0, st, (const uint16_t *)down, (const uint16_t *)scores,
-                       k, (int)(H / 8), (const uint16_t *)h, (const uint16_t *)w, eps,
-                       (uint16_t *)h_out, (uint16_t *)x_out);
+    split ? go(moe_combine_residual_norm_kernel<DT_F16, true>)
+          : go(moe_combine_residual_norm_kernel<DT_F16, false>);
   return hipGetLastError();
 }
 

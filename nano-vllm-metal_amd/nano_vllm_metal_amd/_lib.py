@@ -69,6 +69,7 @@ SIGNATURES = {
     "nvm_moe_forward_stage": [_I, _P, _I64, _I64, _I64, _I64, _I, _I, _I, _I, _I,
                               _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                               _P, _P, _P, _I, _P, _SZ, _P],
+    "nvm_moe_forward_plan": [_I64, _I64, _I64, _I64, _I, _I, _I, ctypes.POINTER(_I)],
     "nvm_moe_scratch_bytes": [ctypes.POINTER(_SZ)],
     "nvm_moe_forward_noalloc": [_P, _I64, _I64, _I64, _I64, _I, _I, _I, _I, _I,
                                 _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,

@@ -327,8 +327,37 @@ def test_forward_stage_validation():
         return lib.nvm_moe_forward_stage(stage, 1, T, 2048, 768, 128, 8, 1, 64, bits, 1, *p, 1,
                                          None, None, 0, 1, 1 << 40, None)
 
-    assert call(4) == L.NVM_ERR_INVALID and "stage" in _err(lib)
+    assert call(6) == L.NVM_ERR_INVALID and "stage" in _err(lib)
     assert call(-1) == L.NVM_ERR_INVALID
     assert call(1, bits=8) == L.NVM_ERR_UNSUPPORTED and "bits" in _err(lib)
     assert call(0, T=0) == 0
     assert call(2, T=600_000) == L.NVM_ERR_UNSUPPORTED and "2 GiB" in _err(lib)
+
+
+def test_forward_plan(monkeypatch):
+    """nvm_moe_forward_plan: one launch for both decode products at the
+    30B-A3B shape from two routed rows per expert on average up to 64 tokens
+    (regime auto or decode), else the separate products; the overrides
+    NVM_FUSED_DOWN and NVM_GEMV_STATIC=0 apply; no device work."""
+    import ctypes
+
+    L, lib = _lib()
+    monkeypatch.delenv("NVM_FUSED_DOWN", raising=False)
+    monkeypatch.delenv("NVM_GEMV_STATIC", raising=False)
+
+    def plan(T, H=2048, I=768, E=128, k=8, gs=64, regime=0):
+        out = ctypes.c_int(-1)
+        assert lib.nvm_moe_forward_plan(T, H, I, E, k, gs, regime, ctypes.byref(out)) == 0
+        return out.value
+
+    assert [plan(T) for T in (1, 8, 31, 32, 64, 65, 4096)] == [0, 0, 0, 1, 1, 0, 0]
+    assert plan(32, regime=1) == 1 and plan(32, regime=2) == 0
+    assert plan(32, H=4096, I=1536) == 0 and plan(32, gs=128) == 0
+    monkeypatch.setenv("NVM_FUSED_DOWN", "1")
+    assert plan(1) == 1 and plan(65) == 0
+    monkeypatch.setenv("NVM_FUSED_DOWN", "0")
+    assert plan(32) == 0
+    monkeypatch.delenv("NVM_FUSED_DOWN")
+    monkeypatch.setenv("NVM_GEMV_STATIC", "0")
+    assert plan(32) == 0
+    assert lib.nvm_moe_forward_plan(32, 2048, 768, 128, 8, 64, 0, None) == L.NVM_ERR_INVALID

@@ -476,6 +476,43 @@ def test_moe_decode_down_combine_is_bit_identical(T, H, I, act, monkeypatch):
     assert_moe_close(to_np(outs[1][0]), y_ref, act, "moe down+combine")
 
 
+@pytest.mark.parametrize("T,E,act,force", [(32, 128, "bfloat16", ""), (64, 128, "bfloat16", ""),
+                                           (40, 128, "float16", ""), (8, 128, "bfloat16", "1"),
+                                           (1, 128, "bfloat16", "1"), (32, 64, "bfloat16", "1")])
+def test_moe_decode_fused_down_is_bit_identical(T, E, act, force, monkeypatch):
+    """The decode gate/up and down products in one launch (two expert-major
+    blocks per expert, each over one half of the down reduction, h kept in
+    LDS; the combine adds the halves) against the two launches: the same y
+    bits, routing and scores, forced both ways (NVM_FUSED_DOWN) where it is
+    chosen and below its batch threshold (few rows, many untouched experts,
+    E = 64); the combine with the residual add and RMSNorm after the block
+    likewise; the fused output also checked against the oracle."""
+    from nano_vllm_metal_amd.fused import moe_residual_rms_norm
+
+    x, w = _moe_case(950 + T + E, T, 2048, E, 768, act)
+    moe = make_moe(w, act, 64, 8, True, DEV)
+    moe.regime = "decode"
+    xs = to_act(x, act, DEV)
+    g = torch.Generator(device=DEV).manual_seed(T)
+    h = (torch.randn(T, 2048, device=DEV, generator=g) * 2).to(xs.dtype)
+    nw = (1 + 0.1 * torch.randn(2048, device=DEV, generator=g)).to(xs.dtype)
+    outs = []
+    for fused in ("0", force or "1"):
+        if force or fused == "0":
+            monkeypatch.setenv("NVM_FUSED_DOWN", fused)
+        else:
+            monkeypatch.delenv("NVM_FUSED_DOWN", raising=False)
+        y, ids, sc = moe.forward(xs, return_routing=True)
+        h2, x2 = moe_residual_rms_norm(moe, xs, h, nw, 1e-6)
+        torch.cuda.synchronize()
+        outs.append((y.clone(), ids.clone(), sc.clone(), h2.clone(), x2.clone()))
+    print(f"fused down T={T} E={E} {act} force={force!r}", flush=True)
+    for a, b, what in zip(outs[0], outs[1], ("y", "ids", "scores", "h_out", "x_out")):
+        assert torch.equal(a, b), f"{what}: fused gate/up + down differs from two launches"
+    y_ref, _, _ = O.moe_forward(x, w, min(8, E), True, act, 64)
+    assert_moe_close(to_np(outs[1][0]), y_ref, act, "moe fused down")
+
+
 def test_moe_235b_decode():
     """H4096 I1536: gate/up through the eight-group slice GEMV (KS 8), down
     through six-group slices in four k-slices."""

@@ -1,11 +1,13 @@
 """nvm_moe_forward_stage: the block's launch sequence one stage at a time.
 
-Stages 0..3 run in order on one workspace must give exactly what
+Stages 0..3 (and 0, 4, 5: both products as the forward launches them, then
+their combine) run in order on one workspace must give exactly what
 nvm_moe_forward gives (the same kernels, the same workspace hand-offs), for
 each of the launch sequences the forward takes: decode batches (routing
-finalised in the gate/up prologue), prefill batches whose int8 router writes
-the fp16 copy of x, prefill batches converted by their own launch, and fp16
-activations.  Repeating a stage must not change what the next one reads.
+finalised in the gate/up prologue; both products in one launch from 32
+tokens), prefill batches whose int8 router writes the fp16 copy of x,
+prefill batches converted by their own launch, and fp16 activations.
+Repeating a stage must not change what the next one reads.
 """
 
 from __future__ import annotations
@@ -39,13 +41,16 @@ def _call(lib, L, moe, x, ws, y, ids, sc, stage=None, regime=0):
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("T,act,regime", [
-    (32, "bfloat16", 0),    # decode: partial logits, gate/up finalising the routing
-    (300, "bfloat16", 0),   # prefill: int8 router writes the fp16 copy of x
-    (100, "bfloat16", 2),   # prefill regime below the int8 router's batch: act_to_f16 launch
-    (200, "float16", 0),    # fp16 activations: the GEMMs stage x themselves
+@pytest.mark.parametrize("T,act,regime,seq", [
+    (32, "bfloat16", 0, (0, 1, 2, 3)),  # decode: partial logits, gate/up finalising the routing
+    (300, "bfloat16", 0, (0, 1, 2, 3)),  # prefill: int8 router writes the fp16 copy of x
+    (100, "bfloat16", 2, (0, 1, 2, 3)),  # prefill below the int8 router's batch: act_to_f16
+    (200, "float16", 0, (0, 1, 2, 3)),  # fp16 activations: the GEMMs stage x themselves
+    (32, "bfloat16", 0, (0, 4, 5)),     # decode, both products in one launch, split combine
+    (64, "float16", 0, (0, 4, 5)),
+    (8, "bfloat16", 0, (0, 4, 5)),      # stage 4 as stages 1 and 2 (no fused launch)
 ])
-def test_stages_in_order_equal_the_forward(T, act, regime):
+def test_stages_in_order_equal_the_forward(T, act, regime, seq):
     from nano_vllm_metal_amd import _lib as L
 
     lib = L.load()
@@ -62,14 +67,14 @@ def test_stages_in_order_equal_the_forward(T, act, regime):
         ids = torch.full((T, k), -1, dtype=torch.int32, device=DEV)
         sc = torch.full((T, k), float("nan"), dtype=x.dtype, device=DEV)
         if staged:
-            for s in range(4):
+            for s in seq:
                 # every stage twice: a repeat must leave the next stage's inputs as they were
                 for _ in range(2):
                     _call(lib, L, moe, x, ws, y, ids, sc, stage=s, regime=regime)
         else:
             _call(lib, L, moe, x, ws, y, ids, sc, regime=regime)
         outs.append((y, ids, sc))
-    print(f"stages T={T} {act} regime={regime}", flush=True)
+    print(f"stages T={T} {act} regime={regime} seq={seq}", flush=True)
     for a, b, what in zip(outs[0], outs[1], ("y", "ids", "scores")):
         assert torch.equal(a, b), f"{what} of the staged calls differs from nvm_moe_forward"
 
