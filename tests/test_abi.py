@@ -336,7 +336,7 @@ def test_forward_stage_validation():
 
 def test_forward_plan(monkeypatch):
     """nvm_moe_forward_plan: one launch for both decode products at the
-    30B-A3B shape from two routed rows per expert on average up to 64 tokens
+    30B-A3B shape from one routed row per expert on average up to 64 tokens
     (regime auto or decode), else the separate products; the overrides
     NVM_FUSED_DOWN and NVM_GEMV_STATIC=0 apply; no device work."""
     import ctypes
@@ -350,7 +350,7 @@ def test_forward_plan(monkeypatch):
         assert lib.nvm_moe_forward_plan(T, H, I, E, k, gs, regime, ctypes.byref(out)) == 0
         return out.value
 
-    assert [plan(T) for T in (1, 8, 31, 32, 64, 65, 4096)] == [0, 0, 0, 1, 1, 0, 0]
+    assert [plan(T) for T in (1, 8, 15, 16, 32, 64, 65, 4096)] == [0, 0, 0, 1, 1, 1, 0, 0]
     assert plan(32, regime=1) == 1 and plan(32, regime=2) == 0
     assert plan(32, H=4096, I=1536) == 0 and plan(32, gs=128) == 0
     monkeypatch.setenv("NVM_FUSED_DOWN", "1")

@@ -477,6 +477,7 @@ def test_moe_decode_down_combine_is_bit_identical(T, H, I, act, monkeypatch):
 
 
 @pytest.mark.parametrize("T,E,act,force", [(32, 128, "bfloat16", ""), (64, 128, "bfloat16", ""),
+                                           (16, 128, "bfloat16", ""),
                                            (40, 128, "float16", ""), (8, 128, "bfloat16", "1"),
                                            (1, 128, "bfloat16", "1"), (32, 64, "bfloat16", "1")])
 def test_moe_decode_fused_down_is_bit_identical(T, E, act, force, monkeypatch):
