@@ -514,6 +514,36 @@ def test_moe_decode_fused_down_is_bit_identical(T, E, act, force, monkeypatch):
     assert_moe_close(to_np(outs[1][0]), y_ref, act, "moe fused down")
 
 
+@pytest.mark.parametrize("T", [20, 40, 64])
+def test_moe_decode_fused_down_skewed(T, monkeypatch):
+    """Zipf(1.1) routing through the fused decode products: popular experts
+    take 17-20 rows (two chunks staged in one phase) or more (several
+    phases), beside experts of one chunk, whose two wavefronts per SIMD
+    share a tile's halves.  The same y bits, routing and scores as the two
+    launches, and y against the oracle."""
+    H, E, I, act = 2048, 128, 768, "bfloat16"
+    x, w = _skewed_case(960 + T, T, H, E, I, act)
+    _, _, ids_ref, _ = O.route_topk(x, *w["router"], 64, 8, True, act)
+    counts = np.bincount(ids_ref.reshape(-1), minlength=E)
+    assert counts.max() > 16 and (counts[counts > 0] <= 16).any(), counts
+    moe = make_moe(w, act, 64, 8, True, DEV)
+    moe.regime = "decode"
+    xs = to_act(x, act, DEV)
+    outs = []
+    for fused in ("0", "1"):
+        monkeypatch.setenv("NVM_FUSED_DOWN", fused)
+        y, ids, sc = moe.forward(xs, return_routing=True)
+        torch.cuda.synchronize()
+        outs.append((y.clone(), ids.clone(), sc.clone()))
+    print(f"fused down skewed T={T}: rows per expert max {counts.max()}, "
+          f"{int(((counts > 16) & (counts <= 20)).sum())} of 17-20, "
+          f"{int((counts > 20).sum())} above 20", flush=True)
+    for a, b, what in zip(outs[0], outs[1], ("y", "ids", "scores")):
+        assert torch.equal(a, b), f"{what}: fused gate/up + down differs from two launches"
+    y_ref, _, _ = O.moe_forward(x, w, 8, True, act, 64)
+    assert_moe_close(to_np(outs[1][0]), y_ref, act, "moe fused down skewed")
+
+
 def test_moe_235b_decode():
     """H4096 I1536: gate/up through the eight-group slice GEMV (KS 8), down
     through six-group slices in four k-slices."""
