@@ -76,18 +76,21 @@ __global__ __launch_bounds__(kNormThreads) void residual_rms_norm_kernel(
 // MoE combine + residual add + RMSNorm, one block per token: the token's k
 // expert outputs summed in slot order exactly as the combine kernel does
 // (y = rnd(sum_j rnd(down_j * score_j))), then h_out = rnd(h + y) and
-// x_out = rnd(rms_norm(h_out) * w).  Eight pairs' loads are in flight at once.
+// x_out = rnd(rms_norm(h_out) * w).  Eight pairs' loads are in flight at once
+// (KK: the top-k as a compile-time count, every pair's loads at once, the
+// float32 halves included; the arithmetic and its order are the same).
 constexpr int kCombChunks = 4;  // 8-value chunks per thread: H <= 256 * 4 * 8
 
 // SPLIT: the down outputs come as the float32 sums of the two halves of the
 // down reduction (down_vals).
-template <int DT, bool SPLIT>
+template <int DT, bool SPLIT, int KK>
 __global__ __launch_bounds__(kNormThreads) void moe_combine_residual_norm_kernel(
-    const void *__restrict__ down, const uint16_t *__restrict__ scores, int k, int H8,
+    const void *__restrict__ down, const uint16_t *__restrict__ scores, int k_arg, int H8,
     const uint16_t *__restrict__ h, const uint16_t *__restrict__ w, float eps,
     uint16_t *__restrict__ h_out, uint16_t *__restrict__ x_out) {
   using A = Act<DT>;
   __shared__ float s_part[kNormThreads / 64];
+  const int k = KK ? KK : k_arg;
   const int64_t t = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t H = (int64_t)H8 * 8;
@@ -98,7 +101,8 @@ __global__ __launch_bounds__(kNormThreads) void moe_combine_residual_norm_kernel
     const int c = tid + kNormThreads * q;
     if (c >= H8) continue;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    constexpr int NB = SPLIT ? 4 : 8;  // pairs whose loads are in flight together
+    // pairs whose loads are in flight together (KK: all of them)
+    constexpr int NB = KK ? KK : SPLIT ? 4 : 8;
     for (int j0 = 0; j0 < k; j0 += NB) {
       float dv[NB][8];
       uint32_t sv[NB];
@@ -245,12 +249,20 @@ hipError_t launch_combine_residual_norm(int dtype, const void *down, const void 
                        (const uint16_t *)scores, k, (int)(H / 8), (const uint16_t *)h,
                        (const uint16_t *)w, eps, (uint16_t *)h_out, (uint16_t *)x_out);
   };
-  if (dtype == DT_BF16)
-    split ? go(moe_combine_residual_norm_kernel<DT_BF16, true>)
-          : go(moe_combine_residual_norm_kernel<DT_BF16, false>);
-  else
-    split ? go(moe_combine_residual_norm_kernel<DT_F16, true>)
-          : go(moe_combine_residual_norm_kernel<DT_F16, false>);
+  if (k == 8) {
+    if (dtype == DT_BF16)
+      split ? go(moe_combine_residual_norm_kernel<DT_BF16, true, 8>)
+            : go(moe_combine_residual_norm_kernel<DT_BF16, false, 8>);
+    else
+      split ? go(moe_combine_residual_norm_kernel<DT_F16, true, 8>)
+            : go(moe_combine_residual_norm_kernel<DT_F16, false, 8>);
+  } else if (dtype == DT_BF16) {
+    split ? go(moe_combine_residual_norm_kernel<DT_BF16, true, 0>)
+          : go(moe_combine_residual_norm_kernel<DT_BF16, false, 0>);
+  } else {
+    split ? go(moe_combine_residual_norm_kernel<DT_F16, true, 0>)
+          : go(moe_combine_residual_norm_kernel<DT_F16, false, 0>);
+  }
   return hipGetLastError();
 }
 

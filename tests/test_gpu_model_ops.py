@@ -97,15 +97,17 @@ def test_qk_norm_rope_store(Hq, Hkv, D, dt, wide):
     assert not kp.permute(0, 2, 1, 3)[~written].any()
 
 
-@pytest.mark.parametrize("T,dt", [(32, torch.bfloat16), (300, torch.float16)])
-def test_moe_combine_residual_norm(T, dt):
+@pytest.mark.parametrize("T,dt,k", [(32, torch.bfloat16, 4), (300, torch.float16, 4),
+                                    (32, torch.bfloat16, 8), (64, torch.float16, 8)])
+def test_moe_combine_residual_norm(T, dt, k):
     """nvm_moe_forward_residual_norm: h_out is bit-identical to h + Moe(x)
-    (the combine's arithmetic, then one rounding), x_out the norm of it."""
+    (the combine's arithmetic, then one rounding), x_out the norm of it;
+    top-8 takes the kernel instance with every pair's loads at once."""
     from nano_vllm_metal_amd import Moe, QuantizedWeights, quantize
     from nano_vllm_metal_amd.fused import moe_residual_rms_norm, residual_rms_norm
 
-    H, E, I, k = 512, 16, 128, 4
-    g = torch.Generator(device=DEV).manual_seed(T)
+    H, E, I = 512, 16, 128
+    g = torch.Generator(device=DEV).manual_seed(T + k)
 
     def qw(*shape, std=0.05):
         wq, s, b = quantize((torch.randn(shape, generator=g, device=DEV) * std).to(dt), 64, 4)
