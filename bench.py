@@ -924,7 +924,7 @@ KERNEL_KEYS = (
     ("dispatch_count", r"dispatch_count_kernel"),
     ("dispatch_scatter", r"dispatch_scatter_kernel"),
     ("dispatch", r"dispatch_kernel"),
-    ("combine", r"combine_kernel<1"),
+    ("combine", r"combine_kernel<1|combine_narrow_kernel<1"),
     # attention (the model port)
     ("attn_causal_prefill", r"causal_prefill_kernel<"),
     ("attn_paged_prefill", r"paged_prefill_kernel<"),
