@@ -1244,8 +1244,9 @@ def main():
                    "moe_intermediate": I, "group_size": gs, "bits": 4,
                    "weight_sets": args.layers, "timing": head["timing"]},
         "hbm_gbs": head["hbm_gbs"],
-        # BASELINE.md's GPU timing protocol: the median of >= 100 individually
-        # timed layer calls after 10 warm-ups, weight sets rotated
+        # the published GPU timing protocol of the reference's figures: the
+        # median of >= 100 individually timed layer calls after 10 warm-ups,
+        # weight sets rotated
         "median_protocol": {"layer_us": head["layer_us_median"],
                             "tokens_per_s": head["tokens_per_s_median"],
                             "samples": head["median_samples"],
